@@ -1,0 +1,263 @@
+// Cached decode step: one new query row per (batch, head) slice against
+// `length` cached keys, with the per-key fp32 demand vector advanced in place.
+//
+// Reference behaviour: /root/reference/src/dilution/kernels.py:937-991
+// (_dilution_decode) and :994-1038 (dilution_decode_step).  The reference runs
+// one program per slice; here the keys are split into chunks so the grid fills
+// 256 CUs, in three launches:
+//
+//   dec_stats  (chunks x n): a_j = q.k_j * scale*log2e -> fp32 scratch AFF,
+//                            chunk-local (max, sum 2^(a-max))
+//   dec_apply  (chunks x n): combine the chunk statistics -> lse; for every key
+//                            p = 2^(a-lse), share = p / (committed + p + eps),
+//                            chunk partials sum(share), sum(share * v);
+//                            committed += p stored in place
+//   dec_finish (n):          out = sum(share * v) / (sum(share) + eps) in the
+//                            query dtype
+//
+// HBM bytes per key: K and V rows (2*D*elt) + demand read+write (8) + AFF
+// write+read (8).  Everything is streamed once with 16-byte row loads.
+#include "dil_common.hpp"
+#include "dil_internal.hpp"
+
+namespace dil {
+
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = kDecThreads / 64;
+
+template <int D>
+struct DecLayout {
+  static constexpr int kLanesPerRow = D / 8;          // each lane owns 8 consecutive d
+  static constexpr int kRowsPerWave = 64 / kLanesPerRow;
+  static constexpr int kRowsPerBlock = kRowsPerWave * kDecWaves;
+};
+
+// Sum over the kLanesPerRow lanes that share one cached row.
+template <int LPR>
+__device__ __forceinline__ float row_reduce(float x) {
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecThreads) void dec_stats(
+    const void* __restrict__ q1, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
+    float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
+    int dt, float qscale) {
+  using L = DecLayout<D>;
+  const int64_t slice = blockIdx.y;
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
+  const int64_t j0 = c * chunk;
+  const int64_t j1 = min(j0 + chunk, length);
+
+  float q[8];
+  load8_f32(q1, slice * q_sn + sub * 8, dt, q);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] *= qscale;
+
+  const int64_t kbase = slice * kv_sn + sub * 8;
+  float* arow = aff + slice * length;
+  float m = -INFINITY, s = 0.f;
+  constexpr int U = 4;   // rows in flight per lane
+  for (int64_t jb = j0 + wave * L::kRowsPerWave + rw; jb < j1; jb += (int64_t)U * L::kRowsPerBlock) {
+    float kv[U][8];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
+      ok[u] = j < j1;
+      if (ok[u]) load8_f32(kc, kbase + j * D, dt, kv[u]);
+    }
+    float a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = fmaf(q[e], ok[u] ? kv[u][e] : 0.f, dot);
+      a[u] = row_reduce<L::kLanesPerRow>(dot);
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
+      if (ok[u]) {
+        if (sub == 0) arow[j] = a[u];
+        tmax = fmaxf(tmax, a[u]);
+      }
+    }
+    if (tmax > -INFINITY) {
+      const float mn = fmaxf(m, tmax);
+      float add = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) add += fast_exp2(a[u] - mn);
+      s = s * fast_exp2(m - mn) + add;
+      m = mn;
+    }
+  }
+  // Lanes of one row hold identical (m, s); count each row once.
+  if (sub != 0) { m = -INFINITY; s = 0.f; }
+  const float wm = wave_max(m);
+  float ws = wave_sum(m == -INFINITY ? 0.f : s * fast_exp2(m - wm));
+  __shared__ float sm[kDecWaves], ss[kDecWaves];
+  if (lane == 0) { sm[wave] = wm; ss[wave] = ws; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bm = -INFINITY;
+    for (int w = 0; w < kDecWaves; ++w) bm = fmaxf(bm, sm[w]);
+    float bs = 0.f;
+    for (int w = 0; w < kDecWaves; ++w)
+      if (sm[w] > -INFINITY) bs += ss[w] * fast_exp2(sm[w] - bm);
+    part[slice * nchunk + c] = make_float2(bm, bs);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecThreads) void dec_apply(
+    const void* __restrict__ vc, int64_t kv_sn, float* __restrict__ committed, int64_t c_sn,
+    const float* __restrict__ aff, const float2* __restrict__ part, float* __restrict__ part_out,
+    int64_t length, int64_t chunk, int nchunk, int dt) {
+  using L = DecLayout<D>;
+  const int64_t slice = blockIdx.y;
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
+
+  // Combine the chunk statistics of this slice (every wave redundantly).
+  float m = -INFINITY, s = 0.f;
+  for (int i = lane; i < nchunk; i += 64) {
+    const float2 ps = part[slice * nchunk + i];
+    const float mn = fmaxf(m, ps.x);
+    if (mn > -INFINITY) {
+      s = s * fast_exp2(m - mn) + ps.y * fast_exp2(ps.x - mn);
+      m = mn;
+    }
+  }
+  const float gm = wave_max(m);
+  const float gs = wave_sum(m == -INFINITY ? 0.f : s * fast_exp2(m - gm));
+  const float lse = gm + __log2f(gs);
+
+  const int64_t j0 = c * chunk;
+  const int64_t j1 = min(j0 + chunk, length);
+  const float* arow = aff + slice * length;
+  float* crow = committed + slice * c_sn;
+  const int64_t vbase = slice * kv_sn + sub * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float ssum = 0.f;
+  constexpr int U = 4;
+  for (int64_t jb = j0 + wave * L::kRowsPerWave + rw; jb < j1; jb += (int64_t)U * L::kRowsPerBlock) {
+    float vv[U][8], a[U], cm[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
+      ok[u] = j < j1;
+      if (ok[u]) {
+        load8_f32(vc, vbase + j * D, dt, vv[u]);
+        a[u] = arow[j];
+        cm[u] = crow[j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
+      const float p = fast_exp2(a[u] - lse);
+      const float sh = p * fast_rcp(cm[u] + p + kEps);
+      if (sub == 0) crow[j] = cm[u] + p;
+      ssum += sh;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(sh, vv[u][e], acc[e]);
+    }
+  }
+  // Reduce over lanes holding the same d-slice, then over waves.
+#pragma unroll
+  for (int o = L::kLanesPerRow; o < 64; o <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+    ssum += __shfl_xor(ssum, o, 64);
+  }
+  __shared__ float red[kDecWaves][D + 1];
+  if (rw == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[wave][sub * 8 + e] = acc[e];
+    if (sub == 0) red[wave][D] = ssum;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i <= D; i += kDecThreads) {
+    float t = 0.f;
+    for (int w = 0; w < kDecWaves; ++w) t += red[w][i];
+    part_out[(slice * nchunk + c) * (D + 1) + i] = t;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void dec_finish(const float* __restrict__ part_out, int nchunk,
+                                                 void* __restrict__ out, int64_t o_sn, int dt) {
+  const int64_t slice = blockIdx.x;
+  const float* base = part_out + slice * nchunk * (D + 1);
+  float ssum = 0.f;
+  for (int c = 0; c < nchunk; ++c) ssum += base[c * (D + 1) + D];
+  const float inv = 1.f / (ssum + kEps);
+  for (int d = threadIdx.x; d < D; d += 64) {
+    float t = 0.f;
+    for (int c = 0; c < nchunk; ++c) t += base[c * (D + 1) + d];
+    store_as(out, slice * o_sn + d, dt, t * inv);
+  }
+}
+
+int64_t decode_chunk(int64_t length) {
+  // 1024 keys per workgroup: at B16 H16 and 128K context that is 32768
+  // workgroups; short contexts collapse to a single chunk.
+  (void)length;
+  return 1024;
+}
+
+template <int D>
+int launch_decode(const DecodeArgs& a) {
+  const int64_t chunk = decode_chunk(a.length);
+  const int nchunk = static_cast<int>((a.length + chunk - 1) / chunk);
+  char* ws = static_cast<char*>(a.workspace);
+  float* aff = reinterpret_cast<float*>(ws);
+  size_t off = align_up(sizeof(float) * a.n * a.length);
+  float2* part = reinterpret_cast<float2*>(ws + off);
+  off += align_up(sizeof(float2) * a.n * nchunk);
+  float* part_out = reinterpret_cast<float*>(ws + off);
+  const float qscale = kLog2e / sqrtf(static_cast<float>(D));
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+  dim3 grid(nchunk, static_cast<unsigned>(a.n));
+  dec_stats<D><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length,
+                                             chunk, nchunk, a.dtype, qscale);
+  dec_apply<D><<<grid, kDecThreads, 0, st>>>(a.v_cache, a.kv_sn, a.committed, a.c_sn, aff, part,
+                                             part_out, a.length, chunk, nchunk, a.dtype);
+  dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 64, 0, st>>>(part_out, nchunk, a.out, a.o_sn,
+                                                                  a.dtype);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+
+int64_t decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
+  const int64_t chunk = decode_chunk(length);
+  const int64_t nchunk = (length + chunk - 1) / chunk;
+  return static_cast<int64_t>(align_up(sizeof(float) * n * length) +
+                              align_up(sizeof(float2) * n * nchunk) +
+                              align_up(sizeof(float) * n * nchunk * (head_dim + 1)));
+}
+
+int decode_step(const DecodeArgs& a) {
+  switch (a.head_dim) {
+    case 16: return launch_decode<16>(a);
+    case 32: return launch_decode<32>(a);
+    case 64: return launch_decode<64>(a);
+    case 128: return launch_decode<128>(a);
+    default: return kErrHeadDim;
+  }
+}
+
+}  // namespace dil

@@ -1,0 +1,93 @@
+// Host-side declarations shared by the kernel translation units and the C ABI.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dil {
+
+// Negative status codes (positive values are hipError_t).  Mirrored by
+// dil_status_string() and by the Python layer.
+constexpr int kErrHeadDim = -1;
+constexpr int kErrDtype = -2;
+constexpr int kErrWorkspace = -3;
+constexpr int kErrShape = -4;
+constexpr int kErrPrecision = -5;
+
+inline size_t align_up(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
+
+struct DecodeArgs {
+  const void* q1;        // (n, D) rows, slice stride q_sn elements
+  int64_t q_sn;
+  const void* k_cache;   // (n, cap, D), slice stride kv_sn elements
+  const void* v_cache;
+  int64_t kv_sn;
+  float* committed;      // (n, cap) fp32, slice stride c_sn
+  int64_t c_sn;
+  void* out;             // (n, D) in `dtype`, slice stride o_sn
+  int64_t o_sn;
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t n, length;
+  int head_dim, dtype;
+  void* stream;
+};
+
+int64_t decode_workspace_bytes(int64_t n, int64_t length, int head_dim);
+int decode_step(const DecodeArgs& a);
+
+// Forward over query rows [q0, q0 + C) against keys [0, Tk), Tk = q0 + C.
+// Plain forward: q0 = 0, C = Tk = T.  Chunked prefill: q0 = chunk start.
+struct ForwardArgs {
+  const void* q;         // (n, C, D) rows, slice stride q_sn
+  int64_t q_sn;
+  const void* k;         // (n, >= Tk, D), slice stride kv_sn
+  const void* v;
+  int64_t kv_sn;
+  int64_t n, C, Tk, q0;
+  int head_dim, dtype, lowp;   // lowp: bf16 MFMA operands; else fp32 operands
+  float* out;            // (n, C, D) fp32, slice stride o_sn
+  int64_t o_sn;
+  float* rmax;           // (n, C) fp32 (log2-domain row max of the scaled affinities)
+  float* rden;           // (n, C) fp32 (sum of 2^(a - rmax))
+  float* ssum;           // (n, C) fp32 (row sum of shares)
+  float* carry;          // (n, ceil(C/32), Tk) fp32 demand checkpoints
+  const float* demand_in;  // (n, >= q0) fp32 demand before row q0, or null
+  int64_t din_sn;
+  float* total;          // (n, Tk) fp32 demand after the last row (may alias demand_in)
+  int64_t tot_sn;
+  float* pk;             // (n, C, D) fp32 scale * p @ k, or null
+  void* workspace;
+  int64_t workspace_bytes;
+  void* stream;
+};
+
+int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int lowp,
+                                int want_pk);
+int forward(const ForwardArgs& a);
+
+struct BackwardArgs {
+  const void* q;         // (n, T, D) each, contiguous slices of T*D
+  const void* k;
+  const void* v;
+  const void* dout;      // (n, T, D) in dout_dtype
+  const float* out;      // (n, T, D) fp32 forward output
+  const float* rmax;     // (n, T)
+  const float* rden;
+  const float* ssum;
+  const float* carry;    // (n, ceil(T/32), T)
+  const float* pk;       // (n, T, D)
+  void* dq;              // (n, T, D) each in grad_dtype
+  void* dk;
+  void* dv;
+  int64_t n, T;
+  int head_dim, dtype, dout_dtype, grad_dtype, lowp;
+  void* workspace;
+  int64_t workspace_bytes;
+  void* stream;
+};
+
+int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int lowp);
+int backward(const BackwardArgs& a);
+
+}  // namespace dil

@@ -1,0 +1,193 @@
+// LDS tile staging, operand fragments and in-register column scans shared by
+// the forward and backward kernels (see the layout conventions in
+// dil_common.hpp).
+#pragma once
+
+#include "dil_common.hpp"
+
+namespace dil {
+
+constexpr int kThreads = 256;   // 4 waves
+constexpr int kTileK = 32;      // keys per tile
+constexpr int kTileQ = 32;      // query rows per wave
+
+inline int64_t pad64(int64_t x) { return (x + 63) / 64 * 64; }
+
+// Number of 32-wide accumulator tiles along the head dimension (head_dim 16
+// uses one tile whose columns >= 16 are padding).
+template <int D> constexpr int kDTiles = (D + 31) / 32;
+
+// ---------------------------------------------------------------------------
+// operand preparation
+
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__ src, int64_t src_sn,
+                                                        int dt, int64_t rows, CT* __restrict__ dst,
+                                                        int64_t dst_sn, CT* __restrict__ dst_t,
+                                                        int64_t t_sn, int64_t rows_pad) {
+  __shared__ float tile[64][D + 1];
+  const int64_t slice = blockIdx.y;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+  constexpr int kVecPerRow = D / 8;
+  for (int idx = threadIdx.x; idx < 64 * kVecPerRow; idx += kThreads) {
+    const int r = idx / kVecPerRow, c8 = (idx % kVecPerRow) * 8;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r0 + r < rows) load8_f32(src, slice * src_sn + (r0 + r) * D + c8, dt, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[r][c8 + e] = v[e];
+  }
+  __syncthreads();
+  if (dst != nullptr) {
+    for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
+      const int r = idx / D, c = idx % D;
+      if (r0 + r < rows) dst[slice * dst_sn + (r0 + r) * D + c] = static_cast<CT>(tile[r][c]);
+    }
+  }
+  if (dst_t != nullptr) {
+    for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
+      const int c = idx / 64, r = idx % 64;
+      if (r0 + r < rows_pad) dst_t[slice * t_sn + static_cast<int64_t>(c) * rows_pad + r0 + r] =
+          static_cast<CT>(tile[r][c]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS staging of 32-row tiles
+
+template <typename CT, int D>
+struct Tiles {
+  static constexpr int kRowPad = 16 / sizeof(CT);          // 16 B per row breaks bank aliasing
+  static constexpr int kKStride = D + kRowPad;              // K tile: [32][D + pad]
+  static constexpr int kTStride = kTileK + kRowPad;         // transposed tile: [D][32 + pad]
+  static constexpr int kChunk = 16 / sizeof(CT);            // elements per 16-byte copy
+  static constexpr int kKChunks = kTileK * D / kChunk;      // 16-byte chunks per K tile
+  static constexpr int kTChunks = D * kTileK / kChunk;
+};
+
+template <typename CT> struct Vec16 { typedef floatx4 type; };
+template <> struct Vec16<__bf16> { typedef bf16x8 type; };
+
+// Copy one K tile (rows [key0, key0+32) of a row-major (rows, D) slice) into
+// registers: each thread owns kKChunks / kThreads 16-byte chunks.
+template <typename CT, int D>
+struct KTileLoader {
+  using T = Tiles<CT, D>;
+  using V = typename Vec16<CT>::type;
+  static constexpr int kPer = (T::kKChunks + kThreads - 1) / kThreads;
+  V r[kPer];
+  __device__ void load(const CT* base, int64_t key0, int64_t nkeys) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int idx = threadIdx.x + u * kThreads;
+      const int row = idx / (D / T::kChunk), c = (idx % (D / T::kChunk)) * T::kChunk;
+      r[u] = V{};
+      if (idx < T::kKChunks && key0 + row < nkeys)
+        r[u] = *reinterpret_cast<const V*>(base + (key0 + row) * D + c);
+    }
+  }
+  __device__ void store(CT* lds) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int idx = threadIdx.x + u * kThreads;
+      const int row = idx / (D / T::kChunk), c = (idx % (D / T::kChunk)) * T::kChunk;
+      if (idx < T::kKChunks) *reinterpret_cast<V*>(lds + row * T::kKStride + c) = r[u];
+    }
+  }
+};
+
+// Copy one transposed tile (rows d in [0, D), columns [key0, key0 + 32)) of a
+// (D, rows_pad) slice into registers.
+template <typename CT, int D>
+struct TTileLoader {
+  using T = Tiles<CT, D>;
+  using V = typename Vec16<CT>::type;
+  static constexpr int kPer = (T::kTChunks + kThreads - 1) / kThreads;
+  static constexpr int kPerRow = kTileK / T::kChunk;
+  V r[kPer];
+  __device__ void load(const CT* base, int64_t rows_pad, int64_t key0) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int idx = threadIdx.x + u * kThreads;
+      const int d = idx / kPerRow, c = (idx % kPerRow) * T::kChunk;
+      r[u] = V{};
+      if (idx < T::kTChunks) r[u] = *reinterpret_cast<const V*>(base + d * rows_pad + key0 + c);
+    }
+  }
+  __device__ void store(CT* lds) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int idx = threadIdx.x + u * kThreads;
+      const int d = idx / kPerRow, c = (idx % kPerRow) * T::kChunk;
+      if (idx < T::kTChunks) *reinterpret_cast<V*>(lds + d * T::kTStride + c) = r[u];
+    }
+  }
+};
+
+// Row fragment of a 32-row tile held in LDS ([32][kKStride]); lane reads row `row`.
+template <typename CT, int D>
+__device__ __forceinline__ void lds_row_frag(RowFrag<CT, D>& rf, const CT* lds, int row, int h) {
+  load_row_frag<CT, D>(rf, lds + row * Tiles<CT, D>::kKStride + h * (D / 2));
+}
+
+// Operand fragment over 32 keys from a transposed LDS tile ([D][kTStride]):
+// lane (row r of the D dimension, half h) supplies, for instruction s, the
+// keys that the permuted accumulator layout assigns to k slots of half h:
+// bf16: keys 16 s + 8 h + [0, 8); fp32: key perm_row(s, h).
+template <typename CT, int D>
+__device__ __forceinline__ typename Mma<CT>::frag lds_t_frag(const CT* lds, int r, int h, int s) {
+  if (D < 32 && r >= D) return typename Mma<CT>::frag{};
+  const CT* row = lds + r * Tiles<CT, D>::kTStride;
+  if constexpr (sizeof(CT) == 2) {
+    return *reinterpret_cast<const bf16x8*>(row + 16 * s + 8 * h);
+  } else {
+    return row[perm_row(s, h)];
+  }
+}
+
+// Operand fragment built from 16 accumulator values of one lane (the
+// permuted layout): instruction s takes registers [s*kPerLane, (s+1)*kPerLane).
+template <typename CT>
+__device__ __forceinline__ typename Mma<CT>::frag acc_frag(const float* v, int s) {
+  return Mma<CT>::pack(v + s * Mma<CT>::kPerLane);
+}
+
+// Identity operand that transposes a 32x32 accumulator tile held in the
+// permuted layout: B[k][n] = 1 where k (the logical row of slot t of
+// instruction s in half h) equals n = lane & 31.
+template <typename CT>
+__device__ __forceinline__ typename Mma<CT>::frag ident_frag(int l32, int h, int s) {
+  if constexpr (sizeof(CT) == 2) {
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = (16 * s + 8 * h + t == l32) ? 1.f : 0.f;
+    return Mma<CT>::pack(v);
+  } else {
+    return (perm_row(s, h) == l32) ? 1.f : 0.f;
+  }
+}
+
+// Column scan over the 32 rows of an accumulator tile in the permuted layout
+// (register i of half h = row 16*(i>>3) + 8*h + (i&7)).  On return x[i] holds
+// base + sum of the column's entries at rows <= row(i): the inclusive demand
+// plus `base`.  Also returns the column total (the same in both halves).
+__device__ __forceinline__ float column_scan_inclusive(float (&x)[16], float base, int h) {
+  // inclusive prefix within each run of 8
+#pragma unroll
+  for (int t = 1; t < 8; ++t) x[t] += x[t - 1];
+#pragma unroll
+  for (int t = 9; t < 16; ++t) x[t] += x[t - 1];
+  const float tlo = x[7], thi = x[15];
+  const float plo = partner32(tlo), phi = partner32(thi);
+  // column order: [h0 lo][h1 lo][h0 hi][h1 hi]
+  const float off_lo = h ? plo : 0.f;
+  const float off_hi = h ? (plo + tlo + phi) : (tlo + plo);
+  const float blo = base + off_lo, bhi = base + off_hi;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) x[t] += blo;
+#pragma unroll
+  for (int t = 8; t < 16; ++t) x[t] += bhi;
+  return tlo + thi + plo + phi;
+}
+
+}  // namespace dil

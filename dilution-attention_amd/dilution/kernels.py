@@ -1,0 +1,384 @@
+"""Dilution attention on MI355X (gfx950): reference, training, prefill and decode.
+
+Drop-in for the reference module ``dilution.kernels``
+(/root/reference/src/dilution/kernels.py).  The public functions keep the
+reference signatures; behind them every launch goes to the hand-written HIP
+kernels of ``libdilution_hip.so`` through its C ABI (include/dilution_hip.h).
+There is no Triton and no CPU fallback: when the library cannot be loaded, or
+the tensors are not on the GPU, the entry points raise.
+
+    p         = causal_softmax(q k^T / sqrt(d))   # bids
+    committed = exclusive_cumsum_cols(p)          # taken by earlier queries
+    share     = p / (committed + p + eps)         # bid vs cumulative demand
+    A         = share / rowsum(share);  out = A @ v
+
+Kernel decomposition (csrc/): a row-statistics pass that also writes
+per-32-row-block column sums of p, an fp64 block scan that turns them into
+demand checkpoints, an output pass with the in-tile demand scan on registers,
+the matching backward (a reverse key-parallel walk for dv, dk and the demand
+adjoint, a row-parallel dq pass, and the softmax-Jacobian correction of dk),
+and a split-K decode step.  Tuning arguments of the Triton reference (block
+sizes, warps, stages) are accepted and ignored: tiles are fixed for gfx950.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _hip
+
+HAS_HIP = _hip.available()
+"""True when libdilution_hip.so is built and loadable (the test gate)."""
+
+# The reference switches training above this length to its key-parallel
+# forward (kernels.py:71-76).  Here one decomposition serves every length; the
+# constant is kept so callers that read it keep working.
+KEY_FORWARD_MIN_SEQ = 256
+
+# Rows per demand checkpoint (aux["carry"] granularity, aux["bwd_block_m"]).
+CHECKPOINT_ROWS = 32
+
+_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+_PRECISIONS = {"ieee": 0, "tf32": 1, "bf16": 2}
+_HEAD_DIMS = (16, 32, 64, 128)
+
+
+def dilution_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """The operator written plainly in fp32 torch ops (kernels.py:40-68).
+
+    q/k/v: (B, H, T, D).  Returns (B, H, T, D) fp32.  This is the spec the
+    kernels are held to; it is never used as a kernel fallback.
+    """
+    seq, head_dim = q.shape[-2], q.shape[-1]
+    aff = (q.float() @ k.float().transpose(-2, -1)) / math.sqrt(head_dim)
+    mask = torch.tril(torch.ones(seq, seq, dtype=torch.bool, device=q.device))
+    aff = aff.masked_fill(~mask, torch.finfo(torch.float32).min)
+    p = aff.softmax(dim=-1)
+    committed = p.cumsum(dim=-2) - p
+    share = p / (committed + p + 1e-9)
+    attn = share / (share.sum(dim=-1, keepdim=True) + 1e-9)
+    return attn @ v.float()
+
+
+# ---------------------------------------------------------------------------
+# helpers
+
+
+def _precision_code(dot_precision: str) -> int:
+    """"ieee" / "tf32": fp32 MFMA operands; "bf16": bf16 MFMA operands
+    (kernels.py:318-325).  gfx950 has no tf32 MFMA, so tf32 runs as ieee."""
+    if dot_precision not in _PRECISIONS:
+        raise ValueError("dot_precision must be one of ieee, tf32, bf16")
+    return _PRECISIONS[dot_precision]
+
+
+def _check_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError("dilution HIP kernels need tensors on the GPU (no CPU path)")
+
+
+def _check_head_dim(head_dim: int) -> None:
+    if head_dim & (head_dim - 1):
+        raise ValueError("head_dim must be a power of two")
+    if head_dim not in _HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {_HEAD_DIMS} on the gfx950 kernels")
+
+
+def _common_dtype(*ts: torch.Tensor) -> torch.dtype:
+    dt = ts[0].dtype
+    for t in ts[1:]:
+        dt = torch.promote_types(dt, t.dtype)
+    if dt not in _DTYPES:
+        dt = torch.float32
+    return dt
+
+
+def _rows(x: torch.Tensor, n: int, t: int, d: int, dtype: torch.dtype) -> torch.Tensor:
+    """(n, t, d) contiguous view or copy in `dtype` (kernels.py:362-364)."""
+    return x.reshape(n, t, d).to(dtype).contiguous()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# forward
+
+
+def dilution_attention_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dot_precision: str = "ieee",
+    block_m: int = 64,
+    block_n: int = 64,
+    return_aux: bool = False,
+    num_warps: int = 4,
+    num_stages: int = 2,
+    _save_pk: bool = False,
+    scratch_budget_gib: float = 16.0,
+):
+    """Fused forward; returns fp32 outputs (kernels.py:328-455).
+
+    With return_aux=True also returns the statistics the backward needs and
+    the inclusive column totals of p (the cached-decode demand after this
+    prefix), as the reference's aux dict: ``pk, rmax, rden, carry, ssum,
+    bwd_block_m, block_m, block_n, dot_precision, num_warps,
+    committed_total``.  ``carry`` holds the demand entering every 32-row block
+    (``bwd_block_m`` = 32).  Without return_aux the (batch, head) slices are
+    processed in groups sized so the (rows, T/32, T) fp32 checkpoint scratch
+    stays under scratch_budget_gib; slices are independent, so results are
+    identical.
+    """
+    prec = _precision_code(dot_precision)
+    lib = _hip.lib()
+    _check_device(q, k, v)
+    batch, heads, seq, head_dim = q.shape
+    _check_head_dim(head_dim)
+    n = batch * heads
+    dt = _common_dtype(q, k, v)
+    qf, kf, vf = (_rows(x, n, seq, head_dim, dt) for x in (q, k, v))
+    dev = q.device
+    nb = (seq + CHECKPOINT_ROWS - 1) // CHECKPOINT_ROWS
+    f32 = dict(device=dev, dtype=torch.float32)
+    out = torch.empty(n, seq, head_dim, **f32)
+    rmax = torch.empty(n, seq, **f32)
+    rden = torch.empty(n, seq, **f32)
+    ssum = torch.empty(n, seq, **f32)
+    total = torch.empty(n, seq, **f32)
+    pk = torch.empty(n, seq, head_dim, **f32) if _save_pk else None
+
+    rows = n
+    if not return_aux:
+        per_row = nb * seq * 4
+        rows = max(1, min(n, int(scratch_budget_gib * 2**30) // max(per_row, 1)))
+    carry = torch.empty(rows, nb, seq, **f32)
+    ws_bytes = lib.dil_forward_workspace_bytes(rows, seq, head_dim, _DTYPES[dt], prec, int(_save_pk))
+    ws = _workspace(ws_bytes, dev)
+    for a in range(0, n, rows):
+        b = min(a + rows, n)
+        status = lib.dil_forward(
+            qf[a:b].data_ptr(), kf[a:b].data_ptr(), vf[a:b].data_ptr(), b - a, seq, head_dim,
+            _DTYPES[dt], prec, out[a:b].data_ptr(), rmax[a:b].data_ptr(), rden[a:b].data_ptr(),
+            ssum[a:b].data_ptr(), carry.data_ptr(), total[a:b].data_ptr(),
+            None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+        _hip.check(status, "dil_forward")
+
+    result = out.reshape(batch, heads, seq, head_dim)
+    if return_aux:
+        aux = dict(pk=pk, rmax=rmax, rden=rden, carry=carry, ssum=ssum, bwd_block_m=CHECKPOINT_ROWS,
+                   block_m=block_m, block_n=block_n, dot_precision=dot_precision,
+                   num_warps=num_warps, committed_total=total.reshape(batch, heads, seq))
+        return result, aux
+    return result
+
+
+# ---------------------------------------------------------------------------
+# training (autograd)
+
+
+class _DilutionAttentionFn(torch.autograd.Function):
+    """Forward + backward on the HIP kernels (kernels.py:829-903).
+
+    Same 12 positional arguments as the reference; the tuning arguments are
+    accepted and ignored.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, dot_precision, block_m, block_n,
+                num_warps, bwd_num_warps, bwd_num_stages, b3_block_n, b3_num_warps, b4_num_warps):
+        out, aux = dilution_attention_forward(
+            q, k, v, dot_precision=dot_precision, block_m=block_m, block_n=block_n,
+            return_aux=True, num_warps=num_warps, _save_pk=any(ctx.needs_input_grad[:3]),
+        )
+        ctx.save_for_backward(q, k, v, out, aux["rmax"], aux["rden"], aux["carry"], aux["ssum"],
+                              aux["pk"])
+        ctx.dot_precision = dot_precision
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, rmax, rden, carry, ssum, pk = ctx.saved_tensors
+        lib = _hip.lib()
+        batch, heads, seq, head_dim = q.shape
+        n = batch * heads
+        prec = _precision_code(ctx.dot_precision)
+        dt = _common_dtype(q, k, v)
+        qf, kf, vf = (_rows(x, n, seq, head_dim, dt) for x in (q, k, v))
+        ddt = dout.dtype if dout.dtype in _DTYPES else torch.float32
+        dof = _rows(dout, n, seq, head_dim, ddt)
+        of = out.reshape(n, seq, head_dim)
+        dev = q.device
+        grads = []
+        gdt = dt
+        dq = torch.empty(n, seq, head_dim, device=dev, dtype=gdt)
+        dk = torch.empty_like(dq)
+        dv = torch.empty_like(dq)
+        ws = _workspace(lib.dil_backward_workspace_bytes(n, seq, head_dim, _DTYPES[dt], prec), dev)
+        status = lib.dil_backward(
+            qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), dof.data_ptr(), of.data_ptr(),
+            rmax.data_ptr(), rden.data_ptr(), ssum.data_ptr(), carry.data_ptr(), pk.data_ptr(),
+            n, seq, head_dim, _DTYPES[dt], _DTYPES[ddt], _DTYPES[gdt], prec,
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+        _hip.check(status, "dil_backward")
+        shape4 = (batch, heads, seq, head_dim)
+        for g, ref in zip((dq, dk, dv), (q, k, v)):
+            grads.append(g.reshape(shape4).to(ref.dtype))
+        return (*grads, None, None, None, None, None, None, None, None, None)
+
+
+def dilution_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dot_precision: str = "bf16",
+    block_m: int = 64,
+    block_n: int = 64,
+    num_warps: int = 4,
+    bwd_num_warps: int = 4,
+    bwd_num_stages: int = 1,
+    b3_block_n: int | None = None,
+    b3_num_warps: int | None = None,
+    b4_num_warps: int | None = 4,
+) -> torch.Tensor:
+    """Differentiable fused dilution attention (kernels.py:906-930).
+
+    dot_precision "bf16" (default) uses bf16 MFMA operands for the score and
+    value products with fp32 accumulation and fp32 demand/share math;
+    "tf32"/"ieee" keep fp32 operands.
+    """
+    return _DilutionAttentionFn.apply(
+        q, k, v, dot_precision, block_m, block_n,
+        num_warps, bwd_num_warps, bwd_num_stages, b3_block_n, b3_num_warps, b4_num_warps,
+    )
+
+
+# ---------------------------------------------------------------------------
+# chunked prefill (no reference counterpart; reference prefills in one call)
+
+
+def dilution_prefill_chunk(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    committed: torch.Tensor,
+    start: int,
+    dot_precision: str = "bf16",
+    return_aux: bool = False,
+):
+    """Rows [start, start + C) of the operator over the cached keys
+    [0, start + C), carrying the fp32 demand vector across chunks.
+
+    q: (B, H, C, D).  k_cache / v_cache: contiguous (B, H, capacity, D) with
+    rows [0, start + C) written.  committed: contiguous (B, H, capacity) fp32
+    holding the column totals of p over rows < start, zero on
+    [start, start + C); advanced in place to the totals over rows < start + C
+    (entries beyond start + C are not touched).  Returns the chunk's outputs
+    (B, H, C, D) fp32, and with return_aux the chunk's rmax/rden/ssum/carry.
+    Chaining chunks reproduces ``dilution_attention_forward`` row for row and
+    its ``aux["committed_total"]``.
+    """
+    prec = _precision_code(dot_precision)
+    lib = _hip.lib()
+    _check_device(q, k_cache, v_cache, committed)
+    batch, heads, chunk, head_dim = q.shape
+    _check_head_dim(head_dim)
+    capacity = k_cache.shape[2]
+    if start < 0 or start + chunk > capacity:
+        raise ValueError(f"rows [{start}, {start + chunk}) outside cache capacity {capacity}")
+    if committed.dtype != torch.float32:
+        raise ValueError("committed must be float32")
+    n = batch * heads
+    dt = k_cache.dtype if k_cache.dtype in _DTYPES else torch.float32
+    if v_cache.dtype != dt or k_cache.dtype != dt:
+        raise ValueError("k_cache and v_cache must share a float dtype")
+    kf = k_cache.view(n, capacity, head_dim)
+    vf = v_cache.view(n, capacity, head_dim)
+    cf = committed.view(n, capacity)
+    qf = _rows(q, n, chunk, head_dim, dt)
+    dev = q.device
+    nb = (chunk + CHECKPOINT_ROWS - 1) // CHECKPOINT_ROWS
+    f32 = dict(device=dev, dtype=torch.float32)
+    out = torch.empty(n, chunk, head_dim, **f32)
+    rmax = torch.empty(n, chunk, **f32)
+    rden = torch.empty(n, chunk, **f32)
+    ssum = torch.empty(n, chunk, **f32)
+    carry = torch.empty(n, nb, start + chunk, **f32)
+    ws = _workspace(lib.dil_prefill_workspace_bytes(n, chunk, start, head_dim, _DTYPES[dt], prec), dev)
+    status = lib.dil_prefill_chunk(
+        qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), n, chunk, start, capacity, head_dim,
+        _DTYPES[dt], prec, cf.data_ptr(), out.data_ptr(), rmax.data_ptr(), rden.data_ptr(),
+        ssum.data_ptr(), carry.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+    _hip.check(status, "dil_prefill_chunk")
+    result = out.reshape(batch, heads, chunk, head_dim)
+    if return_aux:
+        return result, dict(rmax=rmax, rden=rden, ssum=ssum, carry=carry,
+                            bwd_block_m=CHECKPOINT_ROWS, dot_precision=dot_precision)
+    return result
+
+
+# ---------------------------------------------------------------------------
+# cached decode
+
+
+def dilution_decode_step(
+    q1: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    committed: torch.Tensor,
+    length: int,
+    block_n: int = 512,
+    num_warps: int = 8,
+) -> torch.Tensor:
+    """Fused decode step; returns the new row's output (B, H, 1, D) in q1.dtype
+    (kernels.py:994-1038).
+
+    q1: (B, H, 1, D).  k_cache / v_cache: contiguous (B, H, capacity, D)
+    buffers whose first `length` positions are valid, the new token already
+    written at position length-1.  committed: contiguous (B, H, capacity) fp32
+    accumulator (column totals of p over all previous rows; position length-1
+    must be zero).  It is advanced in place to include this row; positions
+    >= length are never touched.
+    """
+    lib = _hip.lib()
+    batch, heads, one, head_dim = q1.shape
+    if one != 1:
+        raise ValueError("decode step takes exactly one query row per (batch, head)")
+    if head_dim & (head_dim - 1):
+        raise ValueError("head_dim must be a power of two")
+    capacity = k_cache.shape[2]
+    if not 1 <= length <= capacity:
+        raise ValueError(f"length {length} outside cache capacity {capacity}")
+    _check_head_dim(head_dim)
+    _check_device(q1, k_cache, v_cache, committed)
+    if committed.dtype != torch.float32:
+        raise ValueError("committed must be float32")
+    n = batch * heads
+    dt = k_cache.dtype if k_cache.dtype in _DTYPES else torch.float32
+    if v_cache.dtype != dt or k_cache.dtype != dt:
+        raise ValueError("k_cache and v_cache must share a float dtype")
+    kf = k_cache.view(n, capacity, head_dim)
+    vf = v_cache.view(n, capacity, head_dim)
+    cf = committed.view(n, capacity)
+    qf = q1.reshape(n, head_dim).to(dt).contiguous()
+    out = torch.empty(n, head_dim, device=q1.device, dtype=dt)
+    ws = _workspace(lib.dil_decode_workspace_bytes(n, length, head_dim), q1.device)
+    status = lib.dil_decode_step(qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), cf.data_ptr(),
+                                 out.data_ptr(), n, capacity, length, head_dim, _DTYPES[dt],
+                                 ws.data_ptr(), ws.numel(), _stream())
+    _hip.check(status, "dil_decode_step")
+    if out.dtype != q1.dtype:
+        out = out.to(q1.dtype)
+    return out.view(batch, heads, 1, head_dim)

@@ -1,0 +1,130 @@
+/*
+ * C ABI of the MI355X (gfx950) dilution-attention library, libdilution_hip.so.
+ *
+ * The reference (Royer-Research-Labs/Dilution-Attention) has no native code:
+ * its hot path is Triton kernels launched from Python.  Each entry point below
+ * replaces one reference host routine and the kernel launches it makes; the
+ * Python module dilution/kernels.py binds them with ctypes and keeps the
+ * reference's Python signatures.
+ *
+ * Conventions
+ *   - All tensor arguments are device pointers.  Slices are the flattened
+ *     (batch * heads) dimension n; rows within a slice are contiguous with
+ *     head_dim elements each.
+ *   - dtype:     0 = float32, 1 = bfloat16, 2 = float16 (storage type of
+ *                q / k / v / dout / outputs where stated).
+ *   - precision: 0 = "ieee", 1 = "tf32" (both fp32 MFMA operands on gfx950,
+ *                which has no tf32 MFMA), 2 = "bf16" (bf16 MFMA operands).
+ *                fp32 accumulation and fp32 demand/share math in every mode.
+ *   - head_dim in {16, 32, 64, 128}.
+ *   - Every launch is asynchronous on `stream` (a hipStream_t); no entry point
+ *     synchronises, allocates device memory or keeps state between calls.
+ *     Scratch memory is caller-provided (`workspace`, at least the size the
+ *     matching *_workspace_bytes query returns, 256-byte aligned).
+ *   - Return value: 0 on success, a positive hipError_t from the launch, or a
+ *     negative argument error (see dil_status_string).
+ */
+#ifndef DILUTION_HIP_H
+#define DILUTION_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Version of this ABI (bumped on any signature change). */
+int dil_abi_version(void);
+
+/* Human-readable text for a status code returned by the entry points. */
+const char* dil_status_string(int status);
+
+/*
+ * Forward over a whole sequence, with everything the backward needs.
+ * Replaces dilution_attention_forward (src/dilution/kernels.py:328-455) and
+ * the launches it makes (_dilution_k1 :137-198, _dilution_scan :251-264,
+ * _dilution_k2 :267-315).
+ *
+ * q, k, v:   (n, seq, head_dim) in `dtype`.
+ * out:       (n, seq, head_dim) float32.
+ * rmax/rden: (n, seq) float32 row statistics: p_ij = 2^(a_ij - rmax_i) / rden_i
+ *            with a_ij = log2(e) * q_i.k_j / sqrt(head_dim).
+ * ssum:      (n, seq) float32 row sums of the shares.
+ * carry:     (n, ceil(seq/32), seq) float32; carry[:, b, j] = sum of p_ij over
+ *            rows i < 32*b (the demand checkpoint at every 32-row block).
+ * committed_total: (n, seq) float32 column totals of p (the decode demand).
+ * pk:        (n, seq, head_dim) float32 (p @ k)/sqrt(head_dim), or NULL.
+ */
+int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
+                                    int precision, int want_pk);
+int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
+                int head_dim, int dtype, int precision, float* out, float* rmax, float* rden,
+                float* ssum, float* carry, float* committed_total, float* pk, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/*
+ * Chunked prefill: rows [start, start + chunk) of the operator against the
+ * cached keys [0, start + chunk), carrying the demand vector across chunks.
+ * No reference counterpart: the reference prefills the whole prompt at once
+ * (src/dilution/model.py:198-229, kernels.py:328-455 with return_aux=True);
+ * this entry point is the same forward with an incoming demand.
+ *
+ * q_chunk:   (n, chunk, head_dim) in `dtype`.
+ * k_cache, v_cache: (n, capacity, head_dim) in `dtype`, rows [0, start+chunk)
+ *            valid.
+ * committed: (n, capacity) float32.  On entry [0, start) holds the demand of
+ *            rows < start and [start, start+chunk) is zero; on return
+ *            [0, start+chunk) holds the demand of rows < start+chunk.  Entries
+ *            at and beyond start+chunk are not touched.
+ * out:       (n, chunk, head_dim) float32.
+ * rmax, rden, ssum: (n, chunk) float32; carry: (n, ceil(chunk/32), start+chunk).
+ */
+int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
+                                    int dtype, int precision);
+int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_cache, int64_t n,
+                      int64_t chunk, int64_t start, int64_t capacity, int head_dim, int dtype,
+                      int precision, float* committed, float* out, float* rmax, float* rden,
+                      float* ssum, float* carry, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/*
+ * Backward.  Replaces _DilutionAttentionFn.backward
+ * (src/dilution/kernels.py:851-903) and its launches (_dilution_ba :678-775,
+ * _dilution_bc :778-809, _dilution_dq_epilogue :815-826, and the torch dbar
+ * glue at :866).
+ *
+ * q, k, v:   (n, seq, head_dim) in `dtype` (the forward inputs).
+ * dout:      (n, seq, head_dim) in `dout_dtype`.
+ * out, rmax, rden, ssum, carry, pk: the forward's outputs (pk required).
+ * dq, dk, dv: (n, seq, head_dim) in `grad_dtype`.
+ */
+int64_t dil_backward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
+                                     int precision);
+int dil_backward(const void* q, const void* k, const void* v, const void* dout,
+                 const float* out, const float* rmax, const float* rden, const float* ssum,
+                 const float* carry, const float* pk, int64_t n, int64_t seq, int head_dim,
+                 int dtype, int dout_dtype, int grad_dtype, int precision, void* dq, void* dk,
+                 void* dv, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Cached decode step.  Replaces dilution_decode_step
+ * (src/dilution/kernels.py:994-1038) and _dilution_decode (:937-991).
+ *
+ * q1:        (n, head_dim) in `dtype` (the new row).
+ * k_cache, v_cache: (n, capacity, head_dim) in `dtype`; rows [0, length) valid,
+ *            the new token written at length-1.
+ * committed: (n, capacity) float32 column totals of p over earlier rows, with
+ *            committed[:, length-1] == 0.  Advanced in place over [0, length)
+ *            to include this row; [length, capacity) is never touched.
+ * out:       (n, head_dim) in `dtype`.
+ */
+int64_t dil_decode_workspace_bytes(int64_t n, int64_t length, int head_dim);
+int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, float* committed,
+                    void* out, int64_t n, int64_t capacity, int64_t length, int head_dim,
+                    int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DILUTION_HIP_H */

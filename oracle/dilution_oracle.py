@@ -1,0 +1,319 @@
+"""CPU oracle for the dilution-attention hot path.  TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker (or, for the CPU
+baseline, as the thing timed on host cores).  The product path
+(``dilution.kernels``) never imports it and has no CPU fallback.
+
+Every function restates the reference operator from its published source, in
+code written for this repository:
+
+  reference operator            /root/reference/src/dilution/kernels.py:40-68
+  operator definition           /root/reference/docs/operator.md:1-23
+  row statistics (K1 sweep 1)   /root/reference/src/dilution/kernels.py:159-182
+  saved query correction pk     /root/reference/src/dilution/kernels.py:166-182
+  carry checkpoints / totals    /root/reference/tests/test_kernels.py:130-149
+  cached decode step            /root/reference/src/dilution/kernels.py:937-991,
+                                /root/reference/src/dilution/model.py:231-257
+  prefill demand hand-off       /root/reference/src/dilution/model.py:198-229
+  backward decomposition        /root/reference/docs/kernels.md:62-84,
+                                /root/reference/src/dilution/kernels.py:678-775
+
+Pinning (each function is checked by something other than a retyping of its
+own formula; see tests/test_oracle.py):
+
+  attention_fp32          fp64 brute-force loops (attention_loops_f64), the
+                          q = 0 harmonic-number closed form, T = 1, causality,
+                          shift invariance, and planted-mistake variants that
+                          must fail those checks.
+  attention_loops_f64     the harmonic closed form (independent of softmax
+                          and cumsum code) and agreement with attention_fp32.
+  row_stats / bids        torch.softmax (a library routine) at fp64.
+  demand_totals, carry    harmonic closed form H_T - H_j; fp64 loop sums.
+  grads_autograd          torch.autograd.gradcheck (finite differences, fp64).
+  grads_closed_form_f64   autograd through attention_fp32 at fp64.
+  decode_step             the full-sequence rows of attention_loops_f64, token
+                          after token, and the demand == column sums.
+  prefill_chunk           the full-sequence rows and demand == column sums.
+  pk                      (p @ k) / sqrt(d) via fp64 matmul of torch.softmax.
+
+No function here is "parity unpinned".
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+EPS = 1e-9          # kernels.py:66-67 (share denominator and row normalise)
+LOG2E = 1.4426950408889634
+
+
+# ---------------------------------------------------------------------------
+# forward
+
+
+def attention_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """fp32 restatement of dilution_attention_reference (kernels.py:40-68).
+
+    q, k, v: (B, H, T, D) of any float dtype; math in fp32; returns fp32.
+    """
+    t, d = q.shape[-2], q.shape[-1]
+    s = torch.matmul(q.float(), k.float().transpose(-2, -1)) / math.sqrt(d)
+    causal = torch.ones(t, t, dtype=torch.bool, device=q.device).tril()
+    s = s.masked_fill(~causal, torch.finfo(torch.float32).min)
+    p = torch.softmax(s, dim=-1)
+    demand_before = torch.cumsum(p, dim=-2) - p          # exclusive column sums
+    share = p / (demand_before + p + EPS)
+    a = share / (share.sum(dim=-1, keepdim=True) + EPS)
+    return torch.matmul(a, v.float())
+
+
+def attention_f64(q, k, v) -> torch.Tensor:
+    """The same formula evaluated in float64 (used where fp32 rounding of the
+    oracle itself would dominate a tolerance)."""
+    t, d = q.shape[-2], q.shape[-1]
+    q, k, v = (torch.as_tensor(x).double() for x in (q, k, v))
+    s = torch.matmul(q, k.transpose(-2, -1)) / math.sqrt(d)
+    causal = torch.ones(t, t, dtype=torch.bool).tril()
+    s = s.masked_fill(~causal, -math.inf)
+    p = torch.softmax(s, dim=-1)
+    demand_before = torch.cumsum(p, dim=-2) - p
+    share = p / (demand_before + p + EPS)
+    a = share / (share.sum(dim=-1, keepdim=True) + EPS)
+    return torch.matmul(a, v)
+
+
+def attention_loops_f64(q, k, v) -> np.ndarray:
+    """Brute-force float64 loops over (row, key): no softmax, cumsum or matmul
+    library call.  For tiny T only (O(B H T^2 D) Python-level work is kept
+    vectorised over B, H and D only)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    b, h, t, d = q.shape
+    out = np.zeros((b, h, t, d))
+    demand = np.zeros((b, h, t))           # running column totals, row by row
+    for i in range(t):
+        aff = np.stack([(q[:, :, i, :] * k[:, :, j, :]).sum(-1) for j in range(i + 1)], -1)
+        aff = aff / math.sqrt(d)
+        m = aff.max(-1, keepdims=True)
+        e = np.exp(aff - m)
+        p = e / e.sum(-1, keepdims=True)   # (b, h, i+1)
+        share = np.empty_like(p)
+        for j in range(i + 1):
+            share[..., j] = p[..., j] / (demand[..., j] + p[..., j] + EPS)
+        total = share.sum(-1, keepdims=True) + EPS
+        for j in range(i + 1):
+            out[:, :, i, :] += (share[..., j] / total[..., 0])[..., None] * v[:, :, j, :]
+        demand[..., : i + 1] += p
+    return out
+
+
+def harmonic_closed_form(t: int, v) -> tuple[np.ndarray, np.ndarray]:
+    """q = 0: every affinity is 0, so p_ij = 1/(i+1) for j <= i.
+
+    Exclusive demand is H_i - H_j (H_m = sum_{s=1..m} 1/s), the share is
+    (1/(i+1)) / (H_{i+1} - H_j + eps) and the decode totals are H_T - H_j.
+    Returns (out (.., T, D) for the given v, totals (T,)).  Pure closed form:
+    no softmax, no cumsum.
+    """
+    v = np.asarray(v, dtype=np.float64)
+    harm = np.concatenate([[0.0], np.cumsum(1.0 / np.arange(1, t + 1, dtype=np.float64))])
+    i = np.arange(t)[:, None]
+    j = np.arange(t)[None, :]
+    share = np.where(j <= i, (1.0 / (i + 1)) / (harm[i + 1] - harm[j] + EPS), 0.0)
+    a = share / (share.sum(-1, keepdims=True) + EPS)
+    out = np.matmul(a, v)
+    totals = harm[t] - harm[np.arange(t)]
+    return out, totals
+
+
+# ---------------------------------------------------------------------------
+# statistics the kernels expose through aux
+
+
+def bids(q, k, dtype=torch.float64) -> torch.Tensor:
+    """Causal softmax bids p (B, H, T, T) (kernels.py:59-64)."""
+    t, d = q.shape[-2], q.shape[-1]
+    q = torch.as_tensor(q).to(dtype)
+    k = torch.as_tensor(k).to(dtype)
+    s = torch.matmul(q, k.transpose(-2, -1)) / math.sqrt(d)
+    causal = torch.ones(t, t, dtype=torch.bool).tril()
+    return torch.softmax(s.masked_fill(~causal, -math.inf), dim=-1)
+
+
+def row_stats(q, k) -> tuple[torch.Tensor, torch.Tensor]:
+    """(rmax, rden) as K1 defines them (kernels.py:159-182): rmax is the row
+    max of the scaled affinities in the log2 domain and rden = sum 2^(a - rmax),
+    so that p = 2^(a - rmax) / rden."""
+    t, d = q.shape[-2], q.shape[-1]
+    q = torch.as_tensor(q).double()
+    k = torch.as_tensor(k).double()
+    a = torch.matmul(q, k.transpose(-2, -1)) * (LOG2E / math.sqrt(d))
+    causal = torch.ones(t, t, dtype=torch.bool).tril()
+    a = a.masked_fill(~causal, -math.inf)
+    rmax = a.max(-1).values
+    rden = torch.exp2(a - rmax[..., None]).sum(-1)
+    return rmax, rden
+
+
+def demand_totals(q, k) -> torch.Tensor:
+    """Inclusive column totals of p over all rows: aux["committed_total"],
+    the decode accumulator after a prefix (kernels.py:451-453, 264)."""
+    return bids(q, k).sum(-2)
+
+
+def carry_checkpoints(q, k, block: int) -> torch.Tensor:
+    """carry[:, :, rb, j] = sum_{i < rb*block} p_ij (test_kernels.py:143-149);
+    keys j >= rb*block are exactly zero by causality."""
+    p = bids(q, k)
+    t = p.shape[-1]
+    nb = (t + block - 1) // block
+    incl = torch.cumsum(p, dim=-2)
+    out = torch.zeros(*p.shape[:-2], nb, t, dtype=p.dtype)
+    for rb in range(1, nb):
+        out[..., rb, :] = incl[..., rb * block - 1, :]
+    return out
+
+
+def pk(q, k) -> torch.Tensor:
+    """Saved query-side Jacobian correction (p @ k) / sqrt(d)
+    (kernels.py:166-182; test_kernels.py:46-59)."""
+    d = q.shape[-1]
+    return torch.matmul(bids(q, k), torch.as_tensor(k).double()) / math.sqrt(d)
+
+
+# ---------------------------------------------------------------------------
+# prefill and decode
+
+
+def prefill_chunk(q_chunk, k_all, v_all, demand_in, start: int):
+    """Rows [start, start+C) of the operator given the keys [0, start+C) and
+    the incoming demand D_j = sum_{i<start} p_ij (zero for j >= start).
+
+    Returns (out (.., C, D) float64, demand_out (.., start+C) float64) where
+    demand_out_j = D_j + sum_{start <= i < start+C} p_ij.  Follows the eager
+    prefill (model.py:209-222) generalised to a carried-in demand.
+    """
+    qc = torch.as_tensor(q_chunk).double()
+    ka = torch.as_tensor(k_all).double()
+    va = torch.as_tensor(v_all).double()
+    c, d = qc.shape[-2], qc.shape[-1]
+    tk = start + c
+    ka, va = ka[..., :tk, :], va[..., :tk, :]
+    s = torch.matmul(qc, ka.transpose(-2, -1)) / math.sqrt(d)
+    rows = torch.arange(start, start + c)[:, None]
+    keys = torch.arange(tk)[None, :]
+    s = s.masked_fill(keys > rows, -math.inf)
+    p = torch.softmax(s, dim=-1)
+    dem = torch.as_tensor(demand_in).double()[..., :tk].clone()
+    before = dem[..., None, :] + torch.cumsum(p, dim=-2) - p
+    share = p / (before + p + EPS)
+    a = share / (share.sum(-1, keepdim=True) + EPS)
+    return torch.matmul(a, va), dem + p.sum(-2)
+
+
+def decode_step(q1, k_cache, v_cache, committed, length: int):
+    """One cached decode row (kernels.py:937-991; eager twin model.py:242-257).
+
+    q1: (B, H, 1, D); caches (B, H, cap, D); committed (B, H, cap) holding the
+    column totals of p over earlier rows, with committed[..., length-1] == 0.
+    Returns (out (B, H, 1, D) float64, committed_new float64 with the first
+    `length` entries advanced by p and the rest unchanged).
+    """
+    q = torch.as_tensor(q1).double()
+    k = torch.as_tensor(k_cache).double()[..., :length, :]
+    v = torch.as_tensor(v_cache).double()[..., :length, :]
+    com = torch.as_tensor(committed).double().clone()
+    d = q.shape[-1]
+    a = torch.matmul(q, k.transpose(-2, -1))[..., 0, :] / math.sqrt(d)
+    p = torch.softmax(a, dim=-1)
+    c = com[..., :length]
+    share = p / (c + p + EPS)
+    a_row = share / (share.sum(-1, keepdim=True) + EPS)
+    out = torch.matmul(a_row[..., None, :], v)
+    com[..., :length] = c + p
+    return out, com
+
+
+# ---------------------------------------------------------------------------
+# backward
+
+
+def grads_autograd(q, k, v, dout, dtype=torch.float64):
+    """(dq, dk, dv) by autograd through the reference formula."""
+    fn = attention_f64 if dtype == torch.float64 else attention_fp32
+    xs = [torch.as_tensor(x).to(dtype).detach().clone().requires_grad_(True) for x in (q, k, v)]
+    out = fn(*xs)
+    out.backward(torch.as_tensor(dout).to(out.dtype))
+    return tuple(x.grad for x in xs)
+
+
+def grads_closed_form_f64(q, k, v, dout):
+    """Backward by the published decomposition (docs/kernels.md:62-84,
+    kernels.py:685-698), in float64 numpy.
+
+        ds_ij   = (dO_i . v_j - dO_i . o_i) / (S_i + eps)
+        inv_ij  = 1 / (c_ij + p_ij + eps)
+        dp_ij   = ds_ij (c_ij + eps) inv_ij^2 - sum_{i' > i} ds_i'j p_i'j inv_i'j^2
+        ghat_i  = sum_j p_ij dp_ij
+        da_ij   = p_ij (dp_ij - ghat_i)
+        dq = s da K,  dk = s da^T Q,  dv = A^T dO        (s = 1/sqrt(d))
+
+    Also returns the intermediates (dict) so kernel-internal buffers (ghat,
+    suffix checkpoints, dbar) can be checked.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    do = np.asarray(dout, dtype=np.float64)
+    t, d = q.shape[-2], q.shape[-1]
+    sc = 1.0 / math.sqrt(d)
+    causal = np.tril(np.ones((t, t), dtype=bool))
+    a = np.matmul(q, np.swapaxes(k, -1, -2)) * sc
+    a = np.where(causal, a, -np.inf)
+    a = a - a.max(-1, keepdims=True)
+    e = np.exp(a)
+    p = e / e.sum(-1, keepdims=True)
+    c = np.cumsum(p, axis=-2) - p
+    inv = np.where(causal, 1.0 / (c + p + EPS), 0.0)
+    share = p * inv
+    ssum = share.sum(-1, keepdims=True)
+    attn = share / (ssum + EPS)
+    o = np.matmul(attn, v)
+    dbar = (do * o).sum(-1, keepdims=True)
+    ds = np.where(causal, (np.matmul(do, np.swapaxes(v, -1, -2)) - dbar) / (ssum + EPS), 0.0)
+    dk_share = -ds * p * inv * inv
+    # suffix_ij = sum over later rows i' > i of dk_share_i'j
+    rev = np.flip(np.cumsum(np.flip(dk_share, -2), axis=-2), -2)
+    suffix = rev - dk_share
+    dp = np.where(causal, ds * (c + EPS) * inv * inv + suffix, 0.0)
+    ghat = (p * dp).sum(-1, keepdims=True)
+    da = p * (dp - ghat)
+    dq = np.matmul(da, k) * sc
+    dk = np.matmul(np.swapaxes(da, -1, -2), q) * sc
+    dv = np.matmul(np.swapaxes(attn, -1, -2), do)
+    inter = dict(p=p, committed=c, ssum=ssum[..., 0], dbar=dbar[..., 0], ghat=ghat[..., 0],
+                 suffix=suffix, out=o)
+    return (dq, dk, dv), inter
+
+
+# ---------------------------------------------------------------------------
+# deterministic synthetic inputs (CPU RNG)
+
+
+def make_inputs(shape, seed: int, qk_scale: float = 1.0, with_dout: bool = False,
+                dtype=torch.float32):
+    """q, k ~ qk_scale * N(0,1), v ~ N(0,1) (and dO ~ N(0,1)) from a CPU
+    generator, cast to `dtype`."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(*shape, generator=g) * qk_scale
+    k = torch.randn(*shape, generator=g) * qk_scale
+    v = torch.randn(*shape, generator=g)
+    out = [q.to(dtype), k.to(dtype), v.to(dtype)]
+    if with_dout:
+        out.append(torch.randn(*shape, generator=g).to(dtype))
+    return tuple(out)

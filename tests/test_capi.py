@@ -1,0 +1,83 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol that
+include/dilution_hip.h declares, and its host-side argument checks and size
+queries behave (no device call is made)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dilution_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dil_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from dilution import _hip
+
+    return _hip.lib()
+
+
+def test_header_declares_entry_points():
+    syms = _declared_symbols()
+    for name in ("dil_forward", "dil_backward", "dil_decode_step", "dil_prefill_chunk"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from dilution import _hip
+
+    raw = ctypes.CDLL(_hip.LIB_PATH)
+    for name in _declared_symbols():
+        assert hasattr(raw, name), name
+    assert set(_declared_symbols()) == set(_hip.SIGNATURES)
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.dil_abi_version() == 1
+    assert lib.dil_status_string(0) == b"success"
+    for code in (-1, -2, -3, -4, -5):
+        assert lib.dil_status_string(code) != b"unknown status"
+
+
+def test_workspace_queries(lib):
+    assert lib.dil_decode_workspace_bytes(256, 131072, 64) >= 256 * 131072 * 4
+    small = lib.dil_forward_workspace_bytes(4, 512, 64, 1, 2, 0)
+    assert small > 0
+    # fp32 inputs with bf16 operands need converted copies
+    assert lib.dil_forward_workspace_bytes(4, 512, 64, 0, 2, 0) > small
+    assert lib.dil_forward_workspace_bytes(4, 512, 64, 1, 2, 1) > small
+    assert lib.dil_prefill_workspace_bytes(4, 256, 1024, 64, 1, 2) > 0
+    assert lib.dil_backward_workspace_bytes(4, 512, 64, 1, 2) >= 0
+
+
+def test_argument_errors_before_any_launch(lib):
+    # invalid head_dim / dtype / precision / shapes are rejected on the host
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 48, 1, None, 0, None) == -1
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 64, 7, None, 0, None) == -2
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 9, 64, 1, None, 0, None) == -4
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 64, 1, None, 0, None) == -3
+    assert lib.dil_forward(None, None, None, 1, 8, 64, 1, 9, None, None, None, None, None, None,
+                           None, None, 0, None) == -5
+    assert lib.dil_prefill_chunk(None, None, None, 1, 8, 4, 10, 64, 1, 2, None, None, None, None,
+                                 None, None, None, 0, None) == -4
+
+
+def test_python_layer_raises_without_gpu_tensors():
+    import torch
+    from dilution import kernels
+
+    x = torch.zeros(1, 1, 4, 64)
+    with pytest.raises(RuntimeError):
+        kernels.dilution_attention_forward(x, x, x)
+    with pytest.raises(ValueError):
+        kernels.dilution_attention_forward(x, x, x, dot_precision="fp16")

@@ -1,0 +1,91 @@
+"""Cached decode parity (reference pattern: tests/test_kernels.py:205-241).
+
+Token after token, the HIP decode step must reproduce the oracle's row t of
+the full-sequence operator, advance the fp32 demand vector in place to the
+column sums of p (within 1e-5 of the float64 oracle), and never touch the
+spare capacity beyond `length`.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import max_abs, needs_gpu
+from oracle import dilution_oracle as orc
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+TOL_OUT = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [16, 32, 64, 128])
+def test_decode_matches_oracle_rows(dtype, head_dim):
+    from dilution import kernels
+
+    batch, heads, prefix, steps = 2, 4, 37, 6
+    total = prefix + steps
+    q, k, v = orc.make_inputs((batch, heads, total, head_dim), seed=1000 + head_dim)
+    q, k, v = (x.to(dtype) for x in (q, k, v))           # the kernel's inputs
+    full = orc.attention_f64(q, k, v)                     # oracle on the same (rounded) values
+    prec = "bf16" if dtype == torch.bfloat16 else "ieee"
+    qg, kg, vg = (x.cuda() for x in (q, k, v))
+    _, aux = kernels.dilution_attention_forward(qg[:, :, :prefix], kg[:, :, :prefix],
+                                                vg[:, :, :prefix], dot_precision=prec,
+                                                return_aux=True)
+    capacity = total + 3                                  # spare rows: never touched
+    kc = torch.zeros(batch, heads, capacity, head_dim, device="cuda", dtype=dtype)
+    vc = torch.zeros_like(kc)
+    kc[:, :, :prefix] = kg[:, :, :prefix]
+    vc[:, :, :prefix] = vg[:, :, :prefix]
+    committed = torch.zeros(batch, heads, capacity, device="cuda")
+    committed[:, :, :prefix] = aux["committed_total"]
+    for t in range(prefix, total):
+        kc[:, :, t] = kg[:, :, t]
+        vc[:, :, t] = vg[:, :, t]
+        out = kernels.dilution_decode_step(qg[:, :, t:t + 1], kc, vc, committed, t + 1)
+        assert out.dtype == dtype and out.shape == (batch, heads, 1, head_dim)
+        assert torch.isfinite(out).all()
+        err = max_abs(out[:, :, 0], full[:, :, t])
+        assert err < TOL_OUT[dtype], f"t={t} max abs err {err}"
+    want = orc.demand_totals(q, k)
+    assert max_abs(committed[:, :, :total], want) < 1e-5
+    assert committed[:, :, total:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize("length", [1, 1023, 1024, 1025, 5000])
+def test_decode_long_context_multi_chunk(length):
+    """Lengths that cross the 1024-key chunk boundary of the split-K decode,
+    with a synthetic non-negative demand vector."""
+    from dilution import kernels
+
+    batch, heads, d = 1, 3, 64
+    g = torch.Generator().manual_seed(length)
+    q = torch.randn(batch, heads, 1, d, generator=g)
+    kc = torch.randn(batch, heads, length + 5, d, generator=g)
+    vc = torch.randn(batch, heads, length + 5, d, generator=g)
+    com = torch.rand(batch, heads, length + 5, generator=g) * 3.0
+    com[..., length - 1:] = 0.0
+    out_ref, com_ref = orc.decode_step(q, kc, vc, com, length)
+    comg = com.cuda()
+    out = kernels.dilution_decode_step(q.cuda(), kc.cuda(), vc.cuda(), comg, length)
+    assert max_abs(out, out_ref) < 1e-4
+    assert max_abs(comg, com_ref) < 1e-5
+    assert comg[..., length:].abs().max().item() == 0
+
+
+def test_decode_argument_errors():
+    from dilution import kernels
+
+    kc = torch.zeros(1, 1, 8, 64, device="cuda")
+    com = torch.zeros(1, 1, 8, device="cuda")
+    with pytest.raises(ValueError):
+        kernels.dilution_decode_step(torch.zeros(1, 1, 2, 64, device="cuda"), kc, kc, com, 2)
+    with pytest.raises(ValueError):
+        kernels.dilution_decode_step(torch.zeros(1, 1, 1, 64, device="cuda"), kc, kc, com, 9)
+    with pytest.raises(ValueError):
+        kernels.dilution_decode_step(torch.zeros(1, 1, 1, 64, device="cuda"), kc, kc, com, 0)
+    with pytest.raises(ValueError):
+        bad = torch.zeros(1, 1, 8, 48, device="cuda")
+        kernels.dilution_decode_step(torch.zeros(1, 1, 1, 48, device="cuda"), bad, bad, com, 2)

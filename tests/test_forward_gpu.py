@@ -1,0 +1,180 @@
+"""Forward parity of the HIP kernels against the CPU oracle.
+
+Reference patterns: tests/test_kernels.py:19-75 (block scan, pk, forward),
+:98-106 (bf16 inputs), :130-149 (checkpoints and totals).  Tolerances are the
+north-star ones: fp32 mode <= 1e-4 max-abs; bf16 mode <= 2e-2 max-abs and
+<= 1e-2 mean-relative against the fp32/fp64 oracle on the bf16-rounded inputs;
+demand totals <= 1e-5.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import max_abs, mean_rel, needs_gpu
+from oracle import dilution_oracle as orc
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+
+@pytest.mark.parametrize("seq", [1, 8, 33, 64, 128, 257, 1025])
+@pytest.mark.parametrize("shape", [(1, 1), (2, 4)])
+def test_forward_fp32_matches_oracle(seq, shape):
+    from dilution import kernels
+
+    batch, heads = shape
+    q, k, v = orc.make_inputs((batch, heads, seq, 64), seed=seq)
+    want = orc.attention_f64(q, k, v)
+    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda())
+    assert got.dtype == torch.float32 and got.shape == q.shape
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("head_dim", [16, 32, 128])
+@pytest.mark.parametrize("prec", ["ieee", "tf32"])
+def test_forward_fp32_head_dims(head_dim, prec):
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((2, 2, 200, head_dim), seed=head_dim)
+    want = orc.attention_f64(q, k, v)
+    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision=prec)
+    assert max_abs(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("seq", [1, 64, 257, 2048])
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_forward_bf16_matches_oracle(seq, head_dim):
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((2, 4, seq, head_dim), seed=7 * seq + head_dim, qk_scale=0.5,
+                              dtype=torch.bfloat16)
+    want = orc.attention_fp32(q, k, v)         # oracle on the bf16-rounded values
+    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision="bf16")
+    assert torch.isfinite(got).all()
+    assert max_abs(got, want) < 2e-2
+    assert mean_rel(got, want) < 1e-2
+
+
+def test_forward_fp32_inputs_bf16_operands():
+    """fp32 tensors with dot_precision="bf16" (bf16 MFMA operands) stay within
+    the bf16 tolerance of the fp32 oracle (reference test_kernels.py:98-106)."""
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((2, 4, 128, 64), seed=0)
+    want = orc.attention_fp32(q, k, v)
+    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision="bf16")
+    assert max_abs(got, want) < 5e-2
+
+
+@pytest.mark.parametrize("seq", [1, 65, 257, 2049])
+def test_checkpoints_totals_and_row_stats(seq):
+    """aux["carry"] holds the demand entering every 32-row block,
+    aux["committed_total"] the column totals of p (reference
+    test_kernels.py:130-149; stricter tolerance)."""
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((1, 2, seq, 32), seed=seq)
+    out, aux = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), return_aux=True,
+                                                  _save_pk=True)
+    assert max_abs(out, orc.attention_f64(q, k, v)) < 1e-4
+    assert max_abs(aux["committed_total"], orc.demand_totals(q, k)) < 1e-5
+    bm = aux["bwd_block_m"]
+    assert bm == 32
+    carry = orc.carry_checkpoints(q, k, bm).reshape(2, -1, seq)
+    assert aux["carry"].shape == carry.shape
+    assert max_abs(aux["carry"], carry) < 1e-5
+    rmax, rden = orc.row_stats(q, k)
+    assert max_abs(aux["rmax"], rmax.reshape(2, seq)) < 1e-4
+    lse_got = aux["rmax"].double().cpu() + torch.log2(aux["rden"].double().cpu())
+    lse_want = (rmax + torch.log2(rden)).reshape(2, seq)
+    assert (lse_got - lse_want).abs().max().item() < 1e-5
+
+
+@pytest.mark.parametrize("head_dim", [16, 32, 64, 128])
+def test_saved_query_correction_pk(head_dim):
+    """pk = (p @ k) / sqrt(d) (reference test_kernels.py:46-59)."""
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((1, 2, 257, head_dim), seed=head_dim)
+    _, aux = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), return_aux=True,
+                                                _save_pk=True)
+    assert max_abs(aux["pk"].reshape(1, 2, 257, head_dim), orc.pk(q, k)) < 2e-5
+
+
+def test_row_chunked_forward_is_identical():
+    """A tiny scratch budget forces one (batch, head) slice per launch; slices
+    are independent, so the result is bit-identical."""
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((2, 3, 300, 64), seed=3, dtype=torch.bfloat16)
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    a = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16")
+    b = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", scratch_budget_gib=1e-9)
+    assert torch.equal(a, b)
+
+
+def test_causality_prefix_bit_identical():
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((1, 2, 200, 64), seed=4, dtype=torch.bfloat16)
+    a = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision="bf16")
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    q2[..., 130:, :] += 1
+    k2[..., 130:, :] -= 1
+    v2[..., 130:, :] *= 3
+    b = kernels.dilution_attention_forward(q2.cuda(), k2.cuda(), v2.cuda(), dot_precision="bf16")
+    assert torch.equal(a[..., :128, :], b[..., :128, :])
+
+
+def test_harmonic_closed_form_on_gpu():
+    """q = 0: every bid is 1/(i+1); the kernel output must equal the
+    harmonic-number closed form."""
+    from dilution import kernels
+    import numpy as np
+
+    t = 300
+    g = torch.Generator().manual_seed(9)
+    v = torch.randn(1, 2, t, 64, generator=g)
+    k = torch.randn(1, 2, t, 64, generator=g)
+    q = torch.zeros_like(v)
+    out, aux = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), return_aux=True)
+    cf, totals = orc.harmonic_closed_form(t, v.numpy())
+    assert np.abs(out.double().cpu().numpy() - cf).max() < 1e-4
+    assert np.abs(aux["committed_total"].double().cpu().numpy() - totals).max() < 1e-5
+
+
+@pytest.mark.parametrize("prec,dtype,tol", [("ieee", torch.float32, 1e-4),
+                                            ("bf16", torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("chunk", [32, 100, 256])
+def test_chunked_prefill_matches_full_forward(prec, dtype, tol, chunk):
+    from dilution import kernels
+
+    batch, heads, seq, d = 2, 2, 600, 64
+    q, k, v = orc.make_inputs((batch, heads, seq, d), seed=chunk, dtype=dtype)
+    full = orc.attention_f64(q, k, v)
+    cap = seq + 7
+    kc = torch.zeros(batch, heads, cap, d, dtype=dtype, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:, :, :seq] = k.cuda()
+    vc[:, :, :seq] = v.cuda()
+    committed = torch.zeros(batch, heads, cap, device="cuda")
+    for start in range(0, seq, chunk):
+        stop = min(start + chunk, seq)
+        out = kernels.dilution_prefill_chunk(q[:, :, start:stop].cuda(), kc, vc, committed, start,
+                                             dot_precision=prec)
+        assert max_abs(out, full[:, :, start:stop]) < tol, start
+    assert max_abs(committed[:, :, :seq], orc.demand_totals(q, k)) < 1e-5
+    assert committed[:, :, seq:].abs().max().item() == 0
+
+
+def test_precision_argument_errors():
+    from dilution import kernels
+
+    q = torch.zeros(1, 1, 4, 64, device="cuda")
+    with pytest.raises(ValueError):
+        kernels.dilution_attention_forward(q, q, q, dot_precision="fp8")
+    with pytest.raises(ValueError):
+        x = torch.zeros(1, 1, 4, 48, device="cuda")
+        kernels.dilution_attention_forward(x, x, x)
