@@ -1,10 +1,632 @@
-// Backward of the dilution-attention operator (in progress).
+// Backward of the dilution-attention operator.
+//
+// Reference behaviour: _DilutionAttentionFn.backward,
+// /root/reference/src/dilution/kernels.py:851-903, and the decomposition in
+// /root/reference/docs/kernels.md:62-84:
+//
+//   ds_ij    = (dO_i . v_j - dbar_i) / (S_i + eps),   dbar_i = dO_i . o_i
+//   inv_ij   = 1 / (c_ij + p_ij + eps)               (c: exclusive demand)
+//   dks_ij   = -ds_ij p_ij inv_ij^2                   (adjoint through the demand)
+//   suffix_ij = sum_{i' > i} dks_i'j                  (reverse column scan)
+//   dp_ij    = ds_ij (c_ij + eps) inv_ij^2 + suffix_ij = ds_ij (inv - p inv^2) + suffix_ij
+//   ghat_i   = sum_j p_ij dp_ij,   da_ij = p_ij (dp_ij - ghat_i)
+//   dq = s da K,   dk = s da^T Q,   dv = A^T dO
+//
+// Kernels (gfx950; deterministic, no atomics):
+//   bwd_rows   lse = rmax + log2 rden, 1/(S + eps), dbar per row.
+//   bwd_key    one wave per 32-key tile, query tiles of 32 walked in reverse:
+//              p, demand (checkpoint + in-tile scan), dv += A^T dO, ds from
+//              dO V^T, the running per-key suffix of dks (stored at every tile
+//              boundary), dk_main += (p dp)^T Q.  All products on MFMA with
+//              keys in lanes, so no operand needs a transposition.
+//   bwd_query  one wave per 32-row tile over the causal key tiles: the same
+//              chain with the suffix read from bwd_key's checkpoints; ghat as
+//              the row sum of p dp; (p dp) transposed by an identity MFMA so
+//              (p dp) @ K runs with queries in lanes; dq = s (p dp) K - ghat pk
+//              (pk = s p @ k saved by the forward).
+//   bwd_dkcorr one wave per key tile: dk = dk_main - s sum_i p_ij ghat_i q_i.
 #include "dil_common.hpp"
 #include "dil_internal.hpp"
+#include "dil_tiles.hpp"
 
 namespace dil {
 
-int64_t backward_workspace_bytes(int64_t, int64_t, int, int, int) { return 0; }
-int backward(const BackwardArgs&) { return kErrShape; }
+namespace {
+
+struct BwdParams {
+  const void* q;      // CT rows (n, T, D)
+  const void* k;
+  const void* v;
+  const void* dout;   // CT rows
+  const void* qt;     // CT (n, D, T_pad) transposed copies
+  const void* kt;
+  const void* dot;
+  int64_t T, t_pad, nb;
+  float c, scale;
+  const float* lse;   // (n, T)
+  const float* sinv;
+  const float* dbar;
+  float* ghat;        // (n, T)
+  const float* carry; // (n, nb, T)
+  float* sufk;        // (n, nb, T)
+  float* dkm;         // (n, T, D) fp32: scale * sum_i (p dp)_ij q_i
+  const float* pk;    // (n, T, D)
+  void* dq;
+  void* dk;
+  void* dv;
+  int gdt;            // grad dtype
+};
+
+// ---------------------------------------------------------------------------
+// per-row prologue
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, int ddt,
+                                                const float* __restrict__ out,
+                                                const float* __restrict__ rmax,
+                                                const float* __restrict__ rden,
+                                                const float* __restrict__ ssum, float* __restrict__ lse,
+                                                float* __restrict__ sinv, float* __restrict__ dbar,
+                                                int64_t rows) {
+  constexpr int LPR = D / 8;                    // lanes per row, 8 elements each
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t row = gid / LPR;
+  const int sub = threadIdx.x % LPR;
+  float acc = 0.f;
+  if (row < rows) {
+    float a[8], b[8];
+    load8_f32(dout, row * D + sub * 8, ddt, a);
+    load8_f32(out, row * D + sub * 8, DT_F32, b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(a[e], b[e], acc);
+  }
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+  if (row < rows && sub == 0) {
+    dbar[row] = acc;
+    lse[row] = rmax[row] + __log2f(rden[row]);
+    sinv[row] = 1.f / (ssum[row] + kEps);
+  }
+}
+
+// Per-row statistics of one 32-row tile staged in LDS.
+struct RowStatsLoader {
+  float r;
+  __device__ void load(const float* a, const float* b, const float* c, int64_t row0, int64_t T) {
+    const int t = threadIdx.x;
+    r = 0.f;
+    if (t < 3 * kTileQ) {
+      const float* src = t < kTileQ ? a : (t < 2 * kTileQ ? b : c);
+      const int64_t row = row0 + (t % kTileQ);
+      // rows past the end: lse = +inf makes p = 0
+      r = row < T ? src[row] : (t < kTileQ ? INFINITY : 0.f);
+    }
+  }
+  __device__ void store(float* lds) const {
+    if (threadIdx.x < 3 * kTileQ) lds[threadIdx.x] = r;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// key-parallel reverse pass
+
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
+  using TL = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
+  __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
+  __shared__ float st_s[2][3 * kTileQ];   // lse, sinv, dbar
+
+  const int64_t slice = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int kb0 = blockIdx.x * 4;
+  const int kb = kb0 + wave;                     // key tile of this wave
+  const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
+  const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
+  const bool active = static_cast<int64_t>(kb) * kTileK < P.T;
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.T * D;
+  const CT* dos = static_cast<const CT*>(P.dout) + slice * P.T * D;
+  const CT* qts = static_cast<const CT*>(P.qt) + slice * D * P.t_pad;
+  const CT* dots = static_cast<const CT*>(P.dot) + slice * D * P.t_pad;
+  const float* lse = P.lse + slice * P.T;
+  const float* sinv = P.sinv + slice * P.T;
+  const float* dbar = P.dbar + slice * P.T;
+
+  // this wave's keys as B operands (natural order: lane <-> key)
+  RowFrag<CT, D> kf, vf;
+  if (key < P.T) {
+    load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
+    load_row_frag<CT, D>(vf, static_cast<const CT*>(P.v) + (slice * P.T + key) * D + h * (D / 2));
+  } else {
+    zero_row_frag<CT, D>(kf);
+    zero_row_frag<CT, D>(vf);
+  }
+  floatx16 dka[kDTiles<D>], dva[kDTiles<D>];
+#pragma unroll
+  for (int t = 0; t < kDTiles<D>; ++t) { dka[t] = floatx16{}; dva[t] = floatx16{}; }
+  float sufk = 0.f;
+
+  KTileLoader<CT, D> ql, dl;
+  TTileLoader<CT, D> qtl, dtl;
+  RowStatsLoader sl;
+  auto fetch = [&](int qt) {
+    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
+    ql.load(qs, row0, P.T);
+    dl.load(dos, row0, P.T);
+    qtl.load(qts, P.t_pad, row0);
+    dtl.load(dots, P.t_pad, row0);
+    sl.load(lse, sinv, dbar, row0, P.T);
+  };
+  auto stash = [&](int buf) {
+    ql.store(q_s[buf]);
+    dl.store(do_s[buf]);
+    qtl.store(qt_s[buf]);
+    dtl.store(dot_s[buf]);
+    sl.store(st_s[buf]);
+  };
+  constexpr int kSteps = kTileQ / Mma<CT>::kStep;
+
+  fetch(nq - 1);
+  stash(0);
+  __syncthreads();
+  int it = 0;
+  for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
+    const int buf = it & 1;
+    if (qt - 1 >= kb0) fetch(qt - 1);
+    if (active && qt >= kb) {
+      const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
+      const float* st = st_s[buf];
+      RowFrag<CT, D> qf;
+      lds_row_frag<CT, D>(qf, q_s[buf], rho(l32), h);
+      const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+      const bool diag = qt == kb;
+      float p[16], x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = perm_row(i, h);
+        p[i] = fast_exp2(fmaf(sacc[i], P.c, -st[r]));
+        if (diag && key > row0 + r) p[i] = 0.f;
+        x[i] = p[i];
+      }
+      const float cin = key < P.T ? P.carry[(slice * P.nb + qt) * P.T + key] : 0.f;
+      column_scan_inclusive(x, cin + kEps, h);
+      float inv[16], w[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        inv[i] = fast_rcp(x[i]);
+        w[i] = p[i] * inv[i] * st[kTileQ + perm_row(i, h)];   // attn = share / (S + eps)
+      }
+      // dv^T += dO^T A   (A^T dO with keys in lanes)
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const auto bfr = acc_frag<CT>(w, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          dva[t] = Mma<CT>::mma(lds_t_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
+      }
+      RowFrag<CT, D> dof;
+      lds_row_frag<CT, D>(dof, do_s[buf], rho(l32), h);
+      const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
+      float ds[16], tq[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = perm_row(i, h);
+        ds[i] = (dov[i] - st[2 * kTileQ + r]) * st[kTileQ + r];
+        tq[i] = p[i] * inv[i] * inv[i];      // p inv^2
+        x[i] = -ds[i] * tq[i];               // dks
+      }
+      if (h == 0 && key < P.T) P.sufk[(slice * P.nb + qt) * P.T + key] = sufk;
+      sufk += column_scan_suffix_exclusive(x, sufk, h) ;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i] = p[i] * (ds[i] * (inv[i] - tq[i]) + x[i]);   // p dp
+      // dk_main^T += Q^T (p dp)
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const auto bfr = acc_frag<CT>(w, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          dka[t] = Mma<CT>::mma(lds_t_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
+      }
+    }
+    if (qt - 1 >= kb0) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (key < P.T) {
+    float* dkrow = P.dkm + (slice * P.T + key) * D;
+    const int64_t dvrow = (slice * P.T + key) * D;
+#pragma unroll
+    for (int t = 0; t < kDTiles<D>; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * t + acc_row(i, h);
+        if (d < D) {
+          dkrow[d] = dka[t][i] * P.scale;
+          store_as(P.dv, dvrow + d, P.gdt, dva[t][i]);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// row-parallel dq pass
+
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
+  using TL = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
+  __shared__ float g_s[4][kTileQ];
+
+  const int64_t slice = blockIdx.y;
+  const int g = gridDim.x - 1 - blockIdx.x;            // heavy (late) row groups first
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int qt = g * 4 + wave;
+  const int64_t r0 = static_cast<int64_t>(qt) * kTileQ;
+  const int64_t wg_last = min(static_cast<int64_t>(g * 4 + 4) * kTileQ, P.T);
+  const int nkt_wg = static_cast<int>((wg_last + kTileK - 1) / kTileK);
+  const int nkt_w = r0 < P.T ? qt + 1 : 0;
+
+  const CT* ks = static_cast<const CT*>(P.k) + slice * P.T * D;
+  const CT* vs = static_cast<const CT*>(P.v) + slice * P.T * D;
+  const CT* kts = static_cast<const CT*>(P.kt) + slice * D * P.t_pad;
+
+  // this wave's rows, rho-permuted: register i of half h <-> row perm_row(i, h)
+  RowFrag<CT, D> qf, dof;
+  const int64_t my_row = r0 + rho(l32);
+  if (my_row < P.T) {
+    load_row_frag<CT, D>(qf, static_cast<const CT*>(P.q) + (slice * P.T + my_row) * D + h * (D / 2));
+    load_row_frag<CT, D>(dof, static_cast<const CT*>(P.dout) + (slice * P.T + my_row) * D + h * (D / 2));
+  } else {
+    zero_row_frag<CT, D>(qf);
+    zero_row_frag<CT, D>(dof);
+  }
+  float lse[16], si[16], db[16], gh[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t r = r0 + perm_row(i, h);
+    const bool ok = r < P.T;
+    lse[i] = ok ? P.lse[slice * P.T + r] : INFINITY;
+    si[i] = ok ? P.sinv[slice * P.T + r] : 0.f;
+    db[i] = ok ? P.dbar[slice * P.T + r] : 0.f;
+    gh[i] = 0.f;
+  }
+  constexpr int kSteps = kTileK / Mma<CT>::kStep;
+  typename Mma<CT>::frag ident[kSteps];
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) ident[s] = ident_frag<CT>(l32, h, s);
+  floatx16 dqa[kDTiles<D>];
+#pragma unroll
+  for (int t = 0; t < kDTiles<D>; ++t) dqa[t] = floatx16{};
+  const float* crow = P.carry + (slice * P.nb + qt) * P.T;
+  const float* srow = P.sufk + (slice * P.nb + qt) * P.T;
+
+  KTileLoader<CT, D> kl, vl;
+  TTileLoader<CT, D> ktl;
+  kl.load(ks, 0, P.T);
+  vl.load(vs, 0, P.T);
+  ktl.load(kts, P.t_pad, 0);
+  kl.store(k_s[0]);
+  vl.store(v_s[0]);
+  ktl.store(kt_s[0]);
+  __syncthreads();
+  for (int kt = 0; kt < nkt_wg; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nkt_wg) {
+      const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
+      kl.load(ks, key0n, P.T);
+      vl.load(vs, key0n, P.T);
+      ktl.load(kts, P.t_pad, key0n);
+    }
+    if (kt < nkt_w) {
+      const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);   // key owned by this lane
+      RowFrag<CT, D> kf;
+      lds_row_frag<CT, D>(kf, k_s[buf], rho(l32), h);
+      const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+      const bool diag = kt == qt;
+      float p[16], x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        p[i] = fast_exp2(fmaf(sacc[i], P.c, -lse[i]));
+        if (diag && key > r0 + perm_row(i, h)) p[i] = 0.f;
+        x[i] = p[i];
+      }
+      const bool kok = key < P.T;
+      column_scan_inclusive(x, (kok ? crow[key] : 0.f) + kEps, h);
+      float inv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) inv[i] = fast_rcp(x[i]);
+      RowFrag<CT, D> vf;
+      lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
+      const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
+      float ds[16], tq[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        ds[i] = (dov[i] - db[i]) * si[i];
+        tq[i] = p[i] * inv[i] * inv[i];
+        x[i] = -ds[i] * tq[i];
+      }
+      column_scan_suffix_exclusive(x, kok ? srow[key] : 0.f, h);
+      float w[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        w[i] = p[i] * (ds[i] * (inv[i] - tq[i]) + x[i]);   // p dp
+        gh[i] += w[i];
+      }
+      // transpose (p dp) so queries sit in lanes, then dq += (p dp) K
+      floatx16 xt = floatx16{};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(w, s), ident[s], xt);
+      float xv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xv[i] = xt[i];
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const auto af = acc_frag<CT>(xv, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
+      }
+    }
+    if (kt + 1 < nkt_wg) {
+      kl.store(k_s[buf ^ 1]);
+      vl.store(v_s[buf ^ 1]);
+      ktl.store(kt_s[buf ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // ghat: row sums of p dp over all keys
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float v = gh[i];
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 64);
+    gh[i] = v;
+  }
+  if (l32 == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) g_s[wave][perm_row(i, h)] = gh[i];
+  }
+  __syncthreads();
+  if (h == 0 && r0 + l32 < P.T) P.ghat[slice * P.T + r0 + l32] = g_s[wave][l32];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = acc_row(i, h);
+    if (r0 + row < P.T) {
+      const float gr = g_s[wave][row];
+      const int64_t base = (slice * P.T + r0 + row) * D;
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t) {
+        const int d = 32 * t + l32;
+        if (d < D) store_as(P.dq, base + d, P.gdt, dqa[t][i] * P.scale - gr * P.pk[base + d]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// softmax-Jacobian correction of dk
+
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
+  using TL = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
+  __shared__ float st_s[2][3 * kTileQ];   // lse, ghat, (unused)
+
+  const int64_t slice = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int kb0 = blockIdx.x * 4;
+  const int kb = kb0 + wave;
+  const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
+  const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
+  const bool active = static_cast<int64_t>(kb) * kTileK < P.T;
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.T * D;
+  const CT* qts = static_cast<const CT*>(P.qt) + slice * D * P.t_pad;
+  const float* lse = P.lse + slice * P.T;
+  const float* gh = P.ghat + slice * P.T;
+
+  RowFrag<CT, D> kf;
+  if (key < P.T) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
+  else zero_row_frag<CT, D>(kf);
+  floatx16 dkc[kDTiles<D>];
+#pragma unroll
+  for (int t = 0; t < kDTiles<D>; ++t) dkc[t] = floatx16{};
+
+  KTileLoader<CT, D> ql;
+  TTileLoader<CT, D> qtl;
+  RowStatsLoader sl;
+  auto fetch = [&](int qt) {
+    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
+    ql.load(qs, row0, P.T);
+    qtl.load(qts, P.t_pad, row0);
+    sl.load(lse, gh, gh, row0, P.T);
+  };
+  auto stash = [&](int buf) {
+    ql.store(q_s[buf]);
+    qtl.store(qt_s[buf]);
+    sl.store(st_s[buf]);
+  };
+  constexpr int kSteps = kTileQ / Mma<CT>::kStep;
+
+  fetch(kb0);
+  stash(0);
+  __syncthreads();
+  int it = 0;
+  for (int qt = kb0; qt < nq; ++qt, ++it) {
+    const int buf = it & 1;
+    if (qt + 1 < nq) fetch(qt + 1);
+    if (active && qt >= kb) {
+      const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
+      const float* st = st_s[buf];
+      RowFrag<CT, D> qf;
+      lds_row_frag<CT, D>(qf, q_s[buf], rho(l32), h);
+      const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+      const bool diag = qt == kb;
+      float w[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = perm_row(i, h);
+        float p = fast_exp2(fmaf(sacc[i], P.c, -st[r]));
+        if (diag && key > row0 + r) p = 0.f;
+        w[i] = p * st[kTileQ + r];
+      }
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const auto bfr = acc_frag<CT>(w, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          dkc[t] = Mma<CT>::mma(lds_t_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dkc[t]);
+      }
+    }
+    if (qt + 1 < nq) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (key < P.T) {
+    const int64_t base = (slice * P.T + key) * D;
+#pragma unroll
+    for (int t = 0; t < kDTiles<D>; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * t + acc_row(i, h);
+        if (d < D) store_as(P.dk, base + d, P.gdt, P.dkm[base + d] - dkc[t][i] * P.scale);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+struct BwdWorkspace {
+  size_t lse, sinv, dbar, ghat, sufk, dkm, qt, kt, dot, qc, kc, vc, doc, total;
+};
+
+BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int lowp) {
+  const size_t ct = lowp ? 2 : 4;
+  const int ctc = lowp ? DT_BF16 : DT_F32;
+  const bool convert = dtype != ctc;
+  const bool convert_do = dout_dtype != ctc;
+  const int64_t nb = (T + kTileQ - 1) / kTileQ;
+  const size_t rowf = align_up(4 * n * T);
+  const size_t tsz = align_up(ct * n * D * pad64(T));
+  const size_t rsz = align_up(ct * n * T * D);
+  BwdWorkspace w{};
+  w.lse = 0;
+  w.sinv = w.lse + rowf;
+  w.dbar = w.sinv + rowf;
+  w.ghat = w.dbar + rowf;
+  w.sufk = w.ghat + rowf;
+  w.dkm = w.sufk + align_up(4 * n * nb * T);
+  w.qt = w.dkm + align_up(4 * n * T * D);
+  w.kt = w.qt + tsz;
+  w.dot = w.kt + tsz;
+  w.qc = w.dot + tsz;
+  w.kc = w.qc + (convert ? rsz : 0);
+  w.vc = w.kc + (convert ? rsz : 0);
+  w.doc = w.vc + (convert ? rsz : 0);
+  w.total = w.doc + (convert_do ? rsz : 0);
+  return w;
+}
+
+template <typename CT, int D>
+int launch_backward(const BackwardArgs& a) {
+  // the workspace is sized for the worst case (dout converted), so that the
+  // size query need not know dout's dtype
+  const int ctc = sizeof(CT) == 2 ? DT_BF16 : DT_F32;
+  const BwdWorkspace w = bwd_layout(a.n, a.T, D, a.dtype, ctc == DT_BF16 ? DT_F32 : DT_BF16, a.lowp);
+  char* ws = static_cast<char*>(a.workspace);
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+  const bool convert = a.dtype != ctc;
+  const bool convert_do = a.dout_dtype != ctc;
+  const int64_t t_pad = pad64(a.T);
+  const unsigned n = static_cast<unsigned>(a.n);
+  const int64_t sn = a.T * D;
+
+  CT* qt = reinterpret_cast<CT*>(ws + w.qt);
+  CT* kt = reinterpret_cast<CT*>(ws + w.kt);
+  CT* dot = reinterpret_cast<CT*>(ws + w.dot);
+  CT* qc = convert ? reinterpret_cast<CT*>(ws + w.qc) : nullptr;
+  CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
+  CT* vc = convert ? reinterpret_cast<CT*>(ws + w.vc) : nullptr;
+  CT* doc = convert_do ? reinterpret_cast<CT*>(ws + w.doc) : nullptr;
+
+  const dim3 gp(static_cast<unsigned>(t_pad / 64), n);
+  prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt, D * t_pad, t_pad);
+  prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt, D * t_pad, t_pad);
+  if (convert)
+    prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn, nullptr, 0, t_pad);
+  prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot, D * t_pad,
+                                              t_pad);
+
+  BwdParams P{};
+  P.q = convert ? static_cast<const void*>(qc) : a.q;
+  P.k = convert ? static_cast<const void*>(kc) : a.k;
+  P.v = convert ? static_cast<const void*>(vc) : a.v;
+  P.dout = convert_do ? static_cast<const void*>(doc) : a.dout;
+  P.qt = qt;
+  P.kt = kt;
+  P.dot = dot;
+  P.T = a.T;
+  P.t_pad = t_pad;
+  P.nb = (a.T + kTileQ - 1) / kTileQ;
+  P.scale = 1.f / sqrtf(static_cast<float>(D));
+  P.c = kLog2e * P.scale;
+  float* lse = reinterpret_cast<float*>(ws + w.lse);
+  float* sinv = reinterpret_cast<float*>(ws + w.sinv);
+  float* dbar = reinterpret_cast<float*>(ws + w.dbar);
+  P.lse = lse;
+  P.sinv = sinv;
+  P.dbar = dbar;
+  P.ghat = reinterpret_cast<float*>(ws + w.ghat);
+  P.carry = a.carry;
+  P.sufk = reinterpret_cast<float*>(ws + w.sufk);
+  P.dkm = reinterpret_cast<float*>(ws + w.dkm);
+  P.pk = a.pk;
+  P.dq = a.dq;
+  P.dk = a.dk;
+  P.dv = a.dv;
+  P.gdt = a.grad_dtype;
+
+  const int64_t rows = a.n * a.T;
+  const int64_t threads = rows * (D / 8);
+  bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
+      a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbar, rows);
+  const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
+  const dim3 gkey(static_cast<unsigned>((nkt + 3) / 4), n);
+  bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P);
+  bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P);
+  bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int D>
+int dispatch_backward(const BackwardArgs& a) {
+  return a.lowp ? launch_backward<__bf16, D>(a) : launch_backward<float, D>(a);
+}
+
+}  // namespace
+
+int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int lowp) {
+  // sized with dout needing conversion (the larger case)
+  return static_cast<int64_t>(
+      bwd_layout(n, T, head_dim, dtype, lowp ? DT_F32 : DT_BF16, lowp).total);
+}
+
+int backward(const BackwardArgs& a) {
+  switch (a.head_dim) {
+    case 16: return dispatch_backward<16>(a);
+    case 32: return dispatch_backward<32>(a);
+    case 64: return dispatch_backward<64>(a);
+    case 128: return dispatch_backward<128>(a);
+    default: return kErrHeadDim;
+  }
+}
 
 }  // namespace dil

@@ -190,4 +190,36 @@ __device__ __forceinline__ float column_scan_inclusive(float (&x)[16], float bas
   return tlo + thi + plo + phi;
 }
 
+
+// Reverse (suffix) scan over the 32 rows of an accumulator tile in the
+// permuted layout.  On return x[i] holds base + the sum of the column's
+// entries at rows strictly after row(i).  Returns the column total.
+__device__ __forceinline__ float column_scan_suffix_exclusive(float (&x)[16], float base, int h) {
+  float s = 0.f;
+#pragma unroll
+  for (int t = 7; t >= 0; --t) {
+    const float v = x[t];
+    x[t] = s;
+    s += v;
+  }
+  const float tlo = s;
+  s = 0.f;
+#pragma unroll
+  for (int t = 15; t >= 8; --t) {
+    const float v = x[t];
+    x[t] = s;
+    s += v;
+  }
+  const float thi = s;
+  const float plo = partner32(tlo), phi = partner32(thi);
+  // column order: [h0 lo][h1 lo][h0 hi][h1 hi]; add what lies after each run
+  const float off_lo = base + (h ? (phi + thi) : (plo + thi + phi));
+  const float off_hi = base + (h ? 0.f : phi);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) x[t] += off_lo;
+#pragma unroll
+  for (int t = 8; t < 16; ++t) x[t] += off_hi;
+  return tlo + thi + plo + phi;
+}
+
 }  // namespace dil
