@@ -20,7 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(os.path.dirname(HERE), "dilution")
 OUT = os.path.join(PKG, "libdilution_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["dil_api.hip", "dil_decode.hip", "dil_forward.hip", "dil_backward.hip"]
+SOURCES = ["dil_api.hip", "dil_decode.hip", "dil_forward.hip", "dil_backward.hip", "dil_timing.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -558,12 +558,19 @@ int launch_backward(const BackwardArgs& a) {
   CT* doc = convert_do ? reinterpret_cast<CT*>(ws + w.doc) : nullptr;
 
   const dim3 gp(static_cast<unsigned>(t_pad / 64), n);
-  prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt, D * t_pad, t_pad);
-  prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt, D * t_pad, t_pad);
+  DIL_TIMED("prep", st,
+            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt, D * t_pad,
+                                                        t_pad));
+  DIL_TIMED("prep", st,
+            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt, D * t_pad,
+                                                        t_pad));
   if (convert)
-    prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn, nullptr, 0, t_pad);
-  prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot, D * t_pad,
-                                              t_pad);
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn, nullptr, 0,
+                                                          t_pad));
+  DIL_TIMED("prep", st,
+            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot,
+                                                        D * t_pad, t_pad));
 
   BwdParams P{};
   P.q = convert ? static_cast<const void*>(qc) : a.q;
@@ -596,13 +603,14 @@ int launch_backward(const BackwardArgs& a) {
 
   const int64_t rows = a.n * a.T;
   const int64_t threads = rows * (D / 8);
-  bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
-      a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbar, rows);
+  DIL_TIMED("bwd_rows", st,
+            bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
+                a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbar, rows));
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   const dim3 gkey(static_cast<unsigned>((nkt + 3) / 4), n);
-  bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P);
-  bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P);
-  bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P);
+  DIL_TIMED("bwd_key", st, bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P));
+  DIL_TIMED("bwd_query", st, bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P));
+  DIL_TIMED("bwd_dkcorr", st, bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P));
   return static_cast<int>(hipGetLastError());
 }
 

@@ -231,12 +231,16 @@ int launch_decode(const DecodeArgs& a) {
   const float qscale = kLog2e / sqrtf(static_cast<float>(D));
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   dim3 grid(nchunk, static_cast<unsigned>(a.n));
-  dec_stats<D><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length,
-                                             chunk, nchunk, a.dtype, qscale);
-  dec_apply<D><<<grid, kDecThreads, 0, st>>>(a.v_cache, a.kv_sn, a.committed, a.c_sn, aff, part,
-                                             part_out, a.length, chunk, nchunk, a.dtype);
-  dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 64, 0, st>>>(part_out, nchunk, a.out, a.o_sn,
-                                                                  a.dtype);
+  DIL_TIMED("dec_stats", st,
+            dec_stats<D><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff, part,
+                                                       a.length, chunk, nchunk, a.dtype, qscale));
+  DIL_TIMED("dec_apply", st,
+            dec_apply<D><<<grid, kDecThreads, 0, st>>>(a.v_cache, a.kv_sn, a.committed, a.c_sn, aff,
+                                                       part, part_out, a.length, chunk, nchunk,
+                                                       a.dtype));
+  DIL_TIMED("dec_finish", st,
+            dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 64, 0, st>>>(part_out, nchunk, a.out,
+                                                                            a.o_sn, a.dtype));
   return static_cast<int>(hipGetLastError());
 }
 

@@ -403,14 +403,18 @@ int launch_forward(const ForwardArgs& a) {
 
   // operands in the compute type; V^T (and K^T) tiles
   const dim3 gk(static_cast<unsigned>(tk_pad / 64), n);
-  prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr, 0, vt,
-                                              D * tk_pad, tk_pad);
+  DIL_TIMED("prep", st,
+            prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr, 0, vt,
+                                                        D * tk_pad, tk_pad));
   if (convert || kt != nullptr)
-    prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc, a.Tk * D, kt,
-                                                D * tk_pad, tk_pad);
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc, a.Tk * D,
+                                                          kt, D * tk_pad, tk_pad));
   if (convert) {
     const dim3 gq(static_cast<unsigned>(pad64(a.C) / 64), n);
-    prep_kernel<CT, D><<<gq, kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc, a.C * D, nullptr, 0, 0);
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<gq, kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc, a.C * D,
+                                                          nullptr, 0, 0));
   }
 
   FwdParams P{};
@@ -441,11 +445,12 @@ int launch_forward(const ForwardArgs& a) {
   P.pk = a.pk;
 
   const dim3 grid(static_cast<unsigned>((a.C + 4 * kTileQ - 1) / (4 * kTileQ)), n);
-  if (a.pk) fwd_stats<CT, D, true><<<grid, kThreads, 0, st>>>(P);
-  else fwd_stats<CT, D, false><<<grid, kThreads, 0, st>>>(P);
-  fwd_scan<<<dim3(static_cast<unsigned>((a.Tk + 255) / 256), n), 256, 0, st>>>(
-      a.carry, P.nb, a.Tk, a.q0, a.C, a.demand_in, a.din_sn, a.total, a.tot_sn);
-  fwd_out<CT, D><<<grid, kThreads, 0, st>>>(P);
+  if (a.pk) DIL_TIMED("fwd_stats", st, fwd_stats<CT, D, true><<<grid, kThreads, 0, st>>>(P));
+  else DIL_TIMED("fwd_stats", st, fwd_stats<CT, D, false><<<grid, kThreads, 0, st>>>(P));
+  DIL_TIMED("fwd_scan", st,
+            fwd_scan<<<dim3(static_cast<unsigned>((a.Tk + 255) / 256), n), 256, 0, st>>>(
+                a.carry, P.nb, a.Tk, a.q0, a.C, a.demand_in, a.din_sn, a.total, a.tot_sn));
+  DIL_TIMED("fwd_out", st, fwd_out<CT, D><<<grid, kThreads, 0, st>>>(P));
   return static_cast<int>(hipGetLastError());
 }
 

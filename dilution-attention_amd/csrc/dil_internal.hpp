@@ -16,6 +16,30 @@ constexpr int kErrPrecision = -5;
 
 inline size_t align_up(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
 
+// Brackets one kernel launch with hipEvents on `stream` while kernel timing
+// is enabled (dil_timing_enable); a no-op otherwise.  `name` must be a string
+// literal: it is kept until the timing is read.
+class LaunchTimer {
+ public:
+  LaunchTimer(const char* name, void* stream);
+  ~LaunchTimer();
+  LaunchTimer(const LaunchTimer&) = delete;
+  LaunchTimer& operator=(const LaunchTimer&) = delete;
+
+ private:
+  const char* name_;
+  void* stream_;
+  void* start_ = nullptr;
+  void* stop_ = nullptr;
+};
+
+// Launch `expr` (a kernel launch statement) inside a LaunchTimer scope.
+#define DIL_TIMED(name, stream, ...) \
+  do {                               \
+    ::dil::LaunchTimer _dil_t(name, stream); \
+    __VA_ARGS__;                     \
+  } while (0)
+
 struct DecodeArgs {
   const void* q1;        // (n, D) rows, slice stride q_sn elements
   int64_t q_sn;

@@ -33,6 +33,11 @@ SIGNATURES = {
     "dil_decode_workspace_bytes": (_c_int64, [_c_int64, _c_int64, _c_int]),
     "dil_decode_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _c_int,
                                  _c_int, _vp, _c_int64, _vp]),
+    "dil_timing_enable": (_c_int, [_c_int]),
+    "dil_timing_reset": (_c_int, []),
+    "dil_timing_count": (_c_int, []),
+    "dil_timing_read": (_c_int, [_c_int, ctypes.c_char_p, _c_int, ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(_c_int64)]),
 }
 
 ABI_VERSION = 1
@@ -81,3 +86,34 @@ def check(status: int, what: str) -> None:
     if status != 0:
         msg = lib().dil_status_string(status).decode()
         raise RuntimeError(f"{what} failed with status {status}: {msg}")
+
+
+class kernel_timing:
+    """Context manager: per-kernel launch counts and summed HIP-event time of
+    every library launch inside the block.
+
+        with kernel_timing() as kt:
+            ...
+        kt.result  # {name: (launches, total_ms)}
+    """
+
+    def __enter__(self):
+        handle = lib()
+        check(handle.dil_timing_reset(), "dil_timing_reset")
+        handle.dil_timing_enable(1)
+        self.result = {}
+        return self
+
+    def __exit__(self, *exc):
+        handle = lib()
+        handle.dil_timing_enable(0)
+        count = handle.dil_timing_count()
+        name = ctypes.create_string_buffer(64)
+        ms = ctypes.c_double()
+        launches = _c_int64()
+        for i in range(count):
+            check(handle.dil_timing_read(i, name, 64, ctypes.byref(ms), ctypes.byref(launches)),
+                  "dil_timing_read")
+            self.result[name.value.decode()] = (int(launches.value), float(ms.value))
+        check(handle.dil_timing_reset(), "dil_timing_reset")
+        return False

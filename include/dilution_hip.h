@@ -123,6 +123,22 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
                     void* out, int64_t n, int64_t capacity, int64_t length, int head_dim,
                     int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Kernel timing for measurement harnesses.  No reference counterpart (the
+ * reference times its Triton launches with torch.profiler and CUDA events in
+ * scripts/step_profile.py:29-47 and scripts/profile_kernels.py:115-144).
+ *
+ * dil_timing_enable(1) makes every later launch of the entry points above
+ * record a pair of hipEvents on its stream; dil_timing_count() /
+ * dil_timing_read() wait for those events and report, per kernel name, the
+ * number of launches and the summed event-to-event milliseconds since the
+ * last dil_timing_reset().  Off by default.
+ */
+int dil_timing_enable(int on);
+int dil_timing_reset(void);
+int dil_timing_count(void);
+int dil_timing_read(int index, char* name, int name_capacity, double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif
