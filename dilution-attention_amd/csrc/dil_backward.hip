@@ -169,13 +169,23 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
   };
   constexpr int kSteps = kTileQ / Mma<CT>::kStep;
 
+  // demand checkpoint of this lane's key at query tile qt, loaded one tile ahead
+  auto carry_at = [&](int qt) -> float {
+    return (active && qt >= kb && key < P.T) ? P.carry[(slice * P.nb + qt) * P.T + key] : 0.f;
+  };
+  float cin_next = carry_at(nq - 1);
+
   fetch(nq - 1);
   stash(0);
   __syncthreads();
   int it = 0;
   for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
     const int buf = it & 1;
-    if (qt - 1 >= kb0) fetch(qt - 1);
+    const float cin = cin_next;
+    if (qt - 1 >= kb0) {
+      fetch(qt - 1);
+      cin_next = carry_at(qt - 1);
+    }
     if (active && qt >= kb) {
       const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
       const float* st = st_s[buf];
@@ -191,7 +201,6 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
         if (diag && key > row0 + r) p[i] = 0.f;
         x[i] = p[i];
       }
-      const float cin = key < P.T ? P.carry[(slice * P.nb + qt) * P.T + key] : 0.f;
       column_scan_inclusive(x, cin + kEps, h);
       float inv[16], w[16];
 #pragma unroll
@@ -304,6 +313,12 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
   for (int t = 0; t < kDTiles<D>; ++t) dqa[t] = floatx16{};
   const float* crow = P.carry + (slice * P.nb + qt) * P.T;
   const float* srow = P.sufk + (slice * P.nb + qt) * P.T;
+  // demand and suffix checkpoints of this lane's key, loaded one key tile ahead
+  auto ckpt_at = [&](int kt, const float* row) -> float {
+    const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
+    return (kt < nkt_w && key < P.T) ? row[key] : 0.f;
+  };
+  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
 
   KTileLoader<CT, D> kl, vl;
   TTileLoader<CT, D> ktl;
@@ -316,11 +331,14 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
   __syncthreads();
   for (int kt = 0; kt < nkt_wg; ++kt) {
     const int buf = kt & 1;
+    const float cin = cin_next, sin = sin_next;
     if (kt + 1 < nkt_wg) {
       const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
       kl.load(ks, key0n, P.T);
       vl.load(vs, key0n, P.T);
       ktl.load(kts, P.t_pad, key0n);
+      cin_next = ckpt_at(kt + 1, crow);
+      sin_next = ckpt_at(kt + 1, srow);
     }
     if (kt < nkt_w) {
       const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);   // key owned by this lane
@@ -335,8 +353,7 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
         if (diag && key > r0 + perm_row(i, h)) p[i] = 0.f;
         x[i] = p[i];
       }
-      const bool kok = key < P.T;
-      column_scan_inclusive(x, (kok ? crow[key] : 0.f) + kEps, h);
+      column_scan_inclusive(x, cin + kEps, h);
       float inv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) inv[i] = fast_rcp(x[i]);
@@ -350,7 +367,7 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
         tq[i] = p[i] * inv[i] * inv[i];
         x[i] = -ds[i] * tq[i];
       }
-      column_scan_suffix_exclusive(x, kok ? srow[key] : 0.f, h);
+      column_scan_suffix_exclusive(x, sin, h);
       float w[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {

@@ -27,6 +27,8 @@
 #include "dil_internal.hpp"
 #include "dil_tiles.hpp"
 
+#include <type_traits>
+
 namespace dil {
 
 namespace {
@@ -56,10 +58,44 @@ struct FwdParams {
 };
 
 // ---------------------------------------------------------------------------
-// row statistics + block column sums
+// Per-wave tile bounds.  A wave owns query rows [r0, r0 + 32) of the chunk
+// (absolute rows qa0 = q0 + r0 ...).  Key tile kt (keys [32 kt, 32 kt + 32))
+// needs no causal mask when kt < kfull and contributes nothing when
+// kt >= kend.
+
+struct WaveRows {
+  int64_t r0, qa0;
+  int kfull, kend;
+  bool on;
+};
+
+__device__ __forceinline__ WaveRows wave_rows(const FwdParams& P, int g, int wave) {
+  WaveRows w;
+  w.r0 = (static_cast<int64_t>(g) * 4 + wave) * kTileQ;
+  w.qa0 = P.q0 + w.r0;
+  w.on = w.r0 < P.C;
+  const int64_t qlast = min(w.qa0 + kTileQ - 1, P.q0 + P.C - 1);
+  w.kend = w.on ? static_cast<int>(qlast / kTileK) + 1 : 0;
+  w.kfull = w.on ? static_cast<int>((w.qa0 + 1) / kTileK) : 0;
+  return w;
+}
+
+// Key tiles the workgroup (4 consecutive row tiles of group g) has to stage.
+__device__ __forceinline__ int group_key_tiles(const FwdParams& P, int g) {
+  const int64_t qlast = min(P.q0 + (static_cast<int64_t>(g) * 4 + 4) * kTileQ - 1, P.q0 + P.C - 1);
+  return static_cast<int>(qlast / kTileK) + 1;
+}
+
+// Running maximum moves only when a tile exceeds it by this much (in units
+// of the scaled log2 affinity), so the rescaling of the sums is rare; the
+// terms 2^(a - m) then stay below 2^8.
+constexpr float kLazyMax = 8.f;
+
+// ---------------------------------------------------------------------------
+// row statistics (+ pk) and per-32-row-block column sums of p
 
 template <typename CT, int D, bool PK>
-__global__ __launch_bounds__(kThreads) void fwd_stats(FwdParams P) {
+__global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   using T = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
   __shared__ __attribute__((aligned(16))) CT kttile[PK ? 2 : 1][PK ? D * T::kTStride : 1];
@@ -68,32 +104,86 @@ __global__ __launch_bounds__(kThreads) void fwd_stats(FwdParams P) {
   const int64_t slice = blockIdx.y;
   const int g = gridDim.x - 1 - blockIdx.x;            // heavy (late) row groups first
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const int64_t r0 = (static_cast<int64_t>(g) * 4 + wave) * kTileQ;   // first row of this wave (chunk-relative)
-  const int64_t qa0 = P.q0 + r0;                                     // absolute index of that row
-  const int64_t wg_last = min(P.q0 + (static_cast<int64_t>(g) * 4 + 4) * kTileQ, P.Tk);  // keys < wg_last
-  const int nkt_wg = static_cast<int>((wg_last + kTileK - 1) / kTileK);
-  const int64_t w_last = min(qa0 + kTileQ, P.Tk);
-  const int nkt_w = r0 < P.C ? static_cast<int>((w_last + kTileK - 1) / kTileK) : 0;
+  const WaveRows W = wave_rows(P, g, wave);
+  const int nkt_wg = group_key_tiles(P, g);
 
   const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
   const CT* ks = static_cast<const CT*>(P.k) + slice * P.k_sn;
   const CT* kts = PK ? static_cast<const CT*>(P.kt) + slice * P.t_sn : nullptr;
 
+  // Q rows in natural order: the B operand of sweep 1 (lane <-> query) and the
+  // A operand of sweep 2 (register rows <-> queries)
   RowFrag<CT, D> qf;
-  if (r0 + l32 < P.C) load_row_frag<CT, D>(qf, qs + (r0 + l32) * D + h * (D / 2));
+  const bool row_ok = W.r0 + l32 < P.C;
+  if (row_ok) load_row_frag<CT, D>(qf, qs + (W.r0 + l32) * D + h * (D / 2));
   else zero_row_frag<CT, D>(qf);
-  const int64_t my_q = qa0 + l32;   // query owned by this lane in sweep 1
+  const int my_q = static_cast<int>(W.qa0) + l32;      // query of this lane in sweep 1
 
   KTileLoader<CT, D> kl;
   TTileLoader<CT, D> tl;
 
-  // ---- sweep 1: S^T = K Q^T, one query per lane ----
-  float mraw = -INFINITY, lsum = 0.f;
+  // ---- sweep 1: S^T = K Q^T (lane <-> query, registers <-> keys) ----
+  // m: the offset the sums are taken against (moves lazily); mx: exact max
+  float m = -INFINITY, mx = -INFINITY, l0 = 0.f, l1 = 0.f;
   floatx16 pka[PK ? kDTiles<D> : 1];
   if constexpr (PK) {
 #pragma unroll
     for (int t = 0; t < kDTiles<D>; ++t) pka[t] = floatx16{};
   }
+  const float thresh = kLazyMax / P.c;                 // in raw score units
+  auto stats_step = [&](int kt, int buf, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> kf;
+    lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
+    const floatx16 acc = mma_rows<CT, D>(kf, qf, floatx16{});
+    float a[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a[i] = acc[i];
+    if constexpr (DIAG) {
+      const int dq = kt * kTileK + 8 * h - my_q;       // key - query for register i: perm_row(i, 0) + dq
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (16 * (i >> 3) + (i & 7) + dq > 0) a[i] = -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(a[0], a[1]), a[2]);
+#pragma unroll
+    for (int i = 3; i < 15; i += 2) tmax = fmaxf(fmaxf(tmax, a[i]), a[i + 1]);
+    tmax = fmaxf(tmax, a[15]);
+    const HalfPair tp = halves(tmax);                  // one running max per query (both halves)
+    tmax = fmaxf(tp.lo, tp.hi);
+    mx = fmaxf(mx, tmax);
+    const bool take = tmax > m + thresh;
+    if (__any(take)) {
+      const float mnew = take ? tmax : m;
+      const float alpha = take ? (m == -INFINITY ? 0.f : fast_exp2((m - mnew) * P.c)) : 1.f;
+      l0 *= alpha;
+      l1 *= alpha;
+      if constexpr (PK) {
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t) pka[t] *= alpha;
+      }
+      m = mnew;
+    }
+    const float mc = m * P.c;
+    float e[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) e[i] = fast_exp2(fmaf(a[i], P.c, -mc));
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      l0 += e[i];
+      l1 += e[i + 1];
+    }
+    if constexpr (PK) {
+#pragma unroll
+      for (int s = 0; s < kTileK / Mma<CT>::kStep; ++s) {
+        const auto bfr = acc_frag<CT>(e, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          pka[t] = Mma<CT>::mma(lds_t_frag<CT, D>(kttile[buf], 32 * t + l32, h, s), bfr, pka[t]);
+      }
+    }
+  };
+
   kl.load(ks, 0, P.Tk);
   if constexpr (PK) tl.load(kts, P.tk_pad, 0);
   kl.store(ktile[0]);
@@ -105,74 +195,27 @@ __global__ __launch_bounds__(kThreads) void fwd_stats(FwdParams P) {
       kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
       if constexpr (PK) tl.load(kts, P.tk_pad, static_cast<int64_t>(kt + 1) * kTileK);
     }
-    if (kt < nkt_w) {
-      RowFrag<CT, D> kf;
-      lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
-      floatx16 acc = mma_rows<CT, D>(kf, qf, floatx16{});
-      float a[16];
-      const int64_t key0 = static_cast<int64_t>(kt) * kTileK;
-      const bool diag = key0 + kTileK - 1 > qa0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        a[i] = acc[i];
-        if (diag && key0 + perm_row(i, h) > my_q) a[i] = -INFINITY;
-      }
-      float tmax = a[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, a[i]);
-      float mnew = fmaxf(mraw, tmax);
-      if constexpr (PK) mnew = fmaxf(mnew, partner32(mnew));
-      const float msafe = (mnew == -INFINITY) ? 0.f : mnew;
-      const float alpha = (mraw == -INFINITY) ? 0.f : fast_exp2((mraw - msafe) * P.c);
-      const float mc = msafe * P.c;
-      float e[16];
-      float add = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        e[i] = fast_exp2(fmaf(a[i], P.c, -mc));
-        add += e[i];
-      }
-      lsum = fmaf(lsum, alpha, add);
-      if constexpr (PK) {
-        // rescale only when some lane's maximum moved
-        if (__any(alpha != 1.f)) {
-#pragma unroll
-          for (int t = 0; t < kDTiles<D>; ++t) pka[t] *= alpha;
-        }
-#pragma unroll
-        for (int s = 0; s < kTileK / Mma<CT>::kStep; ++s) {
-          const auto bfr = acc_frag<CT>(e, s);
-#pragma unroll
-          for (int t = 0; t < kDTiles<D>; ++t)
-            pka[t] = Mma<CT>::mma(lds_t_frag<CT, D>(kttile[buf], 32 * t + l32, h, s), bfr, pka[t]);
-        }
-      }
-      mraw = mnew;
-    }
+    if (kt < W.kfull) stats_step(kt, buf, std::false_type{});
+    else if (kt < W.kend) stats_step(kt, buf, std::true_type{});
     if (kt + 1 < nkt_wg) {
       kl.store(ktile[buf ^ 1]);
       if constexpr (PK) tl.store(kttile[buf ^ 1]);
     }
     __syncthreads();
   }
-  // combine the two lane halves (different keys, same query)
-  const float pm = partner32(mraw), pl = partner32(lsum);
-  const float mtot = fmaxf(mraw, pm);
-  const float mts = (mtot == -INFINITY) ? 0.f : mtot;
-  const float ltot = (mraw == -INFINITY ? 0.f : lsum * fast_exp2((mraw - mts) * P.c)) +
-                     (pm == -INFINITY ? 0.f : pl * fast_exp2((pm - mts) * P.c));
-  const bool row_ok = r0 + l32 < P.C;
-  const float rmax_v = mtot * P.c;
+  const HalfPair lp = halves(l0 + l1);                 // the halves share m
+  // re-reference the sum to the exact row maximum: p = 2^(a c - rmax) / rden
+  const float ltot = (lp.lo + lp.hi) * fast_exp2((m - mx) * P.c);
+  const float rmax_v = mx * P.c;
   if (h == 0 && row_ok) {
-    P.rmax[slice * P.C + r0 + l32] = rmax_v;
-    P.rden[slice * P.C + r0 + l32] = ltot;
+    P.rmax[slice * P.C + W.r0 + l32] = rmax_v;
+    P.rden[slice * P.C + W.r0 + l32] = ltot;
   }
   if (h == 0) lse_s[wave][l32] = row_ok ? rmax_v + __log2f(ltot) : INFINITY;
   if constexpr (PK) {
-    // halves share the running max, so pka holds the full sum over keys
     if (row_ok) {
-      const float f = P.scale / ltot;
-      float* dst = P.pk + (slice * P.C + r0 + l32) * D;
+      const float f = P.scale / (lp.lo + lp.hi);      // pk was accumulated against m
+      float* dst = P.pk + (slice * P.C + W.r0 + l32) * D;
 #pragma unroll
       for (int t = 0; t < kDTiles<D>; ++t)
 #pragma unroll
@@ -182,33 +225,42 @@ __global__ __launch_bounds__(kThreads) void fwd_stats(FwdParams P) {
   }
   __syncthreads();
 
-  // ---- sweep 2: S = Q K^T, one key per lane: block column sums of p ----
+  // ---- sweep 2: S = Q K^T (lane <-> key): per-block column sums of p ----
   float lse[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) lse[i] = lse_s[wave][acc_row(i, h)];
-  float* sblk = P.carry + (slice * P.nb + r0 / kTileQ) * P.Tk;
+  float* sblk = P.carry + (slice * P.nb + W.r0 / kTileQ) * P.Tk;
+  auto colsum_step = [&](int kt, int buf, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> kf;
+    lds_row_frag<CT, D>(kf, ktile[buf], l32, h);
+    const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float p[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
+    const int key = kt * kTileK + l32;
+    if constexpr (DIAG) {
+      const int dq = key - static_cast<int>(W.qa0) - 4 * h;   // key - query of register i: dq - (8 (i>>2) + (i&3))
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dq > 8 * (i >> 2) + (i & 3)) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] += p[i + 8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] += p[i + 4];
+    const float cs = (p[0] + p[1]) + (p[2] + p[3]);
+    const HalfPair cp = halves(cs);
+    if (h == 0 && key < P.Tk) sblk[key] = cp.lo + cp.hi;
+  };
   kl.load(ks, 0, P.Tk);
   kl.store(ktile[0]);
   __syncthreads();
   for (int kt = 0; kt < nkt_wg; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nkt_wg) kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
-    if (kt < nkt_w) {
-      RowFrag<CT, D> kf;
-      lds_row_frag<CT, D>(kf, ktile[buf], l32, h);
-      floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
-      const int64_t key = static_cast<int64_t>(kt) * kTileK + l32;
-      const bool diag = static_cast<int64_t>(kt) * kTileK + kTileK - 1 > qa0;
-      float cs = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float p = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
-        if (diag && key > qa0 + acc_row(i, h)) p = 0.f;
-        cs += p;
-      }
-      cs += partner32(cs);
-      if (h == 0 && key < P.Tk) sblk[key] = cs;
-    }
+    if (kt < W.kfull) colsum_step(kt, buf, std::false_type{});
+    else if (kt < W.kend) colsum_step(kt, buf, std::true_type{});
     if (kt + 1 < nkt_wg) kl.store(ktile[buf ^ 1]);
     __syncthreads();
   }
@@ -216,6 +268,8 @@ __global__ __launch_bounds__(kThreads) void fwd_stats(FwdParams P) {
 
 // ---------------------------------------------------------------------------
 // exclusive scan of block column sums -> carry checkpoints, totals
+
+constexpr int kScanBatch = 8;
 
 __global__ __launch_bounds__(256) void fwd_scan(float* __restrict__ carry, int64_t nb, int64_t Tk,
                                                 int64_t q0, int64_t C,
@@ -226,13 +280,22 @@ __global__ __launch_bounds__(256) void fwd_scan(float* __restrict__ carry, int64
   if (j >= Tk) return;
   double run = (demand_in != nullptr && j < q0) ? static_cast<double>(demand_in[slice * din_sn + j]) : 0.0;
   float* col = carry + slice * nb * Tk + j;
-  for (int64_t b = 0; b < nb; ++b) {
-    // block b covers rows [q0 + 32 b, q0 + 32 b + 32); keys at or beyond its
-    // end were not written by fwd_stats (their sum is zero by causality)
-    const bool written = j < q0 + 32 * (b + 1) && 32 * b < C;
-    const float s = written ? col[b * Tk] : 0.f;
-    col[b * Tk] = static_cast<float>(run);
-    run += static_cast<double>(s);
+  // block b covers rows [q0 + 32 b, q0 + 32 b + 32); keys at or beyond its end
+  // were not written by fwd_stats (their sum is zero by causality)
+  for (int64_t b0 = 0; b0 < nb; b0 += kScanBatch) {
+    float s[kScanBatch];
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const int64_t b = b0 + u;
+      const bool written = b < nb && j < q0 + 32 * (b + 1) && 32 * b < C;
+      s[u] = written ? col[b * Tk] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const int64_t b = b0 + u;
+      if (b < nb) col[b * Tk] = static_cast<float>(run);
+      run += static_cast<double>(s[u]);
+    }
   }
   total[slice * tot_sn + j] = static_cast<float>(run);
 }
@@ -241,7 +304,7 @@ __global__ __launch_bounds__(256) void fwd_scan(float* __restrict__ carry, int64
 // output pass
 
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void fwd_out(FwdParams P) {
+__global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   using T = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
   __shared__ __attribute__((aligned(16))) CT vttile[2][D * T::kTStride];
@@ -250,38 +313,84 @@ __global__ __launch_bounds__(kThreads) void fwd_out(FwdParams P) {
   const int64_t slice = blockIdx.y;
   const int g = gridDim.x - 1 - blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const int64_t r0 = (static_cast<int64_t>(g) * 4 + wave) * kTileQ;
-  const int64_t qa0 = P.q0 + r0;
-  const int64_t wg_last = min(P.q0 + (static_cast<int64_t>(g) * 4 + 4) * kTileQ, P.Tk);
-  const int nkt_wg = static_cast<int>((wg_last + kTileK - 1) / kTileK);
-  const int64_t w_last = min(qa0 + kTileQ, P.Tk);
-  const int nkt_w = r0 < P.C ? static_cast<int>((w_last + kTileK - 1) / kTileK) : 0;
+  const float hf = static_cast<float>(h);
+  const WaveRows W = wave_rows(P, g, wave);
+  const int nkt_wg = group_key_tiles(P, g);
 
   const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
   const CT* ks = static_cast<const CT*>(P.k) + slice * P.k_sn;
   const CT* vts = static_cast<const CT*>(P.vt) + slice * P.t_sn;
 
-  // Q rows loaded rho-permuted: accumulator register i of half h <-> row perm_row(i, h)
+  // Q rows in QS order: accumulator register i of half h <-> row 16 h + i
   RowFrag<CT, D> qf;
-  const int64_t my_row = r0 + rho(l32);
+  const int64_t my_row = W.r0 + qsig(l32);
   if (my_row < P.C) load_row_frag<CT, D>(qf, qs + my_row * D + h * (D / 2));
   else zero_row_frag<CT, D>(qf);
 
-  float lse[16], rsum[16];
+  float lse[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int64_t r = r0 + perm_row(i, h);
+    const int64_t r = W.r0 + 16 * h + i;
     lse[i] = (r < P.C) ? P.rmax[slice * P.C + r] + __log2f(P.rden[slice * P.C + r]) : INFINITY;
-    rsum[i] = 0.f;
   }
   constexpr int kSteps = kTileK / Mma<CT>::kStep;
   typename Mma<CT>::frag ident[kSteps];
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) ident[s] = ident_frag<CT>(l32, h, s);
+  for (int s = 0; s < kSteps; ++s) ident[s] = ident_qs<CT>(l32, h, s);
   floatx16 o[kDTiles<D>];
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) o[t] = floatx16{};
-  const float* crow = P.carry + (slice * P.nb + r0 / kTileQ) * P.Tk;
+  float rs = 0.f;     // row sum of shares for query l32 over this half's keys
+
+  const float* crow = P.carry + (slice * P.nb + W.r0 / kTileQ) * P.Tk;
+  // demand checkpoint of this lane's key, loaded one key tile ahead
+  auto carry_at = [&](int kt) -> float {
+    const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
+    return (kt < W.kend && key < P.Tk) ? crow[key] : 0.f;
+  };
+  float cin_next = carry_at(0);
+
+  auto out_step = [&](int kt, int buf, float cin, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> kf;
+    lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
+    const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float p[16], x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
+    if constexpr (DIAG) {
+      const int dk = kt * kTileK + rho(l32) - static_cast<int>(W.qa0) - 16 * h;   // key - query(i) = dk - i
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dk > i) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = p[i];
+    scan_incl_qs(x, cin + kEps, hf);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] *= fast_rcp(x[i]);     // share
+    // transpose the share tile: queries in lanes, keys (natural order) in registers
+    floatx16 xt = floatx16{};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(p, s), ident[s], xt);
+    float xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = xt[i];
+    float r0s = 0.f, r1s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      r0s += xv[i];
+      r1s += xv[i + 1];
+    }
+    rs += r0s + r1s;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto af = acc_frag<CT>(xv, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        o[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(vttile[buf], 32 * t + l32, h, s), o[t]);
+    }
+  };
 
   KTileLoader<CT, D> kl;
   TTileLoader<CT, D> vl;
@@ -292,47 +401,14 @@ __global__ __launch_bounds__(kThreads) void fwd_out(FwdParams P) {
   __syncthreads();
   for (int kt = 0; kt < nkt_wg; ++kt) {
     const int buf = kt & 1;
+    const float cin = cin_next;
     if (kt + 1 < nkt_wg) {
       kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
       vl.load(vts, P.tk_pad, static_cast<int64_t>(kt + 1) * kTileK);
+      cin_next = carry_at(kt + 1);
     }
-    if (kt < nkt_w) {
-      const int64_t key0 = static_cast<int64_t>(kt) * kTileK;
-      const int64_t key = key0 + rho(l32);          // key owned by this lane
-      RowFrag<CT, D> kf;
-      lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
-      floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
-      const bool diag = key0 + kTileK - 1 > qa0;
-      float p[16], x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[i] = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
-        if (diag && key > qa0 + perm_row(i, h)) p[i] = 0.f;
-        x[i] = p[i];
-      }
-      const float cin = (key < P.Tk) ? crow[key] : 0.f;
-      column_scan_inclusive(x, cin + kEps, h);
-      float sh[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sh[i] = p[i] * fast_rcp(x[i]);
-        rsum[i] += sh[i];
-      }
-      // transpose the share tile: X[key][query] with queries in lanes
-      floatx16 xt = floatx16{};
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(sh, s), ident[s], xt);
-      float xv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xv[i] = xt[i];
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const auto af = acc_frag<CT>(xv, s);
-#pragma unroll
-        for (int t = 0; t < kDTiles<D>; ++t)
-          o[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(vttile[buf], 32 * t + l32, h, s), o[t]);
-      }
-    }
+    if (kt < W.kfull) out_step(kt, buf, cin, std::false_type{});
+    else if (kt < W.kend) out_step(kt, buf, cin, std::true_type{});
     if (kt + 1 < nkt_wg) {
       kl.store(ktile[buf ^ 1]);
       vl.store(vttile[buf ^ 1]);
@@ -340,33 +416,23 @@ __global__ __launch_bounds__(kThreads) void fwd_out(FwdParams P) {
     __syncthreads();
   }
 
-  // row sums: reduce over the 32 lanes of each half (keys), then publish
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float v = rsum[i];
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 64);
-    rsum[i] = v;
-  }
-  if (l32 == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ssum_s[wave][perm_row(i, h)] = rsum[i];
-  }
+  // row sums: the two halves hold disjoint keys of the same query
+  const HalfPair rp = halves(rs);
+  if (h == 0) ssum_s[wave][l32] = rp.lo + rp.hi;
   __syncthreads();
-  if (h == 0 && r0 + l32 < P.C) P.ssum[slice * P.C + r0 + l32] = ssum_s[wave][l32];
+  if (h == 0 && W.r0 + l32 < P.C) P.ssum[slice * P.C + W.r0 + l32] = ssum_s[wave][l32];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = acc_row(i, h);
-    if (r0 + row < P.C) {
+    if (W.r0 + row < P.C) {
       const float inv = 1.f / (ssum_s[wave][row] + kEps);
-      float* dst = P.out + slice * P.o_sn + (r0 + row) * D;
+      float* dst = P.out + slice * P.o_sn + (W.r0 + row) * D;
 #pragma unroll
       for (int t = 0; t < kDTiles<D>; ++t)
         if (32 * t + l32 < D) dst[32 * t + l32] = o[t][i] * inv;
     }
   }
 }
-
 // ---------------------------------------------------------------------------
 // host side
 

@@ -167,6 +167,81 @@ __device__ __forceinline__ typename Mma<CT>::frag ident_frag(int l32, int h, int
   }
 }
 
+// ---------------------------------------------------------------------------
+// Query-split tile layout ("QS")
+//
+// A score tile S = Q K^T whose A operand (Q) is loaded with lane m holding
+// query row qsig(m) puts, in accumulator register i of lane half h, the query
+// 16 h + i: half 0 holds rows 0..15 and half 1 rows 16..31, each in register
+// order.  A column (one key per lane) then scans down its 32 rows as one
+// 16-long register chain per half plus one exchange between the halves.
+// Contracting over those rows (dv += dO^T A, dk += Q^T (p dp)) uses operand
+// k slots 16 h + 8 s + [0, 8) (bf16) or 16 h + s (fp32) of a transposed tile.
+
+__device__ __forceinline__ int qsig(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+
+// Values of x in the two lanes of the pair (l & 31, (l & 31) + 32), in every
+// lane of the pair: .lo from the lower-half lane, .hi from the upper-half lane.
+struct HalfPair {
+  float lo, hi;
+};
+__device__ __forceinline__ HalfPair halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return HalfPair{__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+
+// Operand fragment over 32 QS-ordered rows of a transposed LDS tile
+// ([D][kTStride]); lane supplies row r of the D dimension.
+template <typename CT, int D>
+__device__ __forceinline__ typename Mma<CT>::frag lds_tq_frag(const CT* lds, int r, int h, int s) {
+  if (D < 32 && r >= D) return typename Mma<CT>::frag{};
+  const CT* row = lds + r * Tiles<CT, D>::kTStride;
+  if constexpr (sizeof(CT) == 2) {
+    return *reinterpret_cast<const bf16x8*>(row + 16 * h + 8 * s);
+  } else {
+    return row[16 * h + s];
+  }
+}
+
+// Identity operand that transposes a QS-layout tile: B[k][n] = 1 where the
+// query held in k slot k equals n = lane & 31.
+template <typename CT>
+__device__ __forceinline__ typename Mma<CT>::frag ident_qs(int l32, int h, int s) {
+  if constexpr (sizeof(CT) == 2) {
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = (16 * h + 8 * s + t == l32) ? 1.f : 0.f;
+    return Mma<CT>::pack(v);
+  } else {
+    return (16 * h + s == l32) ? 1.f : 0.f;
+  }
+}
+
+// Inclusive column scan of a QS-layout tile: x[i] becomes base + the sum of
+// the column's entries at rows <= 16 h + i.  hf = float(h).  Returns the
+// column total (excluding base).
+__device__ __forceinline__ float scan_incl_qs(float (&x)[16], float base, float hf) {
+#pragma unroll
+  for (int t = 1; t < 16; ++t) x[t] += x[t - 1];
+  const HalfPair tot = halves(x[15]);
+  const float off = fmaf(hf, tot.lo, base);
+#pragma unroll
+  for (int t = 0; t < 16; ++t) x[t] += off;
+  return tot.lo + tot.hi;
+}
+
+// Inclusive suffix scan of a QS-layout tile: x[i] becomes base + the sum of
+// the column's entries at rows >= 16 h + i.  Returns the column total.
+__device__ __forceinline__ float scan_suffix_qs(float (&x)[16], float base, float hf) {
+#pragma unroll
+  for (int t = 14; t >= 0; --t) x[t] += x[t + 1];
+  const HalfPair tot = halves(x[0]);
+  const float off = fmaf(1.f - hf, tot.hi, base);
+#pragma unroll
+  for (int t = 0; t < 16; ++t) x[t] += off;
+  return tot.lo + tot.hi;
+}
+
 // Column scan over the 32 rows of an accumulator tile in the permuted layout
 // (register i of half h = row 16*(i>>3) + 8*h + (i&7)).  On return x[i] holds
 // base + sum of the column's entries at rows <= row(i): the inclusive demand
