@@ -42,6 +42,8 @@ struct BwdParams {
   const void* kt;
   const void* dot;
   int64_t T, t_pad, nb;
+  int64_t n;          // slices
+  int kgroups;        // 128-row (or 128-key) groups per slice
   float c, scale;
   const float* lse;   // (n, T)
   const float* sinv;
@@ -119,9 +121,11 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
   __shared__ float st_s[2][3 * kTileQ];   // lse, sinv, dbar
 
-  const int64_t slice = blockIdx.y;
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const int kb0 = blockIdx.x * 4;
+  const int kb0 = item.idx * 4;
   const int kb = kb0 + wave;                     // key tile of this wave
   const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
   const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
@@ -271,8 +275,10 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
   __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
   __shared__ float g_s[4][kTileQ];
 
-  const int64_t slice = blockIdx.y;
-  const int g = gridDim.x - 1 - blockIdx.x;            // heavy (late) row groups first
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int g = item.idx;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const int qt = g * 4 + wave;
   const int64_t r0 = static_cast<int64_t>(qt) * kTileQ;
@@ -436,9 +442,11 @@ __global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ float st_s[2][3 * kTileQ];   // lse, ghat, (unused)
 
-  const int64_t slice = blockIdx.y;
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const int kb0 = blockIdx.x * 4;
+  const int kb0 = item.idx * 4;
   const int kb = kb0 + wave;
   const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
   const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
@@ -624,7 +632,9 @@ int launch_backward(const BackwardArgs& a) {
             bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
                 a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbar, rows));
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
-  const dim3 gkey(static_cast<unsigned>((nkt + 3) / 4), n);
+  P.n = a.n;
+  P.kgroups = (nkt + 3) / 4;
+  const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("bwd_query", st, bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("bwd_dkcorr", st, bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P));

@@ -42,6 +42,8 @@ struct FwdParams {
   const void* kt;         // CT (n, D, Tk_pad) or null
   int64_t t_sn, tk_pad;
   int64_t C, Tk, q0, nb;
+  int64_t n;              // slices
+  int groups;             // 128-row groups per slice
   float c;                // log2(e) / sqrt(D)
   float scale;            // 1 / sqrt(D)
   float* out;
@@ -101,8 +103,10 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   __shared__ __attribute__((aligned(16))) CT kttile[PK ? 2 : 1][PK ? D * T::kTStride : 1];
   __shared__ float lse_s[4][kTileQ];
 
-  const int64_t slice = blockIdx.y;
-  const int g = gridDim.x - 1 - blockIdx.x;            // heavy (late) row groups first
+  const WorkItem item = xcd_work_item(P.groups, P.n, true);   // heavy (late) row groups first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int g = item.idx;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const WaveRows W = wave_rows(P, g, wave);
   const int nkt_wg = group_key_tiles(P, g);
@@ -304,14 +308,16 @@ __global__ __launch_bounds__(256) void fwd_scan(float* __restrict__ carry, int64
 // output pass
 
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
+__global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) void fwd_out(FwdParams P) {
   using T = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
   __shared__ __attribute__((aligned(16))) CT vttile[2][D * T::kTStride];
   __shared__ float ssum_s[4][kTileQ];
 
-  const int64_t slice = blockIdx.y;
-  const int g = gridDim.x - 1 - blockIdx.x;
+  const WorkItem item = xcd_work_item(P.groups, P.n, true);
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int g = item.idx;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const float hf = static_cast<float>(h);
   const WaveRows W = wave_rows(P, g, wave);
@@ -327,11 +333,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   if (my_row < P.C) load_row_frag<CT, D>(qf, qs + my_row * D + h * (D / 2));
   else zero_row_frag<CT, D>(qf);
 
-  float lse[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t r = W.r0 + 16 * h + i;
-    lse[i] = (r < P.C) ? P.rmax[slice * P.C + r] + __log2f(P.rden[slice * P.C + r]) : INFINITY;
+  // log2-sum-exp of this wave's rows, read from LDS at every tile (keeps
+  // registers for occupancy)
+  __shared__ __attribute__((aligned(16))) float lse_s[4][kTileQ];
+  if (h == 0) {
+    const int64_t r = W.r0 + l32;
+    lse_s[wave][l32] = (r < P.C) ? P.rmax[slice * P.C + r] + __log2f(P.rden[slice * P.C + r]) : INFINITY;
   }
   constexpr int kSteps = kTileK / Mma<CT>::kStep;
   typename Mma<CT>::frag ident[kSteps];
@@ -355,6 +362,15 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
     RowFrag<CT, D> kf;
     lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
     const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float lse[16];
+    {
+      const floatx4* lp = reinterpret_cast<const floatx4*>(&lse_s[wave][16 * h]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const floatx4 v = lp[u];
+        lse[4 * u] = v[0]; lse[4 * u + 1] = v[1]; lse[4 * u + 2] = v[2]; lse[4 * u + 3] = v[3];
+      }
+    }
     float p[16], x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
@@ -510,7 +526,9 @@ int launch_forward(const ForwardArgs& a) {
   P.tot_sn = a.tot_sn;
   P.pk = a.pk;
 
-  const dim3 grid(static_cast<unsigned>((a.C + 4 * kTileQ - 1) / (4 * kTileQ)), n);
+  P.n = a.n;
+  P.groups = static_cast<int>((a.C + 4 * kTileQ - 1) / (4 * kTileQ));
+  const dim3 grid(static_cast<unsigned>(xcd_grid(P.groups * a.n)));
   if (a.pk) DIL_TIMED("fwd_stats", st, fwd_stats<CT, D, true><<<grid, kThreads, 0, st>>>(P));
   else DIL_TIMED("fwd_stats", st, fwd_stats<CT, D, false><<<grid, kThreads, 0, st>>>(P));
   DIL_TIMED("fwd_scan", st,

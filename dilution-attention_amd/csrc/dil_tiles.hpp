@@ -168,6 +168,41 @@ __device__ __forceinline__ typename Mma<CT>::frag ident_frag(int l32, int h, int
 }
 
 // ---------------------------------------------------------------------------
+// XCD-aware work mapping.
+//
+// The dispatcher hands workgroups to the 8 XCDs of an MI355X round-robin by
+// linear workgroup id, and each XCD has its own L2.  Work item L of a 1-D
+// grid of kXcds * per workgroups goes to workgroup b with
+// L = (b % kXcds) * per + b / kXcds, so an XCD runs a contiguous range of
+// items: consecutive tiles of the same (batch, head) slice, whose K/V (or
+// Q/dO) streams then stay in that XCD's L2.
+
+constexpr int kXcds = 8;
+
+inline int64_t xcd_grid(int64_t items) { return kXcds * ((items + kXcds - 1) / kXcds); }
+
+struct WorkItem {
+  int64_t slice;
+  int idx;       // tile-group index within the slice, in dispatch order
+  bool valid;
+};
+
+// items = groups * slices.  The items of a slice are dispatched in order
+// idx = 0, 1, ...; `reverse` maps that order to groups - 1, ..., 0.
+__device__ __forceinline__ WorkItem xcd_work_item(int groups, int64_t slices, bool reverse) {
+  const int64_t total = static_cast<int64_t>(groups) * slices;
+  const int64_t per = (total + kXcds - 1) / kXcds;
+  const int64_t b = blockIdx.x;
+  const int64_t L = (b % kXcds) * per + b / kXcds;
+  WorkItem w;
+  w.valid = L < total;
+  w.slice = L / groups;
+  const int r = static_cast<int>(L % groups);
+  w.idx = reverse ? groups - 1 - r : r;
+  return w;
+}
+
+// ---------------------------------------------------------------------------
 // Query-split tile layout ("QS")
 //
 // A score tile S = Q K^T whose A operand (Q) is loaded with lane m holding
