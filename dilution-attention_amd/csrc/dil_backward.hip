@@ -2,32 +2,36 @@
 //
 // Reference behaviour: _DilutionAttentionFn.backward,
 // /root/reference/src/dilution/kernels.py:851-903, and the decomposition in
-// /root/reference/docs/kernels.md:62-84:
+// /root/reference/docs/kernels.md:62-84.  With s = 1/sqrt(d), C the inclusive
+// column demand (c + p) and S the row sum of shares:
 //
-//   ds_ij    = (dO_i . v_j - dbar_i) / (S_i + eps),   dbar_i = dO_i . o_i
-//   inv_ij   = 1 / (c_ij + p_ij + eps)               (c: exclusive demand)
-//   dks_ij   = -ds_ij p_ij inv_ij^2                   (adjoint through the demand)
-//   suffix_ij = sum_{i' > i} dks_i'j                  (reverse column scan)
-//   dp_ij    = ds_ij (c_ij + eps) inv_ij^2 + suffix_ij = ds_ij (inv - p inv^2) + suffix_ij
-//   ghat_i   = sum_j p_ij dp_ij,   da_ij = p_ij (dp_ij - ghat_i)
-//   dq = s da K,   dk = s da^T Q,   dv = A^T dO
+//   ds_ij  = (dO_i . v_j - dO_i . o_i) / (S_i + eps) = (dO_i . v_j) sinv_i - dbs_i
+//   inv_ij = 1 / (C_ij + eps),   sh_ij = p_ij inv_ij
+//   g_ij   = ds_ij sh_ij inv_ij                  (adjoint flowing into the demand)
+//   G_ij   = sum_{i' >= i} g_i'j                 (inclusive reverse column scan)
+//   dp_ij  = ds_ij inv_ij - G_ij,   p dp = ds_ij sh_ij - p_ij G_ij
+//   ghat_i = sum_j (p dp)_ij,   da_ij = (p dp)_ij - p_ij ghat_i
+//   dq = s da K,   dk = s da^T Q,   dv = (sh sinv)^T dO
 //
-// Kernels (gfx950; deterministic, no atomics):
-//   bwd_rows   lse = rmax + log2 rden, 1/(S + eps), dbar per row.
-//   bwd_key    one wave per 32-key tile, query tiles of 32 walked in reverse:
-//              p, demand (checkpoint + in-tile scan), dv += A^T dO, ds from
-//              dO V^T, the running per-key suffix of dks (stored at every tile
-//              boundary), dk_main += (p dp)^T Q.  All products on MFMA with
-//              keys in lanes, so no operand needs a transposition.
-//   bwd_query  one wave per 32-row tile over the causal key tiles: the same
-//              chain with the suffix read from bwd_key's checkpoints; ghat as
-//              the row sum of p dp; (p dp) transposed by an identity MFMA so
-//              (p dp) @ K runs with queries in lanes; dq = s (p dp) K - ghat pk
-//              (pk = s p @ k saved by the forward).
-//   bwd_dkcorr one wave per key tile: dk = dk_main - s sum_i p_ij ghat_i q_i.
+// Kernels (gfx950, deterministic, no atomics; tiles in the query-split layout
+// of dil_tiles.hpp, causal diagonal tiles peeled out of the main loops):
+//   bwd_rows    per row: lse = rmax + log2 rden, sinv = 1/(S + eps),
+//               dbs = (dO . o) sinv.
+//   bwd_key     one wave per 32-key tile, query tiles walked in reverse:
+//               dv += (sh sinv)^T dO and dk_main += (p dp)^T Q on MFMA with
+//               keys in lanes; the running suffix G per key is stored at every
+//               tile boundary for bwd_query.
+//   bwd_query   one wave per 32-row tile over its causal key tiles: the same
+//               chain with G from the checkpoints; ghat = row sums of p dp;
+//               (p dp) transposed by an identity MFMA so dq += (p dp) K runs
+//               with queries in lanes; dq = s dq_main - ghat pk.
+//   prep_ghat_q (ghat * Q)^T tiles for the correction.
+//   bwd_dkcorr  one wave per key tile: dk = s dk_main - s sum_i p_ij (ghat_i q_i).
 #include "dil_common.hpp"
 #include "dil_internal.hpp"
 #include "dil_tiles.hpp"
+
+#include <type_traits>
 
 namespace dil {
 
@@ -41,17 +45,18 @@ struct BwdParams {
   const void* qt;     // CT (n, D, T_pad) transposed copies
   const void* kt;
   const void* dot;
+  const void* qgt;    // CT (n, D, T_pad): (ghat * q)^T
   int64_t T, t_pad, nb;
   int64_t n;          // slices
-  int kgroups;        // 128-row (or 128-key) groups per slice
+  int kgroups;        // groups of 4 tiles (128 keys or rows) per slice
   float c, scale;
   const float* lse;   // (n, T)
   const float* sinv;
-  const float* dbar;
+  const float* dbs;
   float* ghat;        // (n, T)
   const float* carry; // (n, nb, T)
   float* sufk;        // (n, nb, T)
-  float* dkm;         // (n, T, D) fp32: scale * sum_i (p dp)_ij q_i
+  float* dkm;         // (n, T, D) fp32: sum_i (p dp)_ij q_i
   const float* pk;    // (n, T, D)
   void* dq;
   void* dk;
@@ -68,7 +73,7 @@ __global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, i
                                                 const float* __restrict__ rmax,
                                                 const float* __restrict__ rden,
                                                 const float* __restrict__ ssum, float* __restrict__ lse,
-                                                float* __restrict__ sinv, float* __restrict__ dbar,
+                                                float* __restrict__ sinv, float* __restrict__ dbs,
                                                 int64_t rows) {
   constexpr int LPR = D / 8;                    // lanes per row, 8 elements each
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -85,46 +90,87 @@ __global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, i
 #pragma unroll
   for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
   if (row < rows && sub == 0) {
-    dbar[row] = acc;
+    const float si = 1.f / (ssum[row] + kEps);
     lse[row] = rmax[row] + __log2f(rden[row]);
-    sinv[row] = 1.f / (ssum[row] + kEps);
+    sinv[row] = si;
+    dbs[row] = acc * si;
   }
 }
 
-// Per-row statistics of one 32-row tile staged in LDS.
+// (ghat * q)^T in the compute type, zero-padded to t_pad columns.
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ q,
+                                                        const float* __restrict__ ghat, int64_t T,
+                                                        int64_t t_pad, CT* __restrict__ dst) {
+  __shared__ float tile[64][D + 1];
+  const int64_t slice = blockIdx.y;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+  for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
+    const int r = idx / D, c = idx % D;
+    const int64_t row = r0 + r;
+    tile[r][c] = row < T ? static_cast<float>(q[(slice * T + row) * D + c]) * ghat[slice * T + row] : 0.f;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
+    const int c = idx / 64, r = idx % 64;
+    dst[(slice * D + c) * t_pad + r0 + r] = static_cast<CT>(tile[r][c]);
+  }
+}
+
+// Per-row statistics of one 32-row tile staged in LDS: up to three arrays of
+// 32 floats (rows past the end: the first array reads +inf, so p = 0).
+template <int NARR>
 struct RowStatsLoader {
   float r;
   __device__ void load(const float* a, const float* b, const float* c, int64_t row0, int64_t T) {
     const int t = threadIdx.x;
     r = 0.f;
-    if (t < 3 * kTileQ) {
+    if (t < NARR * kTileQ) {
       const float* src = t < kTileQ ? a : (t < 2 * kTileQ ? b : c);
       const int64_t row = row0 + (t % kTileQ);
-      // rows past the end: lse = +inf makes p = 0
       r = row < T ? src[row] : (t < kTileQ ? INFINITY : 0.f);
     }
   }
   __device__ void store(float* lds) const {
-    if (threadIdx.x < 3 * kTileQ) lds[threadIdx.x] = r;
+    if (threadIdx.x < NARR * kTileQ) lds[threadIdx.x] = r;
   }
 };
 
-// ---------------------------------------------------------------------------
-// key-parallel reverse pass
+// 16 consecutive floats of LDS into registers (four 16-byte reads).
+__device__ __forceinline__ void lds_read16(const float* src, float (&v)[16]) {
+  const floatx4* p = reinterpret_cast<const floatx4*>(src);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const floatx4 x = p[u];
+    v[4 * u] = x[0];
+    v[4 * u + 1] = x[1];
+    v[4 * u + 2] = x[2];
+    v[4 * u + 3] = x[3];
+  }
+}
 
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
+constexpr int bwd_occupancy() {
+  return (sizeof(CT) == 2 && D <= 64) ? 2 : 1;
+}
+
+// ---------------------------------------------------------------------------
+// key-parallel reverse pass: dv, dk_main, suffix checkpoints
+
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(BwdParams P) {
   using TL = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
-  __shared__ float st_s[2][3 * kTileQ];   // lse, sinv, dbar
+  __shared__ __attribute__((aligned(16))) float st_s[2][3 * kTileQ];   // lse, sinv, dbs
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const float hf = static_cast<float>(h);
   const int kb0 = item.idx * 4;
   const int kb = kb0 + wave;                     // key tile of this wave
   const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
@@ -137,9 +183,9 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
   const CT* dots = static_cast<const CT*>(P.dot) + slice * D * P.t_pad;
   const float* lse = P.lse + slice * P.T;
   const float* sinv = P.sinv + slice * P.T;
-  const float* dbar = P.dbar + slice * P.T;
+  const float* dbs = P.dbs + slice * P.T;
 
-  // this wave's keys as B operands (natural order: lane <-> key)
+  // this wave's keys as B operands (lane <-> key)
   RowFrag<CT, D> kf, vf;
   if (key < P.T) {
     load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
@@ -150,19 +196,23 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
   }
   floatx16 dka[kDTiles<D>], dva[kDTiles<D>];
 #pragma unroll
-  for (int t = 0; t < kDTiles<D>; ++t) { dka[t] = floatx16{}; dva[t] = floatx16{}; }
+  for (int t = 0; t < kDTiles<D>; ++t) {
+    dka[t] = floatx16{};
+    dva[t] = floatx16{};
+  }
   float sufk = 0.f;
+  float* sufk_col = P.sufk + slice * P.nb * P.T + key;
 
   KTileLoader<CT, D> ql, dl;
   TTileLoader<CT, D> qtl, dtl;
-  RowStatsLoader sl;
+  RowStatsLoader<3> sl;
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
     dl.load(dos, row0, P.T);
     qtl.load(qts, P.t_pad, row0);
     dtl.load(dots, P.t_pad, row0);
-    sl.load(lse, sinv, dbar, row0, P.T);
+    sl.load(lse, sinv, dbs, row0, P.T);
   };
   auto stash = [&](int buf) {
     ql.store(q_s[buf]);
@@ -177,8 +227,68 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
   auto carry_at = [&](int qt) -> float {
     return (active && qt >= kb && key < P.T) ? P.carry[(slice * P.nb + qt) * P.T + key] : 0.f;
   };
-  float cin_next = carry_at(nq - 1);
 
+  auto step = [&](int qt, int buf, float cin, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    const float* st = st_s[buf];
+    RowFrag<CT, D> qf;
+    lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
+    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float lz[16], p[16], x[16];
+    lds_read16(st + 16 * h, lz);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
+    if constexpr (DIAG) {
+      const int dk = l32 - 16 * h;               // key - row(i) = dk - i on the diagonal tile
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dk > i) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = p[i];
+    scan_incl_qs(x, cin + kEps, hf);
+    float si[16];
+    lds_read16(st + kTileQ + 16 * h, si);
+    float sh[16], w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = fast_rcp(x[i]);                     // inv
+      sh[i] = p[i] * x[i];
+      w[i] = sh[i] * si[i];                      // attention weight
+    }
+    // dv^T += dO^T A  (keys in lanes)
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto bfr = acc_frag<CT>(w, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
+    }
+    RowFrag<CT, D> dof;
+    lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
+    float db[16];
+    lds_read16(st + 2 * kTileQ + 16 * h, db);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      w[i] = fmaf(dov[i], si[i], -db[i]);        // ds
+      x[i] = w[i] * (sh[i] * x[i]);              // g = ds sh inv
+    }
+    if (h == 0 && active && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk;
+    sufk += scan_suffix_qs(x, sufk, hf);         // x = G
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = fmaf(w[i], sh[i], -p[i] * x[i]);   // p dp
+    // dk_main^T += Q^T (p dp)
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto bfr = acc_frag<CT>(w, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        dka[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
+    }
+  };
+
+  float cin_next = carry_at(nq - 1);
   fetch(nq - 1);
   stash(0);
   __syncthreads();
@@ -190,59 +300,9 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
       fetch(qt - 1);
       cin_next = carry_at(qt - 1);
     }
-    if (active && qt >= kb) {
-      const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-      const float* st = st_s[buf];
-      RowFrag<CT, D> qf;
-      lds_row_frag<CT, D>(qf, q_s[buf], rho(l32), h);
-      const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-      const bool diag = qt == kb;
-      float p[16], x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = perm_row(i, h);
-        p[i] = fast_exp2(fmaf(sacc[i], P.c, -st[r]));
-        if (diag && key > row0 + r) p[i] = 0.f;
-        x[i] = p[i];
-      }
-      column_scan_inclusive(x, cin + kEps, h);
-      float inv[16], w[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        inv[i] = fast_rcp(x[i]);
-        w[i] = p[i] * inv[i] * st[kTileQ + perm_row(i, h)];   // attn = share / (S + eps)
-      }
-      // dv^T += dO^T A   (A^T dO with keys in lanes)
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const auto bfr = acc_frag<CT>(w, s);
-#pragma unroll
-        for (int t = 0; t < kDTiles<D>; ++t)
-          dva[t] = Mma<CT>::mma(lds_t_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
-      }
-      RowFrag<CT, D> dof;
-      lds_row_frag<CT, D>(dof, do_s[buf], rho(l32), h);
-      const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
-      float ds[16], tq[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = perm_row(i, h);
-        ds[i] = (dov[i] - st[2 * kTileQ + r]) * st[kTileQ + r];
-        tq[i] = p[i] * inv[i] * inv[i];      // p inv^2
-        x[i] = -ds[i] * tq[i];               // dks
-      }
-      if (h == 0 && key < P.T) P.sufk[(slice * P.nb + qt) * P.T + key] = sufk;
-      sufk += column_scan_suffix_exclusive(x, sufk, h) ;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) w[i] = p[i] * (ds[i] * (inv[i] - tq[i]) + x[i]);   // p dp
-      // dk_main^T += Q^T (p dp)
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const auto bfr = acc_frag<CT>(w, s);
-#pragma unroll
-        for (int t = 0; t < kDTiles<D>; ++t)
-          dka[t] = Mma<CT>::mma(lds_t_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
-      }
+    if (active) {
+      if (qt > kb) step(qt, buf, cin, std::false_type{});
+      else if (qt == kb) step(qt, buf, cin, std::true_type{});
     }
     if (qt - 1 >= kb0) stash(buf ^ 1);
     __syncthreads();
@@ -257,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
       for (int i = 0; i < 16; ++i) {
         const int d = 32 * t + acc_row(i, h);
         if (d < D) {
-          dkrow[d] = dka[t][i] * P.scale;
+          dkrow[d] = dka[t][i];
           store_as(P.dv, dvrow + d, P.gdt, dva[t][i]);
         }
       }
@@ -268,11 +328,12 @@ __global__ __launch_bounds__(kThreads) void bwd_key(BwdParams P) {
 // row-parallel dq pass
 
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
+__global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(BwdParams P) {
   using TL = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
+  __shared__ __attribute__((aligned(16))) float rs_s[4][3 * kTileQ];   // per wave: lse, sinv, dbs
   __shared__ float g_s[4][kTileQ];
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
@@ -280,6 +341,7 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
   const int64_t slice = item.slice;
   const int g = item.idx;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const float hf = static_cast<float>(h);
   const int qt = g * 4 + wave;
   const int64_t r0 = static_cast<int64_t>(qt) * kTileQ;
   const int64_t wg_last = min(static_cast<int64_t>(g * 4 + 4) * kTileQ, P.T);
@@ -290,9 +352,9 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
   const CT* vs = static_cast<const CT*>(P.v) + slice * P.T * D;
   const CT* kts = static_cast<const CT*>(P.kt) + slice * D * P.t_pad;
 
-  // this wave's rows, rho-permuted: register i of half h <-> row perm_row(i, h)
+  // this wave's rows in QS order: register i of half h <-> row r0 + 16 h + i
   RowFrag<CT, D> qf, dof;
-  const int64_t my_row = r0 + rho(l32);
+  const int64_t my_row = r0 + qsig(l32);
   if (my_row < P.T) {
     load_row_frag<CT, D>(qf, static_cast<const CT*>(P.q) + (slice * P.T + my_row) * D + h * (D / 2));
     load_row_frag<CT, D>(dof, static_cast<const CT*>(P.dout) + (slice * P.T + my_row) * D + h * (D / 2));
@@ -300,23 +362,21 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
     zero_row_frag<CT, D>(qf);
     zero_row_frag<CT, D>(dof);
   }
-  float lse[16], si[16], db[16], gh[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t r = r0 + perm_row(i, h);
+  if (h == 0) {
+    const int64_t r = r0 + l32;
     const bool ok = r < P.T;
-    lse[i] = ok ? P.lse[slice * P.T + r] : INFINITY;
-    si[i] = ok ? P.sinv[slice * P.T + r] : 0.f;
-    db[i] = ok ? P.dbar[slice * P.T + r] : 0.f;
-    gh[i] = 0.f;
+    rs_s[wave][l32] = ok ? P.lse[slice * P.T + r] : INFINITY;
+    rs_s[wave][kTileQ + l32] = ok ? P.sinv[slice * P.T + r] : 0.f;
+    rs_s[wave][2 * kTileQ + l32] = ok ? P.dbs[slice * P.T + r] : 0.f;
   }
   constexpr int kSteps = kTileK / Mma<CT>::kStep;
   typename Mma<CT>::frag ident[kSteps];
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) ident[s] = ident_frag<CT>(l32, h, s);
+  for (int s = 0; s < kSteps; ++s) ident[s] = ident_qs<CT>(l32, h, s);
   floatx16 dqa[kDTiles<D>];
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) dqa[t] = floatx16{};
+  float gh = 0.f;     // row sum of p dp for query l32 over this half's keys
   const float* crow = P.carry + (slice * P.nb + qt) * P.T;
   const float* srow = P.sufk + (slice * P.nb + qt) * P.T;
   // demand and suffix checkpoints of this lane's key, loaded one key tile ahead
@@ -324,8 +384,70 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
     const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
     return (kt < nkt_w && key < P.T) ? row[key] : 0.f;
   };
-  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
 
+  auto step = [&](int kt, int buf, float cin, float sin, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    const float* st = rs_s[wave];
+    RowFrag<CT, D> kf;
+    lds_row_frag<CT, D>(kf, k_s[buf], rho(l32), h);
+    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float lz[16], p[16], x[16];
+    lds_read16(st + 16 * h, lz);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
+    if constexpr (DIAG) {
+      const int dk = rho(l32) - 16 * h;          // key - row(i) = dk - i on the diagonal tile
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dk > i) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = p[i];
+    scan_incl_qs(x, cin + kEps, hf);
+    float sh[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = fast_rcp(x[i]);                     // inv
+      sh[i] = p[i] * x[i];
+    }
+    RowFrag<CT, D> vf;
+    lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
+    float si[16], db[16], ds[16];
+    lds_read16(st + kTileQ + 16 * h, si);
+    lds_read16(st + 2 * kTileQ + 16 * h, db);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      ds[i] = fmaf(dov[i], si[i], -db[i]);
+      x[i] = ds[i] * (sh[i] * x[i]);             // g
+    }
+    scan_suffix_qs(x, sin, hf);                  // x = G
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ds[i] = fmaf(ds[i], sh[i], -p[i] * x[i]);   // p dp
+    // transpose (p dp): queries in lanes, keys (natural order) in registers
+    floatx16 xt = floatx16{};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(ds, s), ident[s], xt);
+    float xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = xt[i];
+    float g0 = 0.f, g1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      g0 += xv[i];
+      g1 += xv[i + 1];
+    }
+    gh += g0 + g1;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto af = acc_frag<CT>(xv, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
+    }
+  };
+
+  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
   KTileLoader<CT, D> kl, vl;
   TTileLoader<CT, D> ktl;
   kl.load(ks, 0, P.T);
@@ -346,55 +468,8 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
       cin_next = ckpt_at(kt + 1, crow);
       sin_next = ckpt_at(kt + 1, srow);
     }
-    if (kt < nkt_w) {
-      const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);   // key owned by this lane
-      RowFrag<CT, D> kf;
-      lds_row_frag<CT, D>(kf, k_s[buf], rho(l32), h);
-      const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-      const bool diag = kt == qt;
-      float p[16], x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[i] = fast_exp2(fmaf(sacc[i], P.c, -lse[i]));
-        if (diag && key > r0 + perm_row(i, h)) p[i] = 0.f;
-        x[i] = p[i];
-      }
-      column_scan_inclusive(x, cin + kEps, h);
-      float inv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) inv[i] = fast_rcp(x[i]);
-      RowFrag<CT, D> vf;
-      lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
-      const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
-      float ds[16], tq[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        ds[i] = (dov[i] - db[i]) * si[i];
-        tq[i] = p[i] * inv[i] * inv[i];
-        x[i] = -ds[i] * tq[i];
-      }
-      column_scan_suffix_exclusive(x, sin, h);
-      float w[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        w[i] = p[i] * (ds[i] * (inv[i] - tq[i]) + x[i]);   // p dp
-        gh[i] += w[i];
-      }
-      // transpose (p dp) so queries sit in lanes, then dq += (p dp) K
-      floatx16 xt = floatx16{};
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(w, s), ident[s], xt);
-      float xv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xv[i] = xt[i];
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const auto af = acc_frag<CT>(xv, s);
-#pragma unroll
-        for (int t = 0; t < kDTiles<D>; ++t)
-          dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
-      }
-    }
+    if (kt < qt && kt < nkt_w) step(kt, buf, cin, sin, std::false_type{});
+    else if (kt == qt && kt < nkt_w) step(kt, buf, cin, sin, std::true_type{});
     if (kt + 1 < nkt_wg) {
       kl.store(k_s[buf ^ 1]);
       vl.store(v_s[buf ^ 1]);
@@ -403,18 +478,9 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
     __syncthreads();
   }
 
-  // ghat: row sums of p dp over all keys
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float v = gh[i];
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 64);
-    gh[i] = v;
-  }
-  if (l32 == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) g_s[wave][perm_row(i, h)] = gh[i];
-  }
+  // ghat: row sums of p dp over all keys (the halves hold disjoint keys)
+  const HalfPair gp = halves(gh);
+  if (h == 0) g_s[wave][l32] = gp.lo + gp.hi;
   __syncthreads();
   if (h == 0 && r0 + l32 < P.T) P.ghat[slice * P.T + r0 + l32] = g_s[wave][l32];
 #pragma unroll
@@ -436,13 +502,13 @@ __global__ __launch_bounds__(kThreads) void bwd_query(BwdParams P) {
 // softmax-Jacobian correction of dk
 
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
+__global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) void bwd_dkcorr(BwdParams P) {
   using TL = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
-  __shared__ float st_s[2][3 * kTileQ];   // lse, ghat, (unused)
+  __shared__ __attribute__((aligned(16))) CT qgt_s[2][D * TL::kTStride];
+  __shared__ __attribute__((aligned(16))) float st_s[2][kTileQ];   // lse
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -453,9 +519,8 @@ __global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
   const bool active = static_cast<int64_t>(kb) * kTileK < P.T;
 
   const CT* qs = static_cast<const CT*>(P.q) + slice * P.T * D;
-  const CT* qts = static_cast<const CT*>(P.qt) + slice * D * P.t_pad;
+  const CT* qgts = static_cast<const CT*>(P.qgt) + slice * D * P.t_pad;
   const float* lse = P.lse + slice * P.T;
-  const float* gh = P.ghat + slice * P.T;
 
   RowFrag<CT, D> kf;
   if (key < P.T) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
@@ -466,19 +531,43 @@ __global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
 
   KTileLoader<CT, D> ql;
   TTileLoader<CT, D> qtl;
-  RowStatsLoader sl;
+  RowStatsLoader<1> sl;
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
-    qtl.load(qts, P.t_pad, row0);
-    sl.load(lse, gh, gh, row0, P.T);
+    qtl.load(qgts, P.t_pad, row0);
+    sl.load(lse, lse, lse, row0, P.T);
   };
   auto stash = [&](int buf) {
     ql.store(q_s[buf]);
-    qtl.store(qt_s[buf]);
+    qtl.store(qgt_s[buf]);
     sl.store(st_s[buf]);
   };
   constexpr int kSteps = kTileQ / Mma<CT>::kStep;
+
+  auto step = [&](int buf, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> qf;
+    lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
+    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float lz[16], p[16];
+    lds_read16(st_s[buf] + 16 * h, lz);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
+    if constexpr (DIAG) {
+      const int dk = l32 - 16 * h;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dk > i) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto bfr = acc_frag<CT>(p, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        dkc[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qgt_s[buf], 32 * t + l32, h, s), bfr, dkc[t]);
+    }
+  };
 
   fetch(kb0);
   stash(0);
@@ -487,28 +576,9 @@ __global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
   for (int qt = kb0; qt < nq; ++qt, ++it) {
     const int buf = it & 1;
     if (qt + 1 < nq) fetch(qt + 1);
-    if (active && qt >= kb) {
-      const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-      const float* st = st_s[buf];
-      RowFrag<CT, D> qf;
-      lds_row_frag<CT, D>(qf, q_s[buf], rho(l32), h);
-      const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-      const bool diag = qt == kb;
-      float w[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = perm_row(i, h);
-        float p = fast_exp2(fmaf(sacc[i], P.c, -st[r]));
-        if (diag && key > row0 + r) p = 0.f;
-        w[i] = p * st[kTileQ + r];
-      }
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const auto bfr = acc_frag<CT>(w, s);
-#pragma unroll
-        for (int t = 0; t < kDTiles<D>; ++t)
-          dkc[t] = Mma<CT>::mma(lds_t_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dkc[t]);
-      }
+    if (active) {
+      if (qt > kb) step(buf, std::false_type{});
+      else if (qt == kb) step(buf, std::true_type{});
     }
     if (qt + 1 < nq) stash(buf ^ 1);
     __syncthreads();
@@ -521,7 +591,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int d = 32 * t + acc_row(i, h);
-        if (d < D) store_as(P.dk, base + d, P.gdt, P.dkm[base + d] - dkc[t][i] * P.scale);
+        if (d < D) store_as(P.dk, base + d, P.gdt, (P.dkm[base + d] - dkc[t][i]) * P.scale);
       }
   }
 }
@@ -530,7 +600,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dkcorr(BwdParams P) {
 // host side
 
 struct BwdWorkspace {
-  size_t lse, sinv, dbar, ghat, sufk, dkm, qt, kt, dot, qc, kc, vc, doc, total;
+  size_t lse, sinv, dbs, ghat, sufk, dkm, qt, kt, dot, qgt, qc, kc, vc, doc, total;
 };
 
 BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int lowp) {
@@ -545,14 +615,15 @@ BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, 
   BwdWorkspace w{};
   w.lse = 0;
   w.sinv = w.lse + rowf;
-  w.dbar = w.sinv + rowf;
-  w.ghat = w.dbar + rowf;
+  w.dbs = w.sinv + rowf;
+  w.ghat = w.dbs + rowf;
   w.sufk = w.ghat + rowf;
   w.dkm = w.sufk + align_up(4 * n * nb * T);
   w.qt = w.dkm + align_up(4 * n * T * D);
   w.kt = w.qt + tsz;
   w.dot = w.kt + tsz;
-  w.qc = w.dot + tsz;
+  w.qgt = w.dot + tsz;
+  w.qc = w.qgt + tsz;
   w.kc = w.qc + (convert ? rsz : 0);
   w.vc = w.kc + (convert ? rsz : 0);
   w.doc = w.vc + (convert ? rsz : 0);
@@ -577,6 +648,7 @@ int launch_backward(const BackwardArgs& a) {
   CT* qt = reinterpret_cast<CT*>(ws + w.qt);
   CT* kt = reinterpret_cast<CT*>(ws + w.kt);
   CT* dot = reinterpret_cast<CT*>(ws + w.dot);
+  CT* qgt = reinterpret_cast<CT*>(ws + w.qgt);
   CT* qc = convert ? reinterpret_cast<CT*>(ws + w.qc) : nullptr;
   CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
   CT* vc = convert ? reinterpret_cast<CT*>(ws + w.vc) : nullptr;
@@ -605,6 +677,7 @@ int launch_backward(const BackwardArgs& a) {
   P.qt = qt;
   P.kt = kt;
   P.dot = dot;
+  P.qgt = qgt;
   P.T = a.T;
   P.t_pad = t_pad;
   P.nb = (a.T + kTileQ - 1) / kTileQ;
@@ -612,10 +685,10 @@ int launch_backward(const BackwardArgs& a) {
   P.c = kLog2e * P.scale;
   float* lse = reinterpret_cast<float*>(ws + w.lse);
   float* sinv = reinterpret_cast<float*>(ws + w.sinv);
-  float* dbar = reinterpret_cast<float*>(ws + w.dbar);
+  float* dbs = reinterpret_cast<float*>(ws + w.dbs);
   P.lse = lse;
   P.sinv = sinv;
-  P.dbar = dbar;
+  P.dbs = dbs;
   P.ghat = reinterpret_cast<float*>(ws + w.ghat);
   P.carry = a.carry;
   P.sufk = reinterpret_cast<float*>(ws + w.sufk);
@@ -630,13 +703,16 @@ int launch_backward(const BackwardArgs& a) {
   const int64_t threads = rows * (D / 8);
   DIL_TIMED("bwd_rows", st,
             bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
-                a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbar, rows));
+                a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbs, rows));
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
   P.kgroups = (nkt + 3) / 4;
   const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("bwd_query", st, bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P));
+  DIL_TIMED("prep", st,
+            prep_ghat_q<CT, D><<<gp, kThreads, 0, st>>>(static_cast<const CT*>(P.q), P.ghat, a.T,
+                                                        t_pad, qgt));
   DIL_TIMED("bwd_dkcorr", st, bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P));
   return static_cast<int>(hipGetLastError());
 }
