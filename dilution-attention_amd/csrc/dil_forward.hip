@@ -3,24 +3,26 @@
 //
 // Reference behaviour: dilution_attention_forward,
 // /root/reference/src/dilution/kernels.py:328-455, whose row-parallel
-// decomposition (K1 :137-198 -> block scan :251-264 -> K2 :267-315) this
-// follows in structure; the kernels are written for gfx950 MFMA layouts:
+// decomposition (K1 :137-198, block scan :251-264, K2 :267-315) this
+// follows in its statistics and output passes; the kernels are written for
+// gfx950 MFMA layouts:
 //
 //   prep       convert q/k to the MFMA operand type when needed; write V^T
 //              (and K^T for pk) tiles, zero-padded to a multiple of 64 keys.
-//   fwd_stats  one workgroup = 4 waves = 4 tiles of 32 query rows; key tiles
-//              of 32 staged in LDS.  Sweep 1 computes S^T = K Q^T so each lane
-//              owns one query row: online row max / 2^-sum (log2 domain), and
-//              optionally pk^T = K^T p^T with online rescaling.  Sweep 2
-//              recomputes S = Q K^T (each lane owns one key column) and writes
-//              the per-32-row-block column sums of p.
-//   fwd_scan   exclusive scan of the block sums over blocks (fp64 running sum)
-//              -> carry checkpoints; inclusive total -> committed_total.
-//   fwd_out    S = Q K^T with keys in lanes: p, the in-tile column scan on
-//              registers plus the checkpoint, share = p / (demand + p + eps),
-//              row sums; the share tile is transposed by one MFMA against an
-//              identity operand so that share @ V runs on MFMA with queries in
-//              lanes.  out = (share @ V) / (rowsum + eps).
+//   fwd_stats  row-parallel: one workgroup = 4 waves = 4 tiles of 32 query
+//              rows, key tiles of 32 staged in LDS.  S^T = K Q^T puts one query
+//              per lane: online row max and 2^-sum (log2 domain, lazily moved
+//              offset), and optionally pk^T = K^T p^T on MFMA.
+//   fwd_demand key-parallel: one wave per 32 keys walks the 32-row blocks in
+//              causal order with the fp64 running column sum of p (plus any
+//              incoming prefill demand) in a register, writing the demand that
+//              enters every block (the carry checkpoints) and the totals
+//              (committed_total, the decode accumulator).
+//   fwd_out    row-parallel: S = Q K^T with keys in lanes: p, the in-tile
+//              column scan on registers plus the checkpoint, share = p /
+//              (demand + p + eps), row sums; the share tile is transposed by
+//              one MFMA against an identity operand so that share @ V runs on
+//              MFMA with queries in lanes.  out = (share @ V) / (rowsum + eps).
 //
 // Nothing T x T is stored: scratch is the (n, C/32, Tk) fp32 checkpoint array.
 #include "dil_common.hpp"
@@ -44,6 +46,7 @@ struct FwdParams {
   int64_t C, Tk, q0, nb;
   int64_t n;              // slices
   int groups;             // 128-row groups per slice
+  int kgroups;            // 128-key groups per slice
   float c;                // log2(e) / sqrt(D)
   float scale;            // 1 / sqrt(D)
   float* out;
@@ -101,8 +104,6 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   using T = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
   __shared__ __attribute__((aligned(16))) CT kttile[PK ? 2 : 1][PK ? D * T::kTStride : 1];
-  __shared__ float lse_s[4][kTileQ];
-
   const WorkItem item = xcd_work_item(P.groups, P.n, true);   // heavy (late) row groups first
   if (!item.valid) return;
   const int64_t slice = item.slice;
@@ -215,7 +216,6 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
     P.rmax[slice * P.C + W.r0 + l32] = rmax_v;
     P.rden[slice * P.C + W.r0 + l32] = ltot;
   }
-  if (h == 0) lse_s[wave][l32] = row_ok ? rmax_v + __log2f(ltot) : INFINITY;
   if constexpr (PK) {
     if (row_ok) {
       const float f = P.scale / (lp.lo + lp.hi);      // pk was accumulated against m
@@ -227,24 +227,85 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
           if (32 * t + acc_row(i, h) < D) dst[32 * t + acc_row(i, h)] = pka[t][i] * f;
     }
   }
-  __syncthreads();
+}
 
-  // ---- sweep 2: S = Q K^T (lane <-> key): per-block column sums of p ----
-  float lse[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) lse[i] = lse_s[wave][acc_row(i, h)];
-  float* sblk = P.carry + (slice * P.nb + W.r0 / kTileQ) * P.Tk;
-  auto colsum_step = [&](int kt, int buf, auto diag_tag) {
+// ---------------------------------------------------------------------------
+// demand checkpoints: key-parallel walk over the chunk's 32-row blocks
+//
+// One wave per 32-key tile (lane <-> key).  Walking the row blocks in causal
+// order it carries each key's demand -- the incoming demand of rows before the
+// chunk plus the column sums of p over the chunk rows seen so far -- in an
+// fp64 register, stores it as the checkpoint of every block (the demand
+// entering the block) and finally as the key's total.
+
+template <typename CT, int D>
+__global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) void fwd_demand(FwdParams P) {
+  using T = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * T::kKStride];
+  __shared__ __attribute__((aligned(16))) float st_s[2][kTileQ];   // lse of the block's rows
+
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int kb = item.idx * 4 + wave;
+  const int64_t key0 = static_cast<int64_t>(kb) * kTileK;
+  const int64_t key = key0 + l32;
+  const bool key_ok = key < P.Tk;
+
+  // Block b holds chunk rows [32 b, 32 b + 32) = absolute rows q0 + 32 b + [0, 32).
+  // A key tile meets block b when the block's last row reaches its first key;
+  // it needs no mask once the block's first row is past its last key.
+  auto first_block = [&](int64_t k0) -> int64_t {
+    const int64_t t = k0 - P.q0 - (kTileQ - 1);
+    return t > 0 ? (t + kTileQ - 1) / kTileQ : 0;
+  };
+  const int64_t b_wg = first_block(static_cast<int64_t>(item.idx) * 4 * kTileK);
+  const int64_t b_w = first_block(key0);
+  const int64_t nb = P.nb;
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
+  const float* rmax = P.rmax + slice * P.C;
+  const float* rden = P.rden + slice * P.C;
+
+  RowFrag<CT, D> kf;
+  if (key_ok) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + slice * P.k_sn + key * D + h * (D / 2));
+  else zero_row_frag<CT, D>(kf);
+
+  double run = (P.demand_in != nullptr && key < P.q0 && key_ok)
+                   ? static_cast<double>(P.demand_in[slice * P.din_sn + key]) : 0.0;
+  float* ccol = P.carry + slice * nb * P.Tk + key;
+
+  KTileLoader<CT, D> ql;
+  float lse_r = 0.f;
+  auto fetch = [&](int64_t b) {
+    ql.load(qs, b * kTileQ, P.C);
+    if (threadIdx.x < kTileQ) {
+      const int64_t r = b * kTileQ + threadIdx.x;
+      lse_r = r < P.C ? rmax[r] + __log2f(rden[r]) : INFINITY;
+    }
+  };
+  auto stash = [&](int buf) {
+    ql.store(q_s[buf]);
+    if (threadIdx.x < kTileQ) st_s[buf][threadIdx.x] = lse_r;
+  };
+
+  auto step = [&](int64_t b, int buf, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
-    RowFrag<CT, D> kf;
-    lds_row_frag<CT, D>(kf, ktile[buf], l32, h);
-    const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
+    RowFrag<CT, D> qf;
+    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);
+    const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});   // register i <-> row acc_row(i, h)
     float p[16];
+    const float* st = st_s[buf];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
-    const int key = kt * kTileK + l32;
+    for (int u = 0; u < 4; ++u) {
+      const floatx4 lz = *reinterpret_cast<const floatx4*>(st + 8 * u + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[4 * u + e] = fast_exp2(fmaf(acc[4 * u + e], P.c, -lz[e]));
+    }
     if constexpr (DIAG) {
-      const int dq = key - static_cast<int>(W.qa0) - 4 * h;   // key - query of register i: dq - (8 (i>>2) + (i&3))
+      // key - row for register i: dq - (8 (i >> 2) + (i & 3))
+      const int dq = static_cast<int>(key - P.q0 - b * kTileQ) - 4 * h;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         if (dq > 8 * (i >> 2) + (i & 3)) p[i] = 0.f;
@@ -253,55 +314,34 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
     for (int i = 0; i < 8; ++i) p[i] += p[i + 8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[i] += p[i + 4];
-    const float cs = (p[0] + p[1]) + (p[2] + p[3]);
-    const HalfPair cp = halves(cs);
-    if (h == 0 && key < P.Tk) sblk[key] = cp.lo + cp.hi;
+    const HalfPair cp = halves((p[0] + p[1]) + (p[2] + p[3]));
+    run += static_cast<double>(cp.lo + cp.hi);
   };
-  kl.load(ks, 0, P.Tk);
-  kl.store(ktile[0]);
+
+  // blocks that end before this wave's first key take nothing from it: their
+  // checkpoints are the incoming demand, which is zero for these keys
+  if (h == 0 && key_ok)
+    for (int64_t b = 0; b < b_w; ++b) ccol[b * P.Tk] = 0.f;
+  if (b_wg < nb) {
+    fetch(b_wg);
+    stash(0);
+  }
   __syncthreads();
-  for (int kt = 0; kt < nkt_wg; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nkt_wg) kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
-    if (kt < W.kfull) colsum_step(kt, buf, std::false_type{});
-    else if (kt < W.kend) colsum_step(kt, buf, std::true_type{});
-    if (kt + 1 < nkt_wg) kl.store(ktile[buf ^ 1]);
+  int it = 0;
+  for (int64_t b = b_wg; b < nb; ++b, ++it) {
+    const int buf = it & 1;
+    if (b + 1 < nb) fetch(b + 1);
+    // wave-uniform condition: every lane must feed the MFMAs of the step
+    if (b >= b_w && key0 < P.Tk) {
+      if (h == 0 && key_ok) ccol[b * P.Tk] = static_cast<float>(run);   // demand entering block b
+      const int64_t first_row = P.q0 + b * kTileQ;
+      if (key0 + kTileK - 1 <= first_row) step(b, buf, std::false_type{});
+      else step(b, buf, std::true_type{});
+    }
+    if (b + 1 < nb) stash(buf ^ 1);
     __syncthreads();
   }
-}
-
-// ---------------------------------------------------------------------------
-// exclusive scan of block column sums -> carry checkpoints, totals
-
-constexpr int kScanBatch = 8;
-
-__global__ __launch_bounds__(256) void fwd_scan(float* __restrict__ carry, int64_t nb, int64_t Tk,
-                                                int64_t q0, int64_t C,
-                                                const float* __restrict__ demand_in, int64_t din_sn,
-                                                float* __restrict__ total, int64_t tot_sn) {
-  const int64_t slice = blockIdx.y;
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (j >= Tk) return;
-  double run = (demand_in != nullptr && j < q0) ? static_cast<double>(demand_in[slice * din_sn + j]) : 0.0;
-  float* col = carry + slice * nb * Tk + j;
-  // block b covers rows [q0 + 32 b, q0 + 32 b + 32); keys at or beyond its end
-  // were not written by fwd_stats (their sum is zero by causality)
-  for (int64_t b0 = 0; b0 < nb; b0 += kScanBatch) {
-    float s[kScanBatch];
-#pragma unroll
-    for (int u = 0; u < kScanBatch; ++u) {
-      const int64_t b = b0 + u;
-      const bool written = b < nb && j < q0 + 32 * (b + 1) && 32 * b < C;
-      s[u] = written ? col[b * Tk] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < kScanBatch; ++u) {
-      const int64_t b = b0 + u;
-      if (b < nb) col[b * Tk] = static_cast<float>(run);
-      run += static_cast<double>(s[u]);
-    }
-  }
-  total[slice * tot_sn + j] = static_cast<float>(run);
+  if (key_ok && h == 0) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
 }
 
 // ---------------------------------------------------------------------------
@@ -531,9 +571,10 @@ int launch_forward(const ForwardArgs& a) {
   const dim3 grid(static_cast<unsigned>(xcd_grid(P.groups * a.n)));
   if (a.pk) DIL_TIMED("fwd_stats", st, fwd_stats<CT, D, true><<<grid, kThreads, 0, st>>>(P));
   else DIL_TIMED("fwd_stats", st, fwd_stats<CT, D, false><<<grid, kThreads, 0, st>>>(P));
-  DIL_TIMED("fwd_scan", st,
-            fwd_scan<<<dim3(static_cast<unsigned>((a.Tk + 255) / 256), n), 256, 0, st>>>(
-                a.carry, P.nb, a.Tk, a.q0, a.C, a.demand_in, a.din_sn, a.total, a.tot_sn));
+  P.kgroups = static_cast<int>((a.Tk + 4 * kTileK - 1) / (4 * kTileK));
+  DIL_TIMED("fwd_demand", st,
+            fwd_demand<CT, D><<<dim3(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n))),
+                                kThreads, 0, st>>>(P));
   DIL_TIMED("fwd_out", st, fwd_out<CT, D><<<grid, kThreads, 0, st>>>(P));
   return static_cast<int>(hipGetLastError());
 }
