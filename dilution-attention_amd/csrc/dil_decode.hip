@@ -13,10 +13,10 @@
 //                            chunk partials sum(share), sum(share * v);
 //                            committed += p stored in place
 //   dec_finish (n):          out = sum(share * v) / (sum(share) + eps) in the
-//                            query dtype
+//                            query dtype (chunk partials summed in chunk order)
 //
 // HBM bytes per key: K and V rows (2*D*elt) + demand read+write (8) + AFF
-// write+read (8).  Everything is streamed once with 16-byte row loads.
+// write+read (8).  K and V are streamed once with 16-byte non-temporal loads.
 #include "dil_common.hpp"
 #include "dil_internal.hpp"
 
@@ -26,6 +26,7 @@ namespace {
 
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / 64;
+constexpr int kDecUnroll = 2;          // cached rows in flight per lane (measured best)
 
 template <int D>
 struct DecLayout {
@@ -40,6 +41,23 @@ __device__ __forceinline__ float row_reduce(float x) {
 #pragma unroll
   for (int o = 1; o < LPR; o <<= 1) x += __shfl_xor(x, o, 64);
   return x;
+}
+
+// 8 consecutive cached elements of storage dtype `dt` as fp32, read with a
+// non-temporal hint (the cache is streamed once per step).
+__device__ __forceinline__ void load8_stream(const void* base, int64_t idx, int dt, float (&o)[8]) {
+  if (dt == DT_F32) {
+    const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + idx);
+    const floatx4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+    o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
+    o[4] = b[0]; o[5] = b[1]; o[6] = b[2]; o[7] = b[3];
+  } else {
+    const u16x8 r = __builtin_nontemporal_load(
+        reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(base) + idx));
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = (dt == DT_BF16) ? bf16_bits_to_f32(r[e]) : f16_bits_to_f32(r[e]);
+  }
 }
 
 template <int D>
@@ -63,7 +81,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_stats(
   const int64_t kbase = slice * kv_sn + sub * 8;
   float* arow = aff + slice * length;
   float m = -INFINITY, s = 0.f;
-  constexpr int U = 4;   // rows in flight per lane
+  constexpr int U = kDecUnroll;
   for (int64_t jb = j0 + wave * L::kRowsPerWave + rw; jb < j1; jb += (int64_t)U * L::kRowsPerBlock) {
     float kv[U][8];
     bool ok[U];
@@ -71,7 +89,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_stats(
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
       ok[u] = j < j1;
-      if (ok[u]) load8_f32(kc, kbase + j * D, dt, kv[u]);
+      if (ok[u]) load8_stream(kc, kbase + j * D, dt, kv[u]);
     }
     float a[U];
 #pragma unroll
@@ -149,7 +167,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
   const int64_t vbase = slice * kv_sn + sub * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float ssum = 0.f;
-  constexpr int U = 4;
+  constexpr int U = kDecUnroll;
   for (int64_t jb = j0 + wave * L::kRowsPerWave + rw; jb < j1; jb += (int64_t)U * L::kRowsPerBlock) {
     float vv[U][8], a[U], cm[U];
     bool ok[U];
@@ -158,7 +176,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
       const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
       ok[u] = j < j1;
       if (ok[u]) {
-        load8_f32(vc, vbase + j * D, dt, vv[u]);
+        load8_stream(vc, vbase + j * D, dt, vv[u]);
         a[u] = arow[j];
         cm[u] = crow[j];
       }
@@ -196,31 +214,54 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
   }
 }
 
+// One workgroup (256 threads > D) per slice: thread d < D sums column d of
+// the chunk partials, thread D the share totals, four chunks at a time.
 template <int D>
-__global__ __launch_bounds__(64) void dec_finish(const float* __restrict__ part_out, int nchunk,
-                                                 void* __restrict__ out, int64_t o_sn, int dt) {
+__global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part_out, int nchunk,
+                                                  void* __restrict__ out, int64_t o_sn, int dt) {
   const int64_t slice = blockIdx.x;
   const float* base = part_out + slice * nchunk * (D + 1);
-  float ssum = 0.f;
-  for (int c = 0; c < nchunk; ++c) ssum += base[c * (D + 1) + D];
-  const float inv = 1.f / (ssum + kEps);
-  for (int d = threadIdx.x; d < D; d += 64) {
-    float t = 0.f;
-    for (int c = 0; c < nchunk; ++c) t += base[c * (D + 1) + d];
-    store_as(out, slice * o_sn + d, dt, t * inv);
+  __shared__ float tot_s;
+  if (threadIdx.x == D) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int c = 0;
+    for (; c + 4 <= nchunk; c += 4) {
+      s0 += base[(c + 0) * (D + 1) + D];
+      s1 += base[(c + 1) * (D + 1) + D];
+      s2 += base[(c + 2) * (D + 1) + D];
+      s3 += base[(c + 3) * (D + 1) + D];
+    }
+    for (; c < nchunk; ++c) s0 += base[c * (D + 1) + D];
+    tot_s = (s0 + s1) + (s2 + s3);
   }
+  float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+  const int d = threadIdx.x;
+  if (d < D) {
+    int c = 0;
+    for (; c + 4 <= nchunk; c += 4) {
+      t0 += base[(c + 0) * (D + 1) + d];
+      t1 += base[(c + 1) * (D + 1) + d];
+      t2 += base[(c + 2) * (D + 1) + d];
+      t3 += base[(c + 3) * (D + 1) + d];
+    }
+    for (; c < nchunk; ++c) t0 += base[c * (D + 1) + d];
+  }
+  __syncthreads();
+  if (d < D) store_as(out, slice * o_sn + d, dt, ((t0 + t1) + (t2 + t3)) / (tot_s + kEps));
 }
 
-int64_t decode_chunk(int64_t length) {
-  // 1024 keys per workgroup: at B16 H16 and 128K context that is 32768
-  // workgroups; short contexts collapse to a single chunk.
+// Keys per workgroup.  Measured on MI355X at 128K context, B16 H16 d64:
+// 1024-key chunks (32768 workgroups) with two rows in flight per lane stream
+// fastest; larger chunks or deeper unrolling lose occupancy.
+int64_t decode_chunk(int64_t n, int64_t length) {
+  (void)n;
   (void)length;
   return 1024;
 }
 
 template <int D>
 int launch_decode(const DecodeArgs& a) {
-  const int64_t chunk = decode_chunk(a.length);
+  const int64_t chunk = decode_chunk(a.n, a.length);
   const int nchunk = static_cast<int>((a.length + chunk - 1) / chunk);
   char* ws = static_cast<char*>(a.workspace);
   float* aff = reinterpret_cast<float*>(ws);
@@ -239,15 +280,15 @@ int launch_decode(const DecodeArgs& a) {
                                                        part, part_out, a.length, chunk, nchunk,
                                                        a.dtype));
   DIL_TIMED("dec_finish", st,
-            dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 64, 0, st>>>(part_out, nchunk, a.out,
-                                                                            a.o_sn, a.dtype));
+            dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
+                                                                             a.o_sn, a.dtype));
   return static_cast<int>(hipGetLastError());
 }
 
 }  // namespace
 
 int64_t decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
-  const int64_t chunk = decode_chunk(length);
+  const int64_t chunk = decode_chunk(n, length);
   const int64_t nchunk = (length + chunk - 1) / chunk;
   return static_cast<int64_t>(align_up(sizeof(float) * n * length) +
                               align_up(sizeof(float2) * n * nchunk) +
