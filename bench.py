@@ -1,24 +1,32 @@
 """Benchmark of the dilution-attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
-                    [--decode-steps K] [--no-decode] [--no-cpu-baseline]
+                    [--decode-steps K] [--decode-context L] [--no-decode]
+                    [--no-sdpa] [--no-cpu-baseline]
 
-Prints ONE JSON line.  The headline workload (default ``train16k``) is the
-operator's training step, fwd+bwd through ``dilution.kernels.dilution_attention``
-(the autograd drop-in), at B=1 H=16 T=16384 d=64 bf16 with q,k ~ 0.5 N(0,1),
-v, dO ~ N(0,1), inputs resident in HBM before the timed region.  ``value`` is
-algorithmic TFLOP/s, 7 B H T^2 d per step (the causal flash-attention
-fwd+bwd count: forward 2 products, backward 5 including one recompute).
+Prints ONE JSON line.  The headline workload (default ``train16k``,
+BASELINE configs[2]) is the operator's training step, fwd+bwd through
+``dilution.kernels.dilution_attention`` (the autograd drop-in), at B=1 H=16
+T=16384 d=64 bf16 with q,k ~ 0.5 N(0,1), v, dO ~ N(0,1), inputs resident in
+HBM before the timed region.  ``value`` is algorithmic TFLOP/s, 7 B H T^2 d
+per step (the causal flash-attention fwd+bwd count: forward 2 products,
+backward 5 including one recompute), over K steps bracketed by
+torch.cuda.synchronize().
 
 The same line carries
   * ``roofline`` for the step's dominant kernel: its algorithmic FLOPs per
-    launch over its average HIP-event duration inside the timed region;
-  * ``kernels``: per-kernel launches and average milliseconds;
-  * ``decode``: the cached decode step at 128K context (B=16 H=16 d=64 bf16),
-    HBM GB/s over B H L (4d + 8) algorithmic bytes per step, with its own
-    roofline object;
+    launch over its average duration, measured with HIP events recorded by the
+    library around every launch on the launching stream, during a second pass
+    of the same K steps (the first, untimed-by-kernel pass gives ``value``);
+  * ``kernels``: per-kernel launches and average milliseconds of that pass;
+  * ``sdpa``: torch's causal flash attention fwd+bwd at the same shape and
+    dtype on the same GPU, timed the same way (the >= 0.6x comparator);
+  * ``decode``: the cached decode step at 128K context (
+    B=16 H=16 d=64 bf16), HBM GB/s over B H L (4d + 8) algorithmic bytes per
+    step, with its own roofline object;
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
-    formula) timed on this host's cores on a bounded sample of the workload.
+    formula) timed on this host's cores on one (batch, head) slice of the
+    headline workload.
 One GPU only: ``--gpus`` above 1 exits with a message.
 """
 
@@ -26,7 +34,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -38,7 +45,6 @@ for _p in (os.path.join(ROOT, "dilution-attention_amd"), ROOT):
 
 METRIC = "dilution-attn fwd+bwd TFLOP/s & decode HBM GB/s at T=16K, % of MI355X peak"
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
-PEAK_FP32_TFLOPS = 157.3       # MI355X fp32 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
 # Training-step workloads: (batch, heads, seq, head_dim)
@@ -49,17 +55,33 @@ WORKLOADS = {
 
 # Algorithmic products (each B H T^2 d FLOPs causal) that each kernel of the
 # training step carries; they sum to the 7 of the step.  Recomputed products
-# (extra score products, the pk product, the dk correction) count zero.
+# (the pk product, score recomputations, the dk correction) count zero.
 ALGO_PRODUCTS = {
-    "fwd_stats": 1,     # Q K^T (row statistics)
+    "fwd_stats": 1,     # Q K^T
     "fwd_out": 1,       # share @ V
     "bwd_key": 4,       # Q K^T recompute, dO V^T, A^T dO (dv), (p dp)^T Q (dk)
     "bwd_query": 1,     # (p dp) K (dq)
-    "bwd_dkcorr": 0,
-    "bwd_rows": 0,
-    "fwd_scan": 0,
-    "prep": 0,
 }
+
+# Algorithmic bytes per key of each decode kernel (d = head_dim, bf16 cache):
+# dec_stats streams K; dec_apply streams V and reads + writes the demand.
+def decode_bytes_per_key(kernel: str, d: int) -> int:
+    return {"dec_stats": 2 * d, "dec_apply": 2 * d + 8}.get(kernel, 0)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, calibrated
+    against a plain copy) from the committed rocprofv3 measurement of the
+    default workloads, or None when absent."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            rec = json.load(fh)["kernels"][kernel]
+        return int(rec["fetch_bytes"] + rec["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def log(msg: str) -> None:
@@ -75,8 +97,24 @@ def parse_args():
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--decode-context", type=int, default=131072)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (3 times): the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
+
+
+def copy_calibration(dev) -> None:
+    """Three launches of torch's device copy of 2^30 bytes (2^28 fp32)."""
+    import torch
+
+    src = torch.ones(2**28, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": 2**30, "launches": 3}), flush=True)
 
 
 def synthetic_training_inputs(shape, dev, seed=2):
@@ -92,10 +130,38 @@ def synthetic_training_inputs(shape, dev, seed=2):
     return [t.to(dev) for t in (q, k, v, do)]
 
 
-def bench_training(args, dev):
+def timed(step, steps: int) -> float:
+    """Milliseconds per step over `steps` calls, synchronized on both sides."""
     import torch
 
-    from dilution import _hip, kernels
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return max(start.elapsed_time(stop) / steps, wall)
+
+
+def kernel_pass(step, steps: int) -> dict:
+    """Per-kernel {name: (launches, total_ms)} over `steps` calls."""
+    import torch
+
+    from dilution import _hip
+
+    torch.cuda.synchronize()
+    with _hip.kernel_timing() as kt:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    return kt.result
+
+
+def bench_training(args, dev):
+    from dilution import kernels
 
     batch, heads, seq, d = WORKLOADS[args.workload]
     q, k, v, do = synthetic_training_inputs((batch, heads, seq, d), dev)
@@ -109,40 +175,54 @@ def bench_training(args, dev):
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    log(f"{args.workload}: warmup {args.warmup} done")
-
-    torch.cuda.synchronize()
-    with _hip.kernel_timing() as kt:
-        t0 = time.perf_counter()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(args.steps):
-            step()
-        stop.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    ms_event = start.elapsed_time(stop) / args.steps
-    ms = max(ms_event, wall * 1e3 / args.steps)
+    ms = timed(step, args.steps)
     log(f"{args.workload}: {args.steps} timed steps, {ms:.3f} ms/step")
+    per = kernel_pass(step, args.steps)
 
     unit = batch * heads * seq * seq * d            # one causal product: B H T^2 d FLOPs
     flops = 7.0 * unit
-    tflops = flops / (ms * 1e-3) / 1e12
-    per_kernel = {name: {"launches": n, "avg_ms": tot / max(n, 1), "ms_per_step": tot / args.steps}
-                  for name, (n, tot) in kt.result.items()}
-    dom = max(per_kernel, key=lambda nm: per_kernel[nm]["ms_per_step"])
-    dom_flops = ALGO_PRODUCTS.get(dom, 0) * unit     # per launch: every kernel runs once per step
-    dom_ms = per_kernel[dom]["avg_ms"]
+    kernels_out = {name: {"launches": n, "avg_ms": round(tot / max(n, 1), 4),
+                          "ms_per_step": round(tot / args.steps, 4)}
+                   for name, (n, tot) in per.items()}
+    dom = max((nm for nm in per if nm in ALGO_PRODUCTS), key=lambda nm: per[nm][1])
+    n_dom, tot_dom = per[dom]
+    dom_ms = tot_dom / n_dom
+    dom_flops = ALGO_PRODUCTS[dom] * unit
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
     roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "algorithmic_flops_per_launch": dom_flops, "avg_launch_ms": round(dom_ms, 4)}
-    for rec in per_kernel.values():
-        rec["avg_ms"] = round(rec["avg_ms"], 4)
-        rec["ms_per_step"] = round(rec["ms_per_step"], 4)
-    return dict(ms=ms, value=tflops, flops=flops, roofline=roof, kernels=per_kernel,
-                shape=(batch, heads, seq, d))
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": measured_traffic(dom) if args.workload == "train16k" else None,
+            "algorithmic_flops_per_launch": dom_flops, "avg_launch_ms": round(dom_ms, 4),
+            "note": "per-kernel durations from HIP events in a second pass of the same steps; "
+                    "traffic from profiles/hbm_traffic.json"}
+    return dict(ms=ms, value=flops / (ms * 1e-3) / 1e12, roofline=roof, kernels=kernels_out,
+                shape=(batch, heads, seq, d), inputs=(q, k, v, do))
+
+
+def bench_sdpa(args, inputs):
+    """torch causal flash attention fwd+bwd (the softmax comparator) at the
+    same shape; the flash backend is forced so no math-path fallback runs."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    q0, k0, v0, do = inputs
+    xs = [t.detach().clone().requires_grad_(True) for t in (q0, k0, v0)]
+
+    def step():
+        for x in xs:
+            x.grad = None
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            out = torch.nn.functional.scaled_dot_product_attention(*xs, is_causal=True)
+        out.backward(do)
+
+    for _ in range(args.warmup):
+        step()
+    ms = timed(step, args.steps)
+    batch, heads, seq, d = q0.shape
+    tflops = 7.0 * batch * heads * seq * seq * d / (ms * 1e-3) / 1e12
+    log(f"sdpa flash causal fwd+bwd: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")
+    return {"backend": "torch SDPA flash, causal, bf16", "ms_per_step": round(ms, 4),
+            "value": round(tflops, 2), "unit": "TFLOP/s"}
 
 
 def bench_decode(args, dev):
@@ -150,7 +230,7 @@ def bench_decode(args, dev):
     synthetic K/V caches and a non-negative demand vector resident in HBM."""
     import torch
 
-    from dilution import _hip, kernels
+    from dilution import kernels
 
     batch, heads, d, length = 16, 16, 64, args.decode_context
     g = torch.Generator(device=dev).manual_seed(4)
@@ -165,30 +245,28 @@ def bench_decode(args, dev):
 
     for _ in range(3):
         step()
-    torch.cuda.synchronize()
-    with _hip.kernel_timing() as kt:
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(args.decode_steps):
-            step()
-        stop.record()
-        torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / args.decode_steps
+    ms = timed(step, args.decode_steps)
+    per = kernel_pass(step, args.decode_steps)
     nbytes = batch * heads * length * (4 * d + 8)
     gbs = nbytes / (ms * 1e-3) / 1e9
     per_kernel = {name: {"launches": n, "avg_ms": round(tot / max(n, 1), 4)}
-                  for name, (n, tot) in kt.result.items()}
-    kern_ms = sum(tot for (_, tot) in kt.result.values()) / args.decode_steps
-    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+                  for name, (n, tot) in per.items()}
+    dom = max((nm for nm in per if decode_bytes_per_key(nm, d)), key=lambda nm: per[nm][1])
+    n_dom, tot_dom = per[dom]
+    dom_bytes = batch * heads * length * decode_bytes_per_key(dom, d)
+    achieved = dom_bytes / (tot_dom / n_dom * 1e-3) / 1e9
     log(f"decode L={length}: {ms:.3f} ms/step, {gbs:.0f} GB/s")
     return {"metric": "decode HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
+            "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
             "ms_per_step": round(ms, 4), "steps": args.decode_steps,
             "config": {"workload": "C4 cached decode", "batch": batch, "heads": heads,
                        "context": length, "head_dim": d, "dtype": "bf16"},
-            "roofline": {"kernel": "dec_stats+dec_apply+dec_finish (one step)", "bound": "hbm",
-                         "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                         "algorithmic_bytes_per_step": nbytes},
+            "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(achieved / PEAK_HBM_GBS, 4),
+                         "traffic": measured_traffic(dom) if length == 131072 else None,
+                         "algorithmic_bytes_per_launch": dom_bytes,
+                         "avg_launch_ms": round(tot_dom / n_dom, 4)},
             "kernels": per_kernel}
 
 
@@ -239,6 +317,9 @@ def main() -> int:
         print("libdilution_hip.so is not built (run __graft_entry__.build())", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return 0
     tr = bench_training(args, dev)
     batch, heads, seq, d = tr["shape"]
     line = {
@@ -261,6 +342,14 @@ def main() -> int:
         "roofline": tr["roofline"],
         "kernels": tr["kernels"],
     }
+    if not args.no_sdpa:
+        try:
+            sd = bench_sdpa(args, tr["inputs"])
+            sd["ratio_dilution_over_sdpa"] = round(tr["value"] / sd["value"], 3)
+            line["sdpa"] = sd
+        except Exception as exc:  # backend unavailable: report, do not fall back
+            line["sdpa"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
+    del tr["inputs"]
     if not args.no_decode:
         torch.cuda.empty_cache()
         line["decode"] = bench_decode(args, dev)
