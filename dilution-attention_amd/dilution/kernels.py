@@ -12,13 +12,14 @@ the tensors are not on the GPU, the entry points raise.
     share     = p / (committed + p + eps)         # bid vs cumulative demand
     A         = share / rowsum(share);  out = A @ v
 
-Kernel decomposition (csrc/): a row-statistics pass that also writes
-per-32-row-block column sums of p, an fp64 block scan that turns them into
-demand checkpoints, an output pass with the in-tile demand scan on registers,
-the matching backward (a reverse key-parallel walk for dv, dk and the demand
-adjoint, a row-parallel dq pass, and the softmax-Jacobian correction of dk),
-and a split-K decode step.  Tuning arguments of the Triton reference (block
-sizes, warps, stages) are accepted and ignored: tiles are fixed for gfx950.
+Kernel decomposition (csrc/): a row-statistics pass (row max, 2^-sum and the
+saved p @ k), a key-parallel demand walk that writes the demand entering every
+32-row block and the per-key totals (fp64 running sums), an output pass with
+the in-tile demand scan on registers, the matching backward (a reverse
+key-parallel walk for dv, dk and the demand adjoint, a row-parallel dq pass,
+and the softmax-Jacobian correction of dk), and a split-K decode step.  Tuning
+arguments of the Triton reference (block sizes, warps, stages) are accepted
+and ignored: tiles are fixed for gfx950.
 """
 
 from __future__ import annotations
