@@ -5,26 +5,28 @@
 // /root/reference/docs/kernels.md:62-84.  With s = 1/sqrt(d), C the inclusive
 // column demand (c + p) and S the row sum of shares:
 //
-//   ds_ij  = (dO_i . v_j - dO_i . o_i) / (S_i + eps) = (dO_i . v_j) sinv_i - dbs_i
+//   ds_ij  = (dO_i . v_j - dO_i . o_i) / (S_i + eps) = dO'_i . v_j - dbs_i,
+//            dO'_i = dO_i sinv_i (the rows of dO prescaled once), sinv_i = 1/(S_i+eps)
 //   inv_ij = 1 / (C_ij + eps),   sh_ij = p_ij inv_ij
 //   g_ij   = ds_ij sh_ij inv_ij                  (adjoint flowing into the demand)
 //   G_ij   = sum_{i' >= i} g_i'j                 (inclusive reverse column scan)
 //   dp_ij  = ds_ij inv_ij - G_ij,   p dp = ds_ij sh_ij - p_ij G_ij
 //   ghat_i = sum_j (p dp)_ij,   da_ij = (p dp)_ij - p_ij ghat_i
-//   dq = s da K,   dk = s da^T Q,   dv = (sh sinv)^T dO
+//   dq = s da K,   dk = s da^T Q,   dv = sh^T dO' 
 //
 // Kernels (gfx950, deterministic, no atomics; tiles in the query-split layout
 // of dil_tiles.hpp, causal diagonal tiles peeled out of the main loops):
 //   bwd_rows    per row: lse = rmax + log2 rden, sinv = 1/(S + eps),
 //               dbs = (dO . o) sinv.
 //   bwd_key     one wave per 32-key tile, query tiles walked in reverse:
-//               dv += (sh sinv)^T dO and dk_main += (p dp)^T Q on MFMA with
+//               dv += sh^T dO' and dk_main += (p dp)^T Q on MFMA with
 //               keys in lanes; the running suffix G per key is stored at every
 //               tile boundary for bwd_query.
 //   bwd_query   one wave per 32-row tile over its causal key tiles: the same
-//               chain with G from the checkpoints; ghat = row sums of p dp;
-//               (p dp) transposed by an identity MFMA so dq += (p dp) K runs
-//               with queries in lanes; dq = s dq_main - ghat pk.
+//               chain with G from the checkpoints; (p dp) transposed by an
+//               identity MFMA so dq += (p dp) K runs with queries in lanes,
+//               ghat (the row sums of p dp) riding on it as a ones column;
+//               dq = s dq_main - ghat pk.
 //   prep_ghat_q (ghat * Q)^T tiles for the correction.
 //   bwd_dkcorr  one wave per key tile: dk = s dk_main - s sum_i p_ij (ghat_i q_i).
 #include "dil_common.hpp"
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float st_s[2][3 * kTileQ];   // lse, sinv, dbs
+  __shared__ __attribute__((aligned(16))) float st_s[2][2 * kTileQ];   // lse, dbs
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
   if (!item.valid) return;
@@ -182,7 +184,6 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   const CT* qts = static_cast<const CT*>(P.qt) + slice * D * P.t_pad;
   const CT* dots = static_cast<const CT*>(P.dot) + slice * D * P.t_pad;
   const float* lse = P.lse + slice * P.T;
-  const float* sinv = P.sinv + slice * P.T;
   const float* dbs = P.dbs + slice * P.T;
 
   // this wave's keys as B operands (lane <-> key)
@@ -205,14 +206,14 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
 
   KTileLoader<CT, D> ql, dl;
   TTileLoader<CT, D> qtl, dtl;
-  RowStatsLoader<3> sl;
+  RowStatsLoader<2> sl;
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
     dl.load(dos, row0, P.T);
     qtl.load(qts, P.t_pad, row0);
     dtl.load(dots, P.t_pad, row0);
-    sl.load(lse, sinv, dbs, row0, P.T);
+    sl.load(lse, dbs, dbs, row0, P.T);
   };
   auto stash = [&](int buf) {
     ql.store(q_s[buf]);
@@ -247,19 +248,16 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = p[i];
     scan_incl_qs(x, cin + kEps, hf);
-    float si[16];
-    lds_read16(st + kTileQ + 16 * h, si);
     float sh[16], w[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       x[i] = fast_rcp(x[i]);                     // inv
       sh[i] = p[i] * x[i];
-      w[i] = sh[i] * si[i];                      // attention weight
     }
-    // dv^T += dO^T A  (keys in lanes)
+    // dv^T += dO'^T sh  (keys in lanes; dO' carries the 1/(S+eps) of A)
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const auto bfr = acc_frag<CT>(w, s);
+      const auto bfr = acc_frag<CT>(sh, s);
 #pragma unroll
       for (int t = 0; t < kDTiles<D>; ++t)
         dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
@@ -268,13 +266,12 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
     const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
     float db[16];
-    lds_read16(st + 2 * kTileQ + 16 * h, db);
+    lds_read16(st + kTileQ + 16 * h, db);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      w[i] = fmaf(dov[i], si[i], -db[i]);        // ds
+      w[i] = dov[i] - db[i];                     // ds
       x[i] = w[i] * (sh[i] * x[i]);              // g = ds sh inv
     }
-    if (h == 0 && active && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk;
     sufk += scan_suffix_qs(x, sufk, hf);         // x = G
 #pragma unroll
     for (int i = 0; i < 16; ++i) w[i] = fmaf(w[i], sh[i], -p[i] * x[i]);   // p dp
@@ -300,9 +297,11 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
       fetch(qt - 1);
       cin_next = carry_at(qt - 1);
     }
-    if (active) {
+    if (active && qt >= kb) {
+      const float sufk_in = sufk;                // suffix entering this tile from below
       if (qt > kb) step(qt, buf, cin, std::false_type{});
-      else if (qt == kb) step(qt, buf, cin, std::true_type{});
+      else step(qt, buf, cin, std::true_type{});
+      if (h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     }
     if (qt - 1 >= kb0) stash(buf ^ 1);
     __syncthreads();
@@ -333,7 +332,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
   __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float rs_s[4][3 * kTileQ];   // per wave: lse, sinv, dbs
+  __shared__ __attribute__((aligned(16))) float rs_s[4][2 * kTileQ];   // per wave: lse, dbs
   __shared__ float g_s[4][kTileQ];
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
@@ -366,8 +365,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     const int64_t r = r0 + l32;
     const bool ok = r < P.T;
     rs_s[wave][l32] = ok ? P.lse[slice * P.T + r] : INFINITY;
-    rs_s[wave][kTileQ + l32] = ok ? P.sinv[slice * P.T + r] : 0.f;
-    rs_s[wave][2 * kTileQ + l32] = ok ? P.dbs[slice * P.T + r] : 0.f;
+    rs_s[wave][kTileQ + l32] = ok ? P.dbs[slice * P.T + r] : 0.f;
   }
   constexpr int kSteps = kTileK / Mma<CT>::kStep;
   typename Mma<CT>::frag ident[kSteps];
@@ -376,7 +374,9 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
   floatx16 dqa[kDTiles<D>];
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) dqa[t] = floatx16{};
-  float gh = 0.f;     // row sum of p dp for query l32 over this half's keys
+  // ghat rides on the dq products as a ones column: column 0 of this tile
+  floatx16 gacc = floatx16{};
+  const auto ones = ones_col_frag<CT>(l32);
   const float* crow = P.carry + (slice * P.nb + qt) * P.T;
   const float* srow = P.sufk + (slice * P.nb + qt) * P.T;
   // demand and suffix checkpoints of this lane's key, loaded one key tile ahead
@@ -413,12 +413,11 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     RowFrag<CT, D> vf;
     lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
     const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
-    float si[16], db[16], ds[16];
-    lds_read16(st + kTileQ + 16 * h, si);
-    lds_read16(st + 2 * kTileQ + 16 * h, db);
+    float db[16], ds[16];
+    lds_read16(st + kTileQ + 16 * h, db);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      ds[i] = fmaf(dov[i], si[i], -db[i]);
+      ds[i] = dov[i] - db[i];
       x[i] = ds[i] * (sh[i] * x[i]);             // g
     }
     scan_suffix_qs(x, sin, hf);                  // x = G
@@ -431,19 +430,13 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     float xv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) xv[i] = xt[i];
-    float g0 = 0.f, g1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      g0 += xv[i];
-      g1 += xv[i + 1];
-    }
-    gh += g0 + g1;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
       const auto af = acc_frag<CT>(xv, s);
 #pragma unroll
       for (int t = 0; t < kDTiles<D>; ++t)
         dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
+      gacc = Mma<CT>::mma(af, ones, gacc);
     }
   };
 
@@ -478,9 +471,11 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     __syncthreads();
   }
 
-  // ghat: row sums of p dp over all keys (the halves hold disjoint keys)
-  const HalfPair gp = halves(gh);
-  if (h == 0) g_s[wave][l32] = gp.lo + gp.hi;
+  // ghat: column 0 of gacc, register i of half h <-> row acc_row(i, h)
+  if (l32 == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) g_s[wave][acc_row(i, h)] = gacc[i];
+  }
   __syncthreads();
   if (h == 0 && r0 + l32 < P.T) P.ghat[slice * P.T + r0 + l32] = g_s[wave][l32];
 #pragma unroll
@@ -627,7 +622,8 @@ BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, 
   w.kc = w.qc + (convert ? rsz : 0);
   w.vc = w.kc + (convert ? rsz : 0);
   w.doc = w.vc + (convert ? rsz : 0);
-  w.total = w.doc + (convert_do ? rsz : 0);
+  w.total = w.doc + rsz;                      // dO' (dO scaled by sinv) is always built
+  (void)convert_do;
   return w;
 }
 
@@ -640,7 +636,6 @@ int launch_backward(const BackwardArgs& a) {
   char* ws = static_cast<char*>(a.workspace);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const bool convert = a.dtype != ctc;
-  const bool convert_do = a.dout_dtype != ctc;
   const int64_t t_pad = pad64(a.T);
   const unsigned n = static_cast<unsigned>(a.n);
   const int64_t sn = a.T * D;
@@ -652,28 +647,25 @@ int launch_backward(const BackwardArgs& a) {
   CT* qc = convert ? reinterpret_cast<CT*>(ws + w.qc) : nullptr;
   CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
   CT* vc = convert ? reinterpret_cast<CT*>(ws + w.vc) : nullptr;
-  CT* doc = convert_do ? reinterpret_cast<CT*>(ws + w.doc) : nullptr;
+  CT* doc = reinterpret_cast<CT*>(ws + w.doc);
 
   const dim3 gp(static_cast<unsigned>(t_pad / 64), n);
   DIL_TIMED("prep", st,
             prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt, D * t_pad,
-                                                        t_pad));
+                                                        t_pad, nullptr));
   DIL_TIMED("prep", st,
             prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt, D * t_pad,
-                                                        t_pad));
+                                                        t_pad, nullptr));
   if (convert)
     DIL_TIMED("prep", st,
               prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn, nullptr, 0,
-                                                          t_pad));
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot,
-                                                        D * t_pad, t_pad));
+                                                          t_pad, nullptr));
 
   BwdParams P{};
   P.q = convert ? static_cast<const void*>(qc) : a.q;
   P.k = convert ? static_cast<const void*>(kc) : a.k;
   P.v = convert ? static_cast<const void*>(vc) : a.v;
-  P.dout = convert_do ? static_cast<const void*>(doc) : a.dout;
+  P.dout = doc;
   P.qt = qt;
   P.kt = kt;
   P.dot = dot;
@@ -704,6 +696,10 @@ int launch_backward(const BackwardArgs& a) {
   DIL_TIMED("bwd_rows", st,
             bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
                 a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbs, rows));
+  // dO' = dO / (S + eps), row-major and transposed, in the compute type
+  DIL_TIMED("prep", st,
+            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot,
+                                                        D * t_pad, t_pad, sinv));
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
   P.kgroups = (nkt + 3) / 4;

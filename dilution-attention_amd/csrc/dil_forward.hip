@@ -348,10 +348,12 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
 // output pass
 
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) void fwd_out(FwdParams P) {
+__global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   using T = Tiles<CT, D>;
-  __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
-  __shared__ __attribute__((aligned(16))) CT vttile[2][D * T::kTStride];
+  // a stage holds two consecutive key tiles; two stages double-buffer them
+  __shared__ __attribute__((aligned(16))) CT ktile[2][2][kTileK * T::kKStride];
+  __shared__ __attribute__((aligned(16))) CT vttile[2][2][D * T::kTStride];
+  __shared__ __attribute__((aligned(16))) float lse_s[4][kTileQ];
   __shared__ float ssum_s[4][kTileQ];
 
   const WorkItem item = xcd_work_item(P.groups, P.n, true);
@@ -362,6 +364,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   const float hf = static_cast<float>(h);
   const WaveRows W = wave_rows(P, g, wave);
   const int nkt_wg = group_key_tiles(P, g);
+  const int nst = (nkt_wg + 1) / 2;                    // stages of two key tiles
 
   const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
   const CT* ks = static_cast<const CT*>(P.k) + slice * P.k_sn;
@@ -373,9 +376,8 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   if (my_row < P.C) load_row_frag<CT, D>(qf, qs + my_row * D + h * (D / 2));
   else zero_row_frag<CT, D>(qf);
 
-  // log2-sum-exp of this wave's rows, read from LDS at every tile (keeps
+  // log2-sum-exp of this wave's rows, read from LDS at every step (keeps
   // registers for occupancy)
-  __shared__ __attribute__((aligned(16))) float lse_s[4][kTileQ];
   if (h == 0) {
     const int64_t r = W.r0 + l32;
     lse_s[wave][l32] = (r < P.C) ? P.rmax[slice * P.C + r] + __log2f(P.rden[slice * P.C + r]) : INFINITY;
@@ -387,21 +389,30 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   floatx16 o[kDTiles<D>];
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) o[t] = floatx16{};
-  float rs = 0.f;     // row sum of shares for query l32 over this half's keys
+  // row sums of the shares ride on the share @ V products as a ones column:
+  // column 0 of this tile (lanes 0 and 32) accumulates them
+  floatx16 orow = floatx16{};
+  const auto ones = ones_col_frag<CT>(l32);
 
   const float* crow = P.carry + (slice * P.nb + W.r0 / kTileQ) * P.Tk;
-  // demand checkpoint of this lane's key, loaded one key tile ahead
+  // demand checkpoint of this lane's key, loaded one stage ahead
   auto carry_at = [&](int kt) -> float {
     const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
     return (kt < W.kend && key < P.Tk) ? crow[key] : 0.f;
   };
-  float cin_next = carry_at(0);
 
-  auto out_step = [&](int kt, int buf, float cin, auto diag_tag) {
+  // N consecutive key tiles kt0 .. kt0 + N - 1 of stage buffer `buf`, their
+  // phases interleaved so that one tile's MFMAs overlap the other's VALU work
+  auto out_tiles = [&](auto n_tag, auto diag_tag, int kt0, int slot0, int buf, const float* cin) {
+    constexpr int N = decltype(n_tag)::value;
     constexpr bool DIAG = decltype(diag_tag)::value;
-    RowFrag<CT, D> kf;
-    lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
-    const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});
+    floatx16 acc[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      RowFrag<CT, D> kf;
+      lds_row_frag<CT, D>(kf, ktile[buf][slot0 + n], rho(l32), h);
+      acc[n] = mma_rows<CT, D>(qf, kf, floatx16{});
+    }
     float lse[16];
     {
       const floatx4* lp = reinterpret_cast<const floatx4*>(&lse_s[wave][16 * h]);
@@ -411,70 +422,104 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
         lse[4 * u] = v[0]; lse[4 * u + 1] = v[1]; lse[4 * u + 2] = v[2]; lse[4 * u + 3] = v[3];
       }
     }
-    float p[16], x[16];
+    float p[N][16], x[N][16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(acc[i], P.c, -lse[i]));
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) p[n][i] = fast_exp2(fmaf(acc[n][i], P.c, -lse[i]));
     if constexpr (DIAG) {
-      const int dk = kt * kTileK + rho(l32) - static_cast<int>(W.qa0) - 16 * h;   // key - query(i) = dk - i
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (dk > i) p[i] = 0.f;
+      for (int n = 0; n < N; ++n) {
+        const int dk = (kt0 + n) * kTileK + rho(l32) - static_cast<int>(W.qa0) - 16 * h;   // key - query(i) = dk - i
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (dk > i) p[n][i] = 0.f;
+      }
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = p[i];
-    scan_incl_qs(x, cin + kEps, hf);
+    for (int n = 0; n < N; ++n) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] *= fast_rcp(x[i]);     // share
-    // transpose the share tile: queries in lanes, keys (natural order) in registers
-    floatx16 xt = floatx16{};
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(p, s), ident[s], xt);
-    float xv[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) xv[i] = xt[i];
-    float r0s = 0.f, r1s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      r0s += xv[i];
-      r1s += xv[i + 1];
+      for (int i = 0; i < 16; ++i) x[n][i] = p[n][i];
+      scan_incl_qs(x[n], cin[n] + kEps, hf);
     }
-    rs += r0s + r1s;
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const auto af = acc_frag<CT>(xv, s);
+    for (int n = 0; n < N; ++n)
 #pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        o[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(vttile[buf], 32 * t + l32, h, s), o[t]);
+      for (int i = 0; i < 16; ++i) p[n][i] *= fast_rcp(x[n][i]);     // share
+    // transpose each share tile: queries in lanes, keys (natural order) in registers
+    floatx16 xt[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      xt[n] = floatx16{};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) xt[n] = Mma<CT>::mma(acc_frag<CT>(p[n], s), ident[s], xt[n]);
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      float xv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xv[i] = xt[n][i];
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const auto af = acc_frag<CT>(xv, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          o[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(vttile[buf][slot0 + n], 32 * t + l32, h, s), o[t]);
+        orow = Mma<CT>::mma(af, ones, orow);
+      }
     }
   };
 
-  KTileLoader<CT, D> kl;
-  TTileLoader<CT, D> vl;
-  kl.load(ks, 0, P.Tk);
-  vl.load(vts, P.tk_pad, 0);
-  kl.store(ktile[0]);
-  vl.store(vttile[0]);
+  KTileLoader<CT, D> kl[2];
+  TTileLoader<CT, D> vl[2];
+  auto fetch = [&](int st) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int64_t key0 = static_cast<int64_t>(2 * st + n) * kTileK;
+      kl[n].load(ks, key0, P.Tk);
+      vl[n].load(vts, P.tk_pad, key0);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      kl[n].store(ktile[buf][n]);
+      vl[n].store(vttile[buf][n]);
+    }
+  };
+  float cnext[2] = {carry_at(0), carry_at(1)};
+  fetch(0);
+  stash(0);
   __syncthreads();
-  for (int kt = 0; kt < nkt_wg; ++kt) {
-    const int buf = kt & 1;
-    const float cin = cin_next;
-    if (kt + 1 < nkt_wg) {
-      kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
-      vl.load(vts, P.tk_pad, static_cast<int64_t>(kt + 1) * kTileK);
-      cin_next = carry_at(kt + 1);
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    const int kt0 = 2 * st;
+    const float cin[2] = {cnext[0], cnext[1]};
+    if (st + 1 < nst) {
+      fetch(st + 1);
+      cnext[0] = carry_at(kt0 + 2);
+      cnext[1] = carry_at(kt0 + 3);
     }
-    if (kt < W.kfull) out_step(kt, buf, cin, std::false_type{});
-    else if (kt < W.kend) out_step(kt, buf, cin, std::true_type{});
-    if (kt + 1 < nkt_wg) {
-      kl.store(ktile[buf ^ 1]);
-      vl.store(vttile[buf ^ 1]);
+    if (kt0 + 1 < W.kfull) {
+      out_tiles(std::integral_constant<int, 2>{}, std::false_type{}, kt0, 0, buf, cin);
+    } else {
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        if (kt0 + n < W.kfull)
+          out_tiles(std::integral_constant<int, 1>{}, std::false_type{}, kt0 + n, n, buf, cin + n);
+        else if (kt0 + n < W.kend)
+          out_tiles(std::integral_constant<int, 1>{}, std::true_type{}, kt0 + n, n, buf, cin + n);
+      }
     }
+    if (st + 1 < nst) stash(buf ^ 1);
     __syncthreads();
   }
 
-  // row sums: the two halves hold disjoint keys of the same query
-  const HalfPair rp = halves(rs);
-  if (h == 0) ssum_s[wave][l32] = rp.lo + rp.hi;
+  // row sums: column 0 of orow, register i of half h <-> row acc_row(i, h)
+  if (l32 == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ssum_s[wave][acc_row(i, h)] = orow[i];
+  }
   __syncthreads();
   if (h == 0 && W.r0 + l32 < P.C) P.ssum[slice * P.C + W.r0 + l32] = ssum_s[wave][l32];
 #pragma unroll
@@ -527,16 +572,16 @@ int launch_forward(const ForwardArgs& a) {
   const dim3 gk(static_cast<unsigned>(tk_pad / 64), n);
   DIL_TIMED("prep", st,
             prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr, 0, vt,
-                                                        D * tk_pad, tk_pad));
+                                                        D * tk_pad, tk_pad, nullptr));
   if (convert || kt != nullptr)
     DIL_TIMED("prep", st,
               prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc, a.Tk * D,
-                                                          kt, D * tk_pad, tk_pad));
+                                                          kt, D * tk_pad, tk_pad, nullptr));
   if (convert) {
     const dim3 gq(static_cast<unsigned>(pad64(a.C) / 64), n);
     DIL_TIMED("prep", st,
               prep_kernel<CT, D><<<gq, kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc, a.C * D,
-                                                          nullptr, 0, 0));
+                                                          nullptr, 0, 0, nullptr));
   }
 
   FwdParams P{};

@@ -20,11 +20,16 @@ template <int D> constexpr int kDTiles = (D + 31) / 32;
 // ---------------------------------------------------------------------------
 // operand preparation
 
+// Rows of `src` (storage dtype dt) in the compute type CT, optionally scaled
+// per row by rscale[(slice, row)] (in fp32, before the rounding to CT): a
+// row-major copy into dst and/or a transposed (D, rows_pad) copy into dst_t,
+// zero-padded past `rows`.
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__ src, int64_t src_sn,
                                                         int dt, int64_t rows, CT* __restrict__ dst,
                                                         int64_t dst_sn, CT* __restrict__ dst_t,
-                                                        int64_t t_sn, int64_t rows_pad) {
+                                                        int64_t t_sn, int64_t rows_pad,
+                                                        const float* __restrict__ rscale) {
   __shared__ float tile[64][D + 1];
   const int64_t slice = blockIdx.y;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
@@ -32,7 +37,14 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__
   for (int idx = threadIdx.x; idx < 64 * kVecPerRow; idx += kThreads) {
     const int r = idx / kVecPerRow, c8 = (idx % kVecPerRow) * 8;
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (r0 + r < rows) load8_f32(src, slice * src_sn + (r0 + r) * D + c8, dt, v);
+    if (r0 + r < rows) {
+      load8_f32(src, slice * src_sn + (r0 + r) * D + c8, dt, v);
+      if (rscale != nullptr) {
+        const float f = rscale[slice * rows + r0 + r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] *= f;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) tile[r][c8 + e] = v[e];
   }
@@ -249,6 +261,19 @@ __device__ __forceinline__ typename Mma<CT>::frag ident_qs(int l32, int h, int s
     return Mma<CT>::pack(v);
   } else {
     return (16 * h + s == l32) ? 1.f : 0.f;
+  }
+}
+
+// B operand that appends a ones column to a product over 32 k slots: column 0
+// of the 32-wide output tile receives the sum of the A operand's row over k.
+template <typename CT>
+__device__ __forceinline__ typename Mma<CT>::frag ones_col_frag(int l32) {
+  if constexpr (sizeof(CT) == 2) {
+    const float v = l32 == 0 ? 1.f : 0.f;
+    const float w[8] = {v, v, v, v, v, v, v, v};
+    return Mma<CT>::pack(w);
+  } else {
+    return l32 == 0 ? 1.f : 0.f;
   }
 }
 
