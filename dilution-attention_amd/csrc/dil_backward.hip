@@ -232,9 +232,12 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   auto step = [&](int qt, int buf, float cin, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     const float* st = st_s[buf];
-    RowFrag<CT, D> qf;
+    RowFrag<CT, D> qf, dof;
     lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
+    lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
+    // both score-shaped products first: dO V^T runs under the p / demand chain
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
     float lz[16], p[16], x[16];
     lds_read16(st + 16 * h, lz);
 #pragma unroll
@@ -262,9 +265,6 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
       for (int t = 0; t < kDTiles<D>; ++t)
         dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
     }
-    RowFrag<CT, D> dof;
-    lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
     float db[16];
     lds_read16(st + kTileQ + 16 * h, db);
 #pragma unroll
@@ -388,9 +388,12 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
   auto step = [&](int kt, int buf, float cin, float sin, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     const float* st = rs_s[wave];
-    RowFrag<CT, D> kf;
+    RowFrag<CT, D> kf, vf;
     lds_row_frag<CT, D>(kf, k_s[buf], rho(l32), h);
+    lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
+    // both score-shaped products first: dO V^T runs under the p / demand chain
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
     float lz[16], p[16], x[16];
     lds_read16(st + 16 * h, lz);
 #pragma unroll
@@ -410,9 +413,6 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
       x[i] = fast_rcp(x[i]);                     // inv
       sh[i] = p[i] * x[i];
     }
-    RowFrag<CT, D> vf;
-    lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
     float db[16], ds[16];
     lds_read16(st + kTileQ + 16 * h, db);
 #pragma unroll

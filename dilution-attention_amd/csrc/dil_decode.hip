@@ -24,9 +24,12 @@ namespace dil {
 
 namespace {
 
-constexpr int kDecThreads = 256;
+// Measured on MI355X at 128K context, B16 H16 d64 bf16 (sweep over 128-1024
+// threads, 1-4 rows in flight, 512-8192-key chunks): 1024-thread workgroups
+// with two rows in flight per lane over 2048-key chunks stream fastest.
+constexpr int kDecThreads = 1024;
 constexpr int kDecWaves = kDecThreads / 64;
-constexpr int kDecUnroll = 2;          // cached rows in flight per lane (measured best)
+constexpr int kDecUnroll = 2;          // cached rows in flight per lane
 
 template <int D>
 struct DecLayout {
@@ -35,18 +38,31 @@ struct DecLayout {
   static constexpr int kRowsPerBlock = kRowsPerWave * kDecWaves;
 };
 
-// Sum over the kLanesPerRow lanes that share one cached row.
+// Sum over the kLanesPerRow lanes that share one cached row, with DPP lane
+// moves (no LDS traffic).  The full sum is guaranteed only in the first lane
+// of each row group (lane % LPR == 0), the only lane that consumes it.
 template <int LPR>
 __device__ __forceinline__ float row_reduce(float x) {
-#pragma unroll
-  for (int o = 1; o < LPR; o <<= 1) x += __shfl_xor(x, o, 64);
+  constexpr int kQuadXor1 = 0xB1;      // quad_perm [1, 0, 3, 2]
+  constexpr int kQuadXor2 = 0x4E;      // quad_perm [2, 3, 0, 1]
+  constexpr int kRowShl4 = 0x104;      // row_shl:4
+  constexpr int kRowShl8 = 0x108;      // row_shl:8
+  if constexpr (LPR >= 2)
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQuadXor1, 0xF, 0xF, true));
+  if constexpr (LPR >= 4)
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQuadXor2, 0xF, 0xF, true));
+  if constexpr (LPR >= 8)
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowShl4, 0xF, 0xF, true));
+  if constexpr (LPR >= 16)
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowShl8, 0xF, 0xF, true));
   return x;
 }
 
-// 8 consecutive cached elements of storage dtype `dt` as fp32, read with a
+// 8 consecutive cached elements of storage dtype DT as fp32, read with a
 // non-temporal hint (the cache is streamed once per step).
-__device__ __forceinline__ void load8_stream(const void* base, int64_t idx, int dt, float (&o)[8]) {
-  if (dt == DT_F32) {
+template <int DT>
+__device__ __forceinline__ void load8_stream(const void* base, int64_t idx, float (&o)[8]) {
+  if constexpr (DT == DT_F32) {
     const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + idx);
     const floatx4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
     o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
@@ -56,15 +72,15 @@ __device__ __forceinline__ void load8_stream(const void* base, int64_t idx, int 
         reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(base) + idx));
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      o[e] = (dt == DT_BF16) ? bf16_bits_to_f32(r[e]) : f16_bits_to_f32(r[e]);
+      o[e] = (DT == DT_BF16) ? bf16_bits_to_f32(r[e]) : f16_bits_to_f32(r[e]);
   }
 }
 
-template <int D>
+template <int D, int DT>
 __global__ __launch_bounds__(kDecThreads) void dec_stats(
     const void* __restrict__ q1, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
     float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
-    int dt, float qscale) {
+    float qscale) {
   using L = DecLayout<D>;
   const int64_t slice = blockIdx.y;
   const int c = blockIdx.x;
@@ -74,7 +90,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_stats(
   const int64_t j1 = min(j0 + chunk, length);
 
   float q[8];
-  load8_f32(q1, slice * q_sn + sub * 8, dt, q);
+  load8_f32(q1, slice * q_sn + sub * 8, DT, q);
 #pragma unroll
   for (int e = 0; e < 8; ++e) q[e] *= qscale;
 
@@ -89,7 +105,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_stats(
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
       ok[u] = j < j1;
-      if (ok[u]) load8_stream(kc, kbase + j * D, dt, kv[u]);
+      if (ok[u]) load8_stream<DT>(kc, kbase + j * D, kv[u]);
     }
     float a[U];
 #pragma unroll
@@ -135,11 +151,11 @@ __global__ __launch_bounds__(kDecThreads) void dec_stats(
   }
 }
 
-template <int D>
+template <int D, int DT>
 __global__ __launch_bounds__(kDecThreads) void dec_apply(
     const void* __restrict__ vc, int64_t kv_sn, float* __restrict__ committed, int64_t c_sn,
     const float* __restrict__ aff, const float2* __restrict__ part, float* __restrict__ part_out,
-    int64_t length, int64_t chunk, int nchunk, int dt) {
+    int64_t length, int64_t chunk, int nchunk) {
   using L = DecLayout<D>;
   const int64_t slice = blockIdx.y;
   const int c = blockIdx.x;
@@ -176,7 +192,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
       const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
       ok[u] = j < j1;
       if (ok[u]) {
-        load8_stream(vc, vbase + j * D, dt, vv[u]);
+        load8_stream<DT>(vc, vbase + j * D, vv[u]);
         a[u] = arow[j];
         cm[u] = crow[j];
       }
@@ -250,16 +266,14 @@ __global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part
   if (d < D) store_as(out, slice * o_sn + d, dt, ((t0 + t1) + (t2 + t3)) / (tot_s + kEps));
 }
 
-// Keys per workgroup.  Measured on MI355X at 128K context, B16 H16 d64:
-// 1024-key chunks (32768 workgroups) with two rows in flight per lane stream
-// fastest; larger chunks or deeper unrolling lose occupancy.
+// Keys per workgroup (see kDecThreads).
 int64_t decode_chunk(int64_t n, int64_t length) {
   (void)n;
   (void)length;
-  return 1024;
+  return 2048;
 }
 
-template <int D>
+template <int D, int DT>
 int launch_decode(const DecodeArgs& a) {
   const int64_t chunk = decode_chunk(a.n, a.length);
   const int nchunk = static_cast<int>((a.length + chunk - 1) / chunk);
@@ -273,12 +287,12 @@ int launch_decode(const DecodeArgs& a) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   dim3 grid(nchunk, static_cast<unsigned>(a.n));
   DIL_TIMED("dec_stats", st,
-            dec_stats<D><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff, part,
-                                                       a.length, chunk, nchunk, a.dtype, qscale));
+            dec_stats<D, DT><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff,
+                                                           part, a.length, chunk, nchunk, qscale));
   DIL_TIMED("dec_apply", st,
-            dec_apply<D><<<grid, kDecThreads, 0, st>>>(a.v_cache, a.kv_sn, a.committed, a.c_sn, aff,
-                                                       part, part_out, a.length, chunk, nchunk,
-                                                       a.dtype));
+            dec_apply<D, DT><<<grid, kDecThreads, 0, st>>>(a.v_cache, a.kv_sn, a.committed, a.c_sn,
+                                                           aff, part, part_out, a.length, chunk,
+                                                           nchunk));
   DIL_TIMED("dec_finish", st,
             dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
                                                                              a.o_sn, a.dtype));
@@ -295,12 +309,22 @@ int64_t decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
                               align_up(sizeof(float) * n * nchunk * (head_dim + 1)));
 }
 
+template <int D>
+int decode_dtype(const DecodeArgs& a) {
+  switch (a.dtype) {
+    case DT_F32: return launch_decode<D, DT_F32>(a);
+    case DT_BF16: return launch_decode<D, DT_BF16>(a);
+    case DT_F16: return launch_decode<D, DT_F16>(a);
+    default: return kErrDtype;
+  }
+}
+
 int decode_step(const DecodeArgs& a) {
   switch (a.head_dim) {
-    case 16: return launch_decode<16>(a);
-    case 32: return launch_decode<32>(a);
-    case 64: return launch_decode<64>(a);
-    case 128: return launch_decode<128>(a);
+    case 16: return decode_dtype<16>(a);
+    case 32: return decode_dtype<32>(a);
+    case 64: return decode_dtype<64>(a);
+    case 128: return decode_dtype<128>(a);
     default: return kErrHeadDim;
   }
 }

@@ -54,10 +54,10 @@ def test_decode_matches_oracle_rows(dtype, head_dim):
     assert committed[:, :, total:].abs().max().item() == 0
 
 
-@pytest.mark.parametrize("length", [1, 1023, 1024, 1025, 5000])
+@pytest.mark.parametrize("length", [1, 1023, 1024, 1025, 2047, 2048, 2049, 5000, 9000])
 def test_decode_long_context_multi_chunk(length):
-    """Lengths that cross the 1024-key chunk boundary of the split-K decode,
-    with a synthetic non-negative demand vector."""
+    """Lengths around the split-K decode's chunk boundaries (2048 keys per
+    workgroup) and several chunks, with a synthetic non-negative demand vector."""
     from dilution import kernels
 
     batch, heads, d = 1, 3, 64
