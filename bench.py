@@ -21,6 +21,8 @@ The same line carries
   * ``kernels``: per-kernel launches and average milliseconds of that pass;
   * ``sdpa``: torch's causal flash attention fwd+bwd at the same shape and
     dtype on the same GPU, timed the same way (the >= 0.6x comparator);
+  * ``prefill``: chunked prefill of a 16K prompt in 2K chunks (BASELINE
+    configs[3]: B=16 H=16 d=64 bf16), algorithmic TFLOP/s;
   * ``decode``: the cached decode step at 128K context (
     B=16 H=16 d=64 bf16), HBM GB/s over B H L (4d + 8) algorithmic bytes per
     step, with its own roofline object;
@@ -97,6 +99,8 @@ def parse_args():
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--decode-context", type=int, default=131072)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -270,6 +274,39 @@ def bench_decode(args, dev):
             "kernels": per_kernel}
 
 
+def bench_prefill(args, dev):
+    """Chunked prefill: B16 H16 d64 bf16, a 16384-token
+    prompt in 2048-token chunks through ``dilution_prefill_chunk`` with the
+    fp32 demand carried across chunks; algorithmic 2 B H T^2 d FLOPs per
+    prompt (causal QK^T and share @ V)."""
+    import torch
+
+    from dilution import kernels
+
+    batch, heads, d, seq, chunk = 16, 16, 64, 16384, 2048
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(batch, heads, seq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    kc = torch.randn(batch, heads, seq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    vc = torch.randn(batch, heads, seq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    com = torch.zeros(batch, heads, seq, device=dev)
+
+    def prompt():
+        com.zero_()
+        for start in range(0, seq, chunk):
+            kernels.dilution_prefill_chunk(q[:, :, start:start + chunk], kc, vc, com, start,
+                                           dot_precision="bf16")
+
+    prompt()
+    ms = timed(prompt, args.prefill_steps)
+    tflops = 2.0 * batch * heads * seq * seq * d / (ms * 1e-3) / 1e12
+    log(f"prefill 16K in 2K chunks: {ms:.2f} ms/prompt, {tflops:.1f} TFLOP/s")
+    return {"metric": "chunked prefill TFLOP/s", "value": round(tflops, 2), "unit": "TFLOP/s",
+            "ms_per_prompt": round(ms, 3), "steps": args.prefill_steps,
+            "pct_of_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+            "config": {"workload": "C4 chunked prefill", "batch": batch, "heads": heads,
+                       "prompt": seq, "chunk": chunk, "head_dim": d, "dtype": "bf16"}}
+
+
 def cpu_baseline(shape):
     """The fp32 CPU oracle, fwd+bwd through torch autograd, on one (batch,
     head) slice of the workload (the slices are independent and identical in
@@ -353,6 +390,9 @@ def main() -> int:
     if not args.no_decode:
         torch.cuda.empty_cache()
         line["decode"] = bench_decode(args, dev)
+    if not args.no_prefill:
+        torch.cuda.empty_cache()
+        line["prefill"] = bench_prefill(args, dev)
     if not args.no_cpu_baseline:
         torch.cuda.empty_cache()
         line["cpu_baseline"] = cpu_baseline(tr["shape"])

@@ -4,6 +4,6 @@ Royer-Research-Labs/Dilution-Attention on hand-written gfx950 HIP kernels.
 `dilution.kernels` is the drop-in for the reference module of the same name.
 """
 
-from . import kernels
+from . import cache, kernels
 
-__all__ = ["kernels"]
+__all__ = ["cache", "kernels"]

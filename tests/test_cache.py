@@ -1,0 +1,86 @@
+"""Prefill -> decode hand-off through the cache dict (dilution.cache).
+
+Reference patterns: tests/test_kernels.py:205-273 (decode rows equal the
+full-sequence rows, the demand vector equals the column sums, spare capacity
+untouched) and tests/test_model.py:99-110 (cached decode == teacher-forced
+full forward).  Here the prompt is prefilled in chunks (the C4 pattern, at a
+small size), then decoded token by token, and every row is compared with the
+float64 oracle of the whole sequence.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import max_abs, needs_gpu
+from oracle import dilution_oracle as orc
+
+
+def test_cache_requires_gpu_tensors():
+    from dilution import cache as dc
+
+    q = torch.zeros(1, 1, 4, 64)
+    with pytest.raises(RuntimeError):
+        dc.begin_cache(q, q, q)
+
+
+def test_alloc_and_append_follow_the_reference_protocol():
+    """Capacity rule max(capacity, T) and the error past capacity
+    (model.py:76-93) are host logic: checked on CPU tensors."""
+    from dilution import cache as dc
+
+    k = torch.randn(1, 2, 5, 8)
+    c = dc.alloc_cache(k, k, capacity=3)
+    assert c["k"].shape[2] == 5 and c["len"] == 5 and c["committed"].dtype == torch.float32
+    c = dc.alloc_cache(k, k, capacity=7)
+    assert c["k"].shape[2] == 7
+    one = torch.randn(1, 2, 1, 8)
+    assert dc.append_kv(c, one, one) == 6
+    assert torch.equal(c["k"][:, :, 5], one[:, :, 0])
+    dc.append_kv(c, one, one)
+    with pytest.raises(ValueError):
+        dc.append_kv(c, one, one)
+
+
+@pytest.mark.gpu
+@needs_gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("chunk", [None, 96, 256])
+def test_chunked_prefill_then_decode_matches_full_rows(dtype, tol, chunk):
+    from dilution import cache as dc
+
+    batch, heads, d, prompt, steps = 2, 4, 64, 600, 12
+    total = prompt + steps
+    q, k, v = orc.make_inputs((batch, heads, total, d), seed=31 + (chunk or 0))
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    full = orc.attention_f64(q, k, v)                   # oracle on the same (rounded) values
+    qg, kg, vg = (x.cuda() for x in (q, k, v))
+    y, cache = dc.begin_cache(qg[:, :, :prompt], kg[:, :, :prompt], vg[:, :, :prompt],
+                              capacity=total + 5, chunk=chunk)
+    assert y.dtype == dtype and cache["len"] == prompt
+    assert max_abs(y, full[:, :, :prompt]) < tol
+    want = orc.demand_totals(q[:, :, :prompt], k[:, :, :prompt])
+    assert max_abs(cache["committed"][:, :, :prompt], want) < 1e-5
+    for t in range(prompt, total):
+        out = dc.step_cache(qg[:, :, t:t + 1], kg[:, :, t:t + 1], vg[:, :, t:t + 1], cache)
+        assert out.dtype == dtype
+        assert max_abs(out[:, :, 0], full[:, :, t]) < tol, t
+    assert max_abs(cache["committed"][:, :, :total], orc.demand_totals(q, k)) < 1e-5
+    assert cache["committed"][:, :, total:].abs().max().item() == 0
+    assert cache["len"] == total
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_chunked_and_one_call_prefill_agree():
+    """Chunked prefill reproduces the reference's one-call prefill: the same
+    outputs (fp32 rounding apart) and the same demand buffer."""
+    from dilution import cache as dc
+
+    q, k, v = (x.cuda() for x in orc.make_inputs((1, 3, 777, 64), seed=41))
+    y1, c1 = dc.begin_cache(q, k, v, capacity=800, dot_precision="ieee")
+    y2, c2 = dc.begin_cache(q, k, v, capacity=800, chunk=100, dot_precision="ieee")
+    assert max_abs(y1, y2) < 1e-5
+    assert max_abs(c1["committed"], c2["committed"]) < 1e-5
+    assert torch.equal(c1["k"], c2["k"]) and torch.equal(c1["v"], c2["v"])
