@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                     [--decode-steps K] [--decode-context L] [--no-decode]
-                    [--no-sdpa] [--no-cpu-baseline]
+                    [--no-sdpa] [--no-lm] [--no-cpu-baseline]
 
 Prints ONE JSON line.  The headline workload (default ``train16k``,
 BASELINE configs[2]) is the operator's training step, fwd+bwd through
@@ -26,6 +26,9 @@ The same line carries
   * ``decode``: the cached decode step at 128K context (
     B=16 H=16 d=64 bf16), HBM GB/s over B H L (4d + 8) algorithmic bytes per
     step, with its own roofline object;
+  * ``lm``: the whole random-init LM on this
+    operator: training-step, prefill and greedy-decode tokens/s with the
+    attention kernels' share of each;
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
     formula) timed on this host's cores on one (batch, head) slice of the
     headline workload.
@@ -102,6 +105,9 @@ def parse_args():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--no-lm", action="store_true")
+    ap.add_argument("--lm-train-steps", type=int, default=2)
+    ap.add_argument("--lm-decode-tokens", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (3 times): the reference kernel for "
@@ -307,6 +313,86 @@ def bench_prefill(args, dev):
                        "prompt": seq, "chunk": chunk, "head_dim": d, "dtype": "bf16"}}
 
 
+def bench_lm(args, dev):
+    """Whole random-init LM: 12 layers, d_model 1024,
+    16 heads of 64, SwiGLU 4x, RMSNorm, vocab 50304, no position encoding,
+    bf16 weights N(0, 0.02), uniform token ids.  One training step (forward,
+    backward, AdamW) at B4 T16384, timed over ``--lm-train-steps`` steps;
+    then a 16384-token prefill at B8 (2048-token chunks into the caches) and
+    ``--lm-decode-tokens`` greedy decode steps.  The attention kernels' share
+    of each phase comes from the library's per-launch events."""
+    import torch
+
+    from dilution.lm import DilutionLM, LMConfig
+
+    torch.manual_seed(6)
+    cfg = LMConfig()
+    model = DilutionLM(cfg).to(device=dev, dtype=torch.bfloat16)
+    n_params = sum(p.numel() for p in model.parameters())
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.1)
+    g = torch.Generator(device=dev).manual_seed(6)
+    tb, tt = 4, 16384
+    idx = torch.randint(0, cfg.vocab_size, (tb, tt + 1), device=dev, generator=g)
+
+    def train_step():
+        opt.zero_grad(set_to_none=True)
+        _, loss = model(idx[:, :-1], idx[:, 1:])
+        loss.backward()
+        opt.step()
+        return loss
+
+    model.train()
+    loss0 = train_step().item()
+    ms_train = timed(train_step, args.lm_train_steps)
+    attn_train = sum(tot for _, tot in kernel_pass(train_step, 1).values())
+    log(f"lm train step B{tb} T{tt}: {ms_train:.1f} ms, attention kernels {attn_train:.1f} ms, "
+        f"first loss {loss0:.3f}")
+    del opt, idx
+    for p in model.parameters():
+        p.grad = None
+    torch.cuda.empty_cache()
+
+    model.eval()
+    pb, pt, new = 8, 16384, args.lm_decode_tokens
+    prompt = torch.randint(0, cfg.vocab_size, (pb, pt), device=dev, generator=g)
+    model.prefill(prompt[:, :2048], capacity=2048)         # warm the kernels and allocator
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits, caches = model.prefill(prompt, capacity=pt + new)
+    torch.cuda.synchronize()
+    ms_prefill = (time.perf_counter() - t0) * 1e3
+    tok = logits[:, -1].float().argmax(-1, keepdim=True)
+
+    def decode_one():
+        nonlocal logits, tok
+        logits = model.decode_step(tok, caches)
+        tok = logits[:, -1].float().argmax(-1, keepdim=True)
+
+    decode_one()
+    with torch.no_grad():
+        ms_decode = timed(decode_one, new - 2)
+        attn_decode = sum(tot for _, tot in kernel_pass(decode_one, 1).values())
+    log(f"lm prefill B{pb} T{pt}: {ms_prefill:.1f} ms; decode {ms_decode:.3f} ms/token-step "
+        f"(attention kernels {attn_decode:.3f} ms)")
+    return {"metric": "whole-LM tokens/s",
+            "train": {"tokens_per_s": round(tb * tt / (ms_train * 1e-3), 1),
+                      "ms_per_step": round(ms_train, 2), "steps": args.lm_train_steps,
+                      "attention_kernels_ms_per_step": round(attn_train, 2),
+                      "first_loss": round(loss0, 4), "batch": tb, "seq_len": tt,
+                      "includes": "forward, backward, AdamW step"},
+            "prefill": {"tokens_per_s": round(pb * pt / (ms_prefill * 1e-3), 1),
+                        "ms": round(ms_prefill, 2), "batch": pb, "prompt": pt,
+                        "chunk": cfg.prefill_chunk},
+            "decode": {"tokens_per_s": round(pb / (ms_decode * 1e-3), 1),
+                       "ms_per_token_step": round(ms_decode, 4), "timed_steps": new - 2,
+                       "attention_kernels_ms_per_step": round(attn_decode, 4), "batch": pb,
+                       "context": f"{pt + 1}..{pt + new - 1}", "greedy": True},
+            "config": {"workload": "C5 whole-LM", "layers": cfg.n_layers, "d_model": cfg.d_model,
+                       "heads": cfg.n_heads, "head_dim": cfg.d_model // cfg.n_heads,
+                       "mlp": "SwiGLU 4x", "norm": "RMSNorm", "vocab": cfg.vocab_size,
+                       "params": n_params, "dtype": "bf16", "data": "synthetic uniform token ids"}}
+
+
 def cpu_baseline(shape):
     """The fp32 CPU oracle, fwd+bwd through torch autograd, on one (batch,
     head) slice of the workload (the slices are independent and identical in
@@ -393,6 +479,9 @@ def main() -> int:
     if not args.no_prefill:
         torch.cuda.empty_cache()
         line["prefill"] = bench_prefill(args, dev)
+    if not args.no_lm:
+        torch.cuda.empty_cache()
+        line["lm"] = bench_lm(args, dev)
     if not args.no_cpu_baseline:
         torch.cuda.empty_cache()
         line["cpu_baseline"] = cpu_baseline(tr["shape"])

@@ -1,0 +1,194 @@
+"""A decoder-only LM whose attention is the HIP dilution operator.
+
+This is the whole-model harness for the operator: the caller side of the hot
+path, at the shape of the model-level benchmark (12 layers, d_model 1024,
+16 heads of 64, SwiGLU MLP, RMSNorm, no position encoding, vocab 50304, bf16
+weights).  It follows the reference's module layout and cache protocol
+(src/dilution/model.py):
+
+* ``DilutionAttention``: fused q/k/v projection, the operator, output
+  projection (model.py:120-257 with ``use_kernel`` on: training forward
+  through ``kernels.dilution_attention``, no-grad forward through
+  ``kernels.dilution_attention_forward``, prefill and cached decode through
+  ``dilution.cache``);
+* ``Block``: pre-norm residual attention + MLP (model.py:317-339);
+* ``DilutionLM``: embedding tied to the LM head, blocks, final norm;
+  ``forward(idx, targets)`` -> (logits, loss), ``prefill``, ``decode_step``
+  and greedy ``generate`` (model.py:342-512).
+
+The reference normalises with LayerNorm and sizes SwiGLU at 8/3 d_model; the
+model-level benchmark configuration asks for RMSNorm and a 4x SwiGLU, which
+``LMConfig`` selects here.  There is no eager fallback: the attention layers
+run only on the HIP kernels.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import cache as dcache
+from . import kernels
+
+
+@dataclass
+class LMConfig:
+    vocab_size: int = 50304
+    n_layers: int = 12
+    d_model: int = 1024
+    n_heads: int = 16
+    mlp_ratio: float = 4.0          # SwiGLU hidden = mlp_ratio * d_model
+    norm: str = "rms"               # "rms" or "layer"
+    prefill_chunk: int | None = 2048
+
+    def __post_init__(self):
+        if self.d_model % self.n_heads:
+            raise ValueError("d_model must be divisible by n_heads")
+        if self.norm not in ("rms", "layer"):
+            raise ValueError("norm must be 'rms' or 'layer'")
+
+
+def _norm(cfg: LMConfig) -> nn.Module:
+    if cfg.norm == "rms":
+        return nn.RMSNorm(cfg.d_model, eps=1e-5)
+    return nn.LayerNorm(cfg.d_model, eps=1e-5)
+
+
+class DilutionAttention(nn.Module):
+    def __init__(self, cfg: LMConfig):
+        super().__init__()
+        self.n_heads = cfg.n_heads
+        self.d_model = cfg.d_model
+        self.c_attn = nn.Linear(cfg.d_model, 3 * cfg.d_model, bias=False)
+        self.c_proj = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
+        self.prefill_chunk = cfg.prefill_chunk
+
+    def _split_heads(self, x: torch.Tensor):
+        batch, seq, _ = x.shape
+        q, k, v = self.c_attn(x).split(self.d_model, dim=2)
+        shape = (batch, seq, self.n_heads, self.d_model // self.n_heads)
+        return (t.view(shape).transpose(1, 2) for t in (q, k, v))
+
+    def _merge_heads(self, y: torch.Tensor, batch: int, seq: int) -> torch.Tensor:
+        return self.c_proj(y.transpose(1, 2).contiguous().view(batch, seq, self.d_model))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        batch, seq, _ = x.shape
+        q, k, v = self._split_heads(x)
+        prec = "bf16" if q.dtype == torch.bfloat16 else "tf32"
+        if torch.is_grad_enabled():
+            y = kernels.dilution_attention(q, k, v, dot_precision=prec)
+        else:
+            y = kernels.dilution_attention_forward(q, k, v, dot_precision=prec)
+        return self._merge_heads(y.to(x.dtype), batch, seq)
+
+    def begin_cache(self, x: torch.Tensor, capacity: int | None = None):
+        batch, seq, _ = x.shape
+        q, k, v = self._split_heads(x)
+        y, cache = dcache.begin_cache(q, k.contiguous(), v.contiguous(), capacity=capacity,
+                                      chunk=self.prefill_chunk)
+        return self._merge_heads(y.to(x.dtype), batch, seq), cache
+
+    def step_cache(self, x1: torch.Tensor, cache: dict) -> torch.Tensor:
+        batch = x1.shape[0]
+        q1, k1, v1 = self._split_heads(x1)
+        y = dcache.step_cache(q1, k1, v1, cache)
+        return self._merge_heads(y.to(x1.dtype), batch, 1)
+
+
+class SwiGLUMLP(nn.Module):
+    def __init__(self, cfg: LMConfig):
+        super().__init__()
+        hidden = int(cfg.mlp_ratio * cfg.d_model)
+        self.gate_proj = nn.Linear(cfg.d_model, hidden, bias=False)
+        self.up_proj = nn.Linear(cfg.d_model, hidden, bias=False)
+        self.down_proj = nn.Linear(hidden, cfg.d_model, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: LMConfig):
+        super().__init__()
+        self.ln_1 = _norm(cfg)
+        self.attn = DilutionAttention(cfg)
+        self.ln_2 = _norm(cfg)
+        self.mlp = SwiGLUMLP(cfg)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x + self.attn(self.ln_1(x))
+        return x + self.mlp(self.ln_2(x))
+
+    def begin_cache(self, x: torch.Tensor, capacity: int | None = None):
+        y, cache = self.attn.begin_cache(self.ln_1(x), capacity)
+        x = x + y
+        return x + self.mlp(self.ln_2(x)), cache
+
+    def step_cache(self, x1: torch.Tensor, cache: dict) -> torch.Tensor:
+        x1 = x1 + self.attn.step_cache(self.ln_1(x1), cache)
+        return x1 + self.mlp(self.ln_2(x1))
+
+
+class DilutionLM(nn.Module):
+    """Decoder-only LM, tied embeddings, no position encoding (the demand
+    cumsum supplies the order asymmetry)."""
+
+    def __init__(self, cfg: LMConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.wte = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        self.h = nn.ModuleList([Block(cfg) for _ in range(cfg.n_layers)])
+        self.ln_f = _norm(cfg)
+        self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
+        self.wte.weight = self.lm_head.weight
+        self.apply(self._init_weights)
+
+    @staticmethod
+    def _init_weights(module: nn.Module) -> None:
+        if isinstance(module, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    def forward(self, idx: torch.Tensor, targets: torch.Tensor | None = None):
+        x = self.wte(idx)
+        for block in self.h:
+            x = block(x)
+        x = self.ln_f(x)
+        if targets is None:
+            return self.lm_head(x[:, [-1], :]), None
+        logits = self.lm_head(x)
+        loss = F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.reshape(-1),
+                               ignore_index=-100)
+        return logits, loss
+
+    @torch.no_grad()
+    def prefill(self, idx: torch.Tensor, capacity: int | None = None):
+        x = self.wte(idx)
+        caches = []
+        for block in self.h:
+            x, cache = block.begin_cache(x, capacity)
+            caches.append(cache)
+        return self.lm_head(self.ln_f(x[:, [-1], :])), caches
+
+    @torch.no_grad()
+    def decode_step(self, token: torch.Tensor, caches) -> torch.Tensor:
+        x = self.wte(token)
+        for block, cache in zip(self.h, caches):
+            x = block.step_cache(x, cache)
+        return self.lm_head(self.ln_f(x))
+
+    @torch.no_grad()
+    def generate(self, idx: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
+        """Greedy decoding with caches sized prompt + max_new_tokens
+        (model.py:496)."""
+        logits, caches = self.prefill(idx, capacity=idx.shape[1] + max_new_tokens)
+        tokens = idx
+        for step in range(max_new_tokens):
+            nxt = logits[:, -1, :].float().argmax(dim=-1, keepdim=True)
+            tokens = torch.cat([tokens, nxt], dim=1)
+            if step + 1 < max_new_tokens:
+                logits = self.decode_step(nxt, caches)
+        return tokens
