@@ -28,7 +28,8 @@ The same line carries
     step, with its own roofline object;
   * ``lm``: the whole random-init LM on this
     operator: training-step, prefill and greedy-decode tokens/s with the
-    attention kernels' share of each;
+    attention kernels' share of each, and the same LM with softmax (SDPA)
+    attention as the comparator;
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
     formula) timed on this host's cores on one (batch, head) slice of the
     headline workload.
@@ -313,22 +314,17 @@ def bench_prefill(args, dev):
                        "prompt": seq, "chunk": chunk, "head_dim": d, "dtype": "bf16"}}
 
 
-def bench_lm(args, dev):
-    """Whole random-init LM (BASELINE configs[4]): 12 layers, d_model 1024,
-    16 heads of 64, SwiGLU 4x, RMSNorm, vocab 50304, no position encoding,
-    bf16 weights N(0, 0.02), uniform token ids.  One training step (forward,
-    backward, AdamW) at B4 T16384, timed over ``--lm-train-steps`` steps;
-    then a 16384-token prefill at B8 (2048-token chunks into the caches) and
-    ``--lm-decode-tokens`` greedy decode steps.  The attention kernels' share
-    of each phase comes from the library's per-launch events."""
+def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
+    """One training step (forward, backward, AdamW) at B4 T16384, timed over
+    ``--lm-train-steps`` steps, then a 16384-token prefill at B8 and
+    ``decode_tokens`` greedy decode steps, for an all-``kind`` stack."""
     import torch
 
     from dilution.lm import DilutionLM, LMConfig
 
     torch.manual_seed(6)
-    cfg = LMConfig()
+    cfg = LMConfig(attention=kind)
     model = DilutionLM(cfg).to(device=dev, dtype=torch.bfloat16)
-    n_params = sum(p.numel() for p in model.parameters())
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.1)
     g = torch.Generator(device=dev).manual_seed(6)
     tb, tt = 4, 16384
@@ -345,20 +341,20 @@ def bench_lm(args, dev):
     loss0 = train_step().item()
     ms_train = timed(train_step, args.lm_train_steps)
     attn_train = sum(tot for _, tot in kernel_pass(train_step, 1).values())
-    log(f"lm train step B{tb} T{tt}: {ms_train:.1f} ms, attention kernels {attn_train:.1f} ms, "
-        f"first loss {loss0:.3f}")
+    log(f"lm[{kind}] train step B{tb} T{tt}: {ms_train:.1f} ms, dilution kernels "
+        f"{attn_train:.1f} ms, first loss {loss0:.3f}")
     del opt, idx
     for p in model.parameters():
         p.grad = None
     torch.cuda.empty_cache()
 
     model.eval()
-    pb, pt, new = 8, 16384, args.lm_decode_tokens
+    pb, pt = 8, 16384
     prompt = torch.randint(0, cfg.vocab_size, (pb, pt), device=dev, generator=g)
     model.prefill(prompt[:, :2048], capacity=2048)         # warm the kernels and allocator
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    logits, caches = model.prefill(prompt, capacity=pt + new)
+    logits, caches = model.prefill(prompt, capacity=pt + decode_tokens)
     torch.cuda.synchronize()
     ms_prefill = (time.perf_counter() - t0) * 1e3
     tok = logits[:, -1].float().argmax(-1, keepdim=True)
@@ -369,28 +365,50 @@ def bench_lm(args, dev):
         tok = logits[:, -1].float().argmax(-1, keepdim=True)
 
     decode_one()
-    with torch.no_grad():
-        ms_decode = timed(decode_one, new - 2)
-        attn_decode = sum(tot for _, tot in kernel_pass(decode_one, 1).values())
-    log(f"lm prefill B{pb} T{pt}: {ms_prefill:.1f} ms; decode {ms_decode:.3f} ms/token-step "
-        f"(attention kernels {attn_decode:.3f} ms)")
-    return {"metric": "whole-LM tokens/s",
-            "train": {"tokens_per_s": round(tb * tt / (ms_train * 1e-3), 1),
-                      "ms_per_step": round(ms_train, 2), "steps": args.lm_train_steps,
-                      "attention_kernels_ms_per_step": round(attn_train, 2),
-                      "first_loss": round(loss0, 4), "batch": tb, "seq_len": tt,
-                      "includes": "forward, backward, AdamW step"},
-            "prefill": {"tokens_per_s": round(pb * pt / (ms_prefill * 1e-3), 1),
-                        "ms": round(ms_prefill, 2), "batch": pb, "prompt": pt,
-                        "chunk": cfg.prefill_chunk},
-            "decode": {"tokens_per_s": round(pb / (ms_decode * 1e-3), 1),
-                       "ms_per_token_step": round(ms_decode, 4), "timed_steps": new - 2,
-                       "attention_kernels_ms_per_step": round(attn_decode, 4), "batch": pb,
-                       "context": f"{pt + 1}..{pt + new - 1}", "greedy": True},
-            "config": {"workload": "C5 whole-LM", "layers": cfg.n_layers, "d_model": cfg.d_model,
-                       "heads": cfg.n_heads, "head_dim": cfg.d_model // cfg.n_heads,
-                       "mlp": "SwiGLU 4x", "norm": "RMSNorm", "vocab": cfg.vocab_size,
-                       "params": n_params, "dtype": "bf16", "data": "synthetic uniform token ids"}}
+    ms_decode = timed(decode_one, decode_tokens - 2)
+    attn_decode = sum(tot for _, tot in kernel_pass(decode_one, 1).values())
+    log(f"lm[{kind}] prefill B{pb} T{pt}: {ms_prefill:.1f} ms; decode {ms_decode:.3f} "
+        f"ms/token-step (dilution kernels {attn_decode:.3f} ms)")
+    out = {"train": {"tokens_per_s": round(tb * tt / (ms_train * 1e-3), 1),
+                     "ms_per_step": round(ms_train, 2), "steps": args.lm_train_steps,
+                     "first_loss": round(loss0, 4), "batch": tb, "seq_len": tt,
+                     "includes": "forward, backward, AdamW step"},
+           "prefill": {"tokens_per_s": round(pb * pt / (ms_prefill * 1e-3), 1),
+                       "ms": round(ms_prefill, 2), "batch": pb, "prompt": pt},
+           "decode": {"tokens_per_s": round(pb / (ms_decode * 1e-3), 1),
+                      "ms_per_token_step": round(ms_decode, 4), "timed_steps": decode_tokens - 2,
+                      "batch": pb, "context": f"{pt + 1}..{pt + decode_tokens - 1}",
+                      "greedy": True}}
+    if kind == "dilution":
+        out["train"]["attention_kernels_ms_per_step"] = round(attn_train, 2)
+        out["prefill"]["chunk"] = cfg.prefill_chunk
+        out["decode"]["attention_kernels_ms_per_step"] = round(attn_decode, 4)
+    out["config"] = {"workload": "C5 whole-LM", "attention": kind, "layers": cfg.n_layers,
+                     "d_model": cfg.d_model, "heads": cfg.n_heads,
+                     "head_dim": cfg.d_model // cfg.n_heads, "mlp": "SwiGLU 4x",
+                     "norm": "RMSNorm", "vocab": cfg.vocab_size,
+                     "params": sum(p.numel() for p in model.parameters()), "dtype": "bf16",
+                     "data": "synthetic uniform token ids"}
+    del model, caches, logits
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_lm(args, dev):
+    """Whole random-init LM (BASELINE configs[4]): 12 layers, d_model 1024,
+    16 heads of 64, SwiGLU 4x, RMSNorm, vocab 50304, no position encoding,
+    bf16 weights N(0, 0.02), uniform token ids.  All-dilution on the HIP
+    operator, then the same stack with the softmax control (torch SDPA) in
+    every slot as the comparator (fewer decode steps).  The dilution kernels'
+    share of each phase comes from the library's per-launch events."""
+    res = _lm_phases(args, dev, "dilution", args.lm_decode_tokens)
+    res["metric"] = "whole-LM tokens/s"
+    if not args.no_sdpa:
+        try:
+            res["softmax_arm"] = _lm_phases(args, dev, "softmax", min(args.lm_decode_tokens, 130))
+        except Exception as exc:  # backend unavailable: report, do not fall back
+            res["softmax_arm"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
+    return res
 
 
 def cpu_baseline(shape):

@@ -11,6 +11,10 @@ weights).  It follows the reference's module layout and cache protocol
   through ``kernels.dilution_attention``, no-grad forward through
   ``kernels.dilution_attention_forward``, prefill and cached decode through
   ``dilution.cache``);
+* ``SoftmaxAttention``: the parameter-matched causal softmax control on
+  torch SDPA, with a plain KV cache (model.py:96-117), selected per layer by
+  ``LMConfig.attention`` / ``layer_attention`` as in the reference's
+  ``ModelConfig.layer_kinds`` (config.py:134-137);
 * ``Block``: pre-norm residual attention + MLP (model.py:317-339);
 * ``DilutionLM``: embedding tied to the LM head, blocks, final norm;
   ``forward(idx, targets)`` -> (logits, loss), ``prefill``, ``decode_step``
@@ -29,6 +33,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import cache as dcache
 from . import kernels
@@ -43,12 +48,27 @@ class LMConfig:
     mlp_ratio: float = 4.0          # SwiGLU hidden = mlp_ratio * d_model
     norm: str = "rms"               # "rms" or "layer"
     prefill_chunk: int | None = 2048
+    attention: str = "dilution"     # default slot type: "dilution" or "softmax"
+    layer_attention: list | None = None
 
     def __post_init__(self):
         if self.d_model % self.n_heads:
             raise ValueError("d_model must be divisible by n_heads")
         if self.norm not in ("rms", "layer"):
             raise ValueError("norm must be 'rms' or 'layer'")
+        if self.layer_attention is not None and len(self.layer_attention) != self.n_layers:
+            raise ValueError(f"layer_attention must list {self.n_layers} entries")
+        bad = sorted(set(self.layer_kinds()) - set(ATTENTION_TYPES))
+        if bad:
+            raise ValueError(f"attention kinds must be in {ATTENTION_TYPES}; got {bad}")
+
+    def layer_kinds(self) -> list[str]:
+        if self.layer_attention is not None:
+            return list(self.layer_attention)
+        return [self.attention] * self.n_layers
+
+
+ATTENTION_TYPES = ("dilution", "softmax")
 
 
 def _norm(cfg: LMConfig) -> nn.Module:
@@ -57,7 +77,10 @@ def _norm(cfg: LMConfig) -> nn.Module:
     return nn.LayerNorm(cfg.d_model, eps=1e-5)
 
 
-class DilutionAttention(nn.Module):
+class _AttentionBase(nn.Module):
+    """Fused q/k/v projection and output projection shared by both slot
+    types (model.py:41-93)."""
+
     def __init__(self, cfg: LMConfig):
         super().__init__()
         self.n_heads = cfg.n_heads
@@ -74,6 +97,41 @@ class DilutionAttention(nn.Module):
 
     def _merge_heads(self, y: torch.Tensor, batch: int, seq: int) -> torch.Tensor:
         return self.c_proj(y.transpose(1, 2).contiguous().view(batch, seq, self.d_model))
+
+
+def _sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool) -> torch.Tensor:
+    """torch SDPA; half-precision inputs are kept off the math backend, whose
+    batched products take a transposed bf16 operand."""
+    if q.dtype == torch.float32:
+        return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+
+class SoftmaxAttention(_AttentionBase):
+    """Causal softmax attention (torch SDPA): the parameter-matched control."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        batch, seq, _ = x.shape
+        q, k, v = self._split_heads(x)
+        return self._merge_heads(_sdpa(q, k, v, True), batch, seq)
+
+    def begin_cache(self, x: torch.Tensor, capacity: int | None = None):
+        batch, seq, _ = x.shape
+        q, k, v = self._split_heads(x)
+        y = self._merge_heads(_sdpa(q, k, v, True), batch, seq)
+        return y, dcache.alloc_cache(k, v, capacity)
+
+    def step_cache(self, x1: torch.Tensor, cache: dict) -> torch.Tensor:
+        batch = x1.shape[0]
+        q1, k1, v1 = self._split_heads(x1)
+        t = dcache.append_kv(cache, k1, v1)
+        y = _sdpa(q1, cache["k"][:, :, :t], cache["v"][:, :, :t], False)
+        return self._merge_heads(y, batch, 1)
+
+
+class DilutionAttention(_AttentionBase):
+    """The dilution operator on the HIP kernels (model.py:120-257)."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         batch, seq, _ = x.shape
@@ -111,11 +169,14 @@ class SwiGLUMLP(nn.Module):
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 
+_ATTENTION_CLASSES = {"dilution": DilutionAttention, "softmax": SoftmaxAttention}
+
+
 class Block(nn.Module):
-    def __init__(self, cfg: LMConfig):
+    def __init__(self, cfg: LMConfig, kind: str = "dilution"):
         super().__init__()
         self.ln_1 = _norm(cfg)
-        self.attn = DilutionAttention(cfg)
+        self.attn = _ATTENTION_CLASSES[kind](cfg)
         self.ln_2 = _norm(cfg)
         self.mlp = SwiGLUMLP(cfg)
 
@@ -134,14 +195,15 @@ class Block(nn.Module):
 
 
 class DilutionLM(nn.Module):
-    """Decoder-only LM, tied embeddings, no position encoding (the demand
-    cumsum supplies the order asymmetry)."""
+    """Decoder-only LM over dilution / softmax attention slots, tied
+    embeddings, no position encoding (in dilution layers the demand cumsum
+    supplies the order asymmetry)."""
 
     def __init__(self, cfg: LMConfig):
         super().__init__()
         self.cfg = cfg
         self.wte = nn.Embedding(cfg.vocab_size, cfg.d_model)
-        self.h = nn.ModuleList([Block(cfg) for _ in range(cfg.n_layers)])
+        self.h = nn.ModuleList([Block(cfg, kind) for kind in cfg.layer_kinds()])
         self.ln_f = _norm(cfg)
         self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
         self.wte.weight = self.lm_head.weight

@@ -5,7 +5,7 @@ the reference's tests/test_model.py:
   (test_model.py:46-56);
 * cached decode reproduces the teacher-forced full forward
   (test_model.py:99-110) -- here through chunked prefill and the HIP decode
-  step;
+  step, and through the softmax control's KV cache in mixed stacks;
 * a bf16 training step produces a finite loss and finite gradients in
   every parameter.
 """
@@ -18,10 +18,11 @@ import torch
 from gpu_helpers import needs_gpu
 
 
-def _small(dtype=torch.float32, chunk=16):
+def _small(dtype=torch.float32, chunk=16, kinds=None):
     from dilution.lm import DilutionLM, LMConfig
 
-    cfg = LMConfig(vocab_size=97, n_layers=2, d_model=64, n_heads=4, prefill_chunk=chunk)
+    cfg = LMConfig(vocab_size=97, n_layers=2, d_model=64, n_heads=4, prefill_chunk=chunk,
+                   layer_attention=kinds)
     torch.manual_seed(0)
     return DilutionLM(cfg).to(device="cuda", dtype=dtype).eval()
 
@@ -33,12 +34,19 @@ def test_config_validation():
         LMConfig(d_model=100, n_heads=16)
     with pytest.raises(ValueError):
         LMConfig(norm="batch")
+    with pytest.raises(ValueError):
+        LMConfig(n_layers=2, layer_attention=["dilution"])
+    with pytest.raises(ValueError):
+        LMConfig(attention="linear")
+    assert LMConfig(n_layers=2, layer_attention=["softmax", "dilution"]).layer_kinds() == [
+        "softmax", "dilution"]
 
 
 @pytest.mark.gpu
 @needs_gpu
-def test_lm_causality():
-    model = _small()
+@pytest.mark.parametrize("kinds", [None, ["softmax", "dilution"]])
+def test_lm_causality(kinds):
+    model = _small(kinds=kinds)
     g = torch.Generator().manual_seed(1)
     idx = torch.randint(0, 97, (2, 40), generator=g).cuda()
     idx2 = idx.clone()
@@ -59,9 +67,9 @@ def _hidden(model, idx):
 
 @pytest.mark.gpu
 @needs_gpu
-@pytest.mark.parametrize("chunk", [None, 16])
-def test_cached_decode_matches_full_forward(chunk):
-    model = _small(chunk=chunk)
+@pytest.mark.parametrize("chunk,kinds", [(None, None), (16, None), (16, ["dilution", "softmax"])])
+def test_cached_decode_matches_full_forward(chunk, kinds):
+    model = _small(chunk=chunk, kinds=kinds)
     g = torch.Generator().manual_seed(2)
     idx = torch.randint(0, 97, (2, 50), generator=g).cuda()
     prompt = 37
@@ -76,8 +84,9 @@ def test_cached_decode_matches_full_forward(chunk):
 
 @pytest.mark.gpu
 @needs_gpu
-def test_training_step_bf16_finite():
-    model = _small(dtype=torch.bfloat16).train()
+@pytest.mark.parametrize("kinds", [None, ["softmax", "dilution"]])
+def test_training_step_bf16_finite(kinds):
+    model = _small(dtype=torch.bfloat16, kinds=kinds).train()
     g = torch.Generator().manual_seed(3)
     idx = torch.randint(0, 97, (2, 64), generator=g).cuda()
     _, loss = model(idx[:, :-1], idx[:, 1:])
