@@ -99,28 +99,27 @@ __global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, i
   }
 }
 
-// (ghat * q)^T in the compute type, zero-padded to t_pad columns.
+// (ghat * q)^T in the compute type from the transposed copy Q^T (n, D, t_pad),
+// whose padding columns are zero.
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ q,
+__global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ qt,
                                                         const float* __restrict__ ghat, int64_t T,
                                                         int64_t t_pad, CT* __restrict__ dst) {
-  __shared__ float tile[64][D + 1];
   const int64_t slice = blockIdx.y;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
-  for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
-    const int r = idx / D, c = idx % D;
-    const int64_t row = r0 + r;
-    tile[r][c] = row < T ? static_cast<float>(q[(slice * T + row) * D + c]) * ghat[slice * T + row] : 0.f;
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
-    const int c = idx / 64, r = idx % 64;
-    dst[(slice * D + c) * t_pad + r0 + r] = static_cast<CT>(tile[r][c]);
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (col >= t_pad) return;
+  const float gr = col < T ? ghat[slice * T + col] : 0.f;
+#pragma unroll 4
+  for (int d = 0; d < D; ++d) {
+    const int64_t idx = (slice * D + d) * t_pad + col;
+    dst[idx] = static_cast<CT>(static_cast<float>(qt[idx]) * gr);
   }
 }
 
 // Per-row statistics of one 32-row tile staged in LDS: up to three arrays of
-// 32 floats (rows past the end: the first array reads +inf, so p = 0).
+// 32 floats, the second one negated (-dO.o/(S+eps) is the initial value of
+// the dO V^T products).  Rows past the end read +inf from the first array,
+// so that p = 0, and 0 from the others.
 template <int NARR>
 struct RowStatsLoader {
   float r;
@@ -130,7 +129,8 @@ struct RowStatsLoader {
     if (t < NARR * kTileQ) {
       const float* src = t < kTileQ ? a : (t < 2 * kTileQ ? b : c);
       const int64_t row = row0 + (t % kTileQ);
-      r = row < T ? src[row] : (t < kTileQ ? INFINITY : 0.f);
+      const float v = row < T ? src[row] : (t < kTileQ ? INFINITY : 0.f);
+      r = (t >= kTileQ && t < 2 * kTileQ) ? -v : v;
     }
   }
   __device__ void store(float* lds) const {
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float st_s[2][2 * kTileQ];   // lse, dbs
+  __shared__ __attribute__((aligned(16))) float st_s[2][2 * kTileQ];   // lse, -dbs
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
   if (!item.valid) return;
@@ -235,11 +235,14 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     RowFrag<CT, D> qf, dof;
     lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
     lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
-    // both score-shaped products first: dO V^T runs under the p / demand chain
+    float lz[16], ndb[16];
+    lds_read16(st + kTileQ + 16 * h, ndb);
+    // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
+    // and runs under the p / demand chain
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
-    float lz[16], p[16], x[16];
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
     lds_read16(st + 16 * h, lz);
+    float p[16], x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
     if constexpr (DIAG) {
@@ -265,11 +268,9 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
       for (int t = 0; t < kDTiles<D>; ++t)
         dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
     }
-    float db[16];
-    lds_read16(st + kTileQ + 16 * h, db);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      w[i] = dov[i] - db[i];                     // ds
+      w[i] = dov[i];                             // ds
       x[i] = w[i] * (sh[i] * x[i]);              // g = ds sh inv
     }
     sufk += scan_suffix_qs(x, sufk, hf);         // x = G
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
   __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float rs_s[4][2 * kTileQ];   // per wave: lse, dbs
+  __shared__ __attribute__((aligned(16))) float rs_s[4][2 * kTileQ];   // per wave: lse, -dbs
   __shared__ float g_s[4][kTileQ];
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     const int64_t r = r0 + l32;
     const bool ok = r < P.T;
     rs_s[wave][l32] = ok ? P.lse[slice * P.T + r] : INFINITY;
-    rs_s[wave][kTileQ + l32] = ok ? P.dbs[slice * P.T + r] : 0.f;
+    rs_s[wave][kTileQ + l32] = ok ? -P.dbs[slice * P.T + r] : 0.f;
   }
   constexpr int kSteps = kTileK / Mma<CT>::kStep;
   typename Mma<CT>::frag ident[kSteps];
@@ -391,11 +392,14 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     RowFrag<CT, D> kf, vf;
     lds_row_frag<CT, D>(kf, k_s[buf], rho(l32), h);
     lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
-    // both score-shaped products first: dO V^T runs under the p / demand chain
+    float lz[16], ndb[16];
+    lds_read16(st + kTileQ + 16 * h, ndb);
+    // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
+    // and runs under the p / demand chain
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, floatx16{});
-    float lz[16], p[16], x[16];
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
     lds_read16(st + 16 * h, lz);
+    float p[16], x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
     if constexpr (DIAG) {
@@ -413,11 +417,10 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
       x[i] = fast_rcp(x[i]);                     // inv
       sh[i] = p[i] * x[i];
     }
-    float db[16], ds[16];
-    lds_read16(st + kTileQ + 16 * h, db);
+    float ds[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      ds[i] = dov[i] - db[i];
+      ds[i] = dov[i];
       x[i] = ds[i] * (sh[i] * x[i]);             // g
     }
     scan_suffix_qs(x, sin, hf);                  // x = G
@@ -707,8 +710,8 @@ int launch_backward(const BackwardArgs& a) {
   DIL_TIMED("bwd_key", st, bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("bwd_query", st, bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("prep", st,
-            prep_ghat_q<CT, D><<<gp, kThreads, 0, st>>>(static_cast<const CT*>(P.q), P.ghat, a.T,
-                                                        t_pad, qgt));
+            prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>((t_pad + kThreads - 1) / kThreads), n),
+                                 kThreads, 0, st>>>(qt, P.ghat, a.T, t_pad, qgt));
   DIL_TIMED("bwd_dkcorr", st, bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P));
   return static_cast<int>(hipGetLastError());
 }

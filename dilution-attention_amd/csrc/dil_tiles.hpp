@@ -179,6 +179,14 @@ __device__ __forceinline__ typename Mma<CT>::frag ident_frag(int l32, int h, int
   }
 }
 
+// 16 per-register values as an accumulator (the initial value of a product).
+__device__ __forceinline__ floatx16 as_x16(const float (&v)[16]) {
+  floatx16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = v[i];
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // XCD-aware work mapping.
 //
