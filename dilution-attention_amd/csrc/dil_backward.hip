@@ -44,10 +44,10 @@ struct BwdParams {
   const void* k;
   const void* v;
   const void* dout;   // CT rows
-  const void* qt;     // CT (n, D, T_pad) transposed copies
+  const void* qt;     // CT transposed copies, tile-major (T_pad rows per slice)
   const void* kt;
   const void* dot;
-  const void* qgt;    // CT (n, D, T_pad): (ghat * q)^T
+  const void* qgt;    // CT (ghat * q)^T, tile-major
   int64_t T, t_pad, nb;
   int64_t n;          // slices
   int kgroups;        // groups of 4 tiles (128 keys or rows) per slice
@@ -99,20 +99,19 @@ __global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, i
   }
 }
 
-// (ghat * q)^T in the compute type from the transposed copy Q^T (n, D, t_pad),
-// whose padding columns are zero.
+// (ghat * q)^T in the compute type from the tile-major transposed copy Q^T
+// (n, t_pad rows), whose padding rows are zero.  One workgroup per 32-row tile.
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ qt,
                                                         const float* __restrict__ ghat, int64_t T,
                                                         int64_t t_pad, CT* __restrict__ dst) {
   const int64_t slice = blockIdx.y;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (col >= t_pad) return;
-  const float gr = col < T ? ghat[slice * T + col] : 0.f;
-#pragma unroll 4
-  for (int d = 0; d < D; ++d) {
-    const int64_t idx = (slice * D + d) * t_pad + col;
-    dst[idx] = static_cast<CT>(static_cast<float>(qt[idx]) * gr);
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int64_t base = slice * D * t_pad + row0 * D;
+  for (int e = threadIdx.x; e < 32 * D; e += kThreads) {
+    const int64_t row = row0 + (e & 31);
+    const float gr = row < T ? ghat[slice * T + row] : 0.f;
+    dst[base + e] = static_cast<CT>(static_cast<float>(qt[base + e]) * gr);
   }
 }
 
@@ -211,8 +210,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
     dl.load(dos, row0, P.T);
-    qtl.load(qts, P.t_pad, row0);
-    dtl.load(dots, P.t_pad, row0);
+    qtl.load(qts, row0);
+    dtl.load(dots, row0);
     sl.load(lse, dbs, dbs, row0, P.T);
   };
   auto stash = [&](int buf) {
@@ -305,7 +304,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
       if (h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     }
     if (qt - 1 >= kb0) stash(buf ^ 1);
-    __syncthreads();
+    sync_lds();
   }
 
   if (key < P.T) {
@@ -448,7 +447,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
   TTileLoader<CT, D> ktl;
   kl.load(ks, 0, P.T);
   vl.load(vs, 0, P.T);
-  ktl.load(kts, P.t_pad, 0);
+  ktl.load(kts, 0);
   kl.store(k_s[0]);
   vl.store(v_s[0]);
   ktl.store(kt_s[0]);
@@ -460,7 +459,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
       const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
       kl.load(ks, key0n, P.T);
       vl.load(vs, key0n, P.T);
-      ktl.load(kts, P.t_pad, key0n);
+      ktl.load(kts, key0n);
       cin_next = ckpt_at(kt + 1, crow);
       sin_next = ckpt_at(kt + 1, srow);
     }
@@ -471,7 +470,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
       vl.store(v_s[buf ^ 1]);
       ktl.store(kt_s[buf ^ 1]);
     }
-    __syncthreads();
+    sync_lds();
   }
 
   // ghat: column 0 of gacc, register i of half h <-> row acc_row(i, h)
@@ -533,7 +532,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
-    qtl.load(qgts, P.t_pad, row0);
+    qtl.load(qgts, row0);
     sl.load(lse, lse, lse, row0, P.T);
   };
   auto stash = [&](int buf) {
@@ -579,7 +578,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
       else if (qt == kb) step(buf, std::true_type{});
     }
     if (qt + 1 < nq) stash(buf ^ 1);
-    __syncthreads();
+    sync_lds();
   }
 
   if (key < P.T) {
@@ -710,8 +709,8 @@ int launch_backward(const BackwardArgs& a) {
   DIL_TIMED("bwd_key", st, bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("bwd_query", st, bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P));
   DIL_TIMED("prep", st,
-            prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>((t_pad + kThreads - 1) / kThreads), n),
-                                 kThreads, 0, st>>>(qt, P.ghat, a.T, t_pad, qgt));
+            prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), n), kThreads, 0, st>>>(
+                qt, P.ghat, a.T, t_pad, qgt));
   DIL_TIMED("bwd_dkcorr", st, bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P));
   return static_cast<int>(hipGetLastError());
 }

@@ -8,7 +8,8 @@
 // gfx950 MFMA layouts:
 //
 //   prep       convert q/k to the MFMA operand type when needed; write V^T
-//              (and K^T for pk) tiles, zero-padded to a multiple of 64 keys.
+//              (and K^T for pk) as contiguous (D, 32) tiles per 32 keys,
+//              zero-padded to a multiple of 64 keys.
 //   fwd_stats  row-parallel: one workgroup = 4 waves = 4 tiles of 32 query
 //              rows, key tiles of 32 staged in LDS.  S^T = K Q^T puts one query
 //              per lane: online row max and 2^-sum (log2 domain, lazily moved
@@ -40,8 +41,8 @@ struct FwdParams {
   int64_t q_sn;
   const void* k;          // CT rows (n, >= Tk, D), slice stride k_sn
   int64_t k_sn;
-  const void* vt;         // CT (n, D, Tk_pad)
-  const void* kt;         // CT (n, D, Tk_pad) or null
+  const void* vt;         // CT V^T, tile-major (Tk_pad rows per slice)
+  const void* kt;         // CT K^T, tile-major, or null
   int64_t t_sn, tk_pad;
   int64_t C, Tk, q0, nb;
   int64_t n;              // slices
@@ -190,7 +191,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   };
 
   kl.load(ks, 0, P.Tk);
-  if constexpr (PK) tl.load(kts, P.tk_pad, 0);
+  if constexpr (PK) tl.load(kts, 0);
   kl.store(ktile[0]);
   if constexpr (PK) tl.store(kttile[0]);
   __syncthreads();
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
     const int buf = kt & 1;
     if (kt + 1 < nkt_wg) {
       kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
-      if constexpr (PK) tl.load(kts, P.tk_pad, static_cast<int64_t>(kt + 1) * kTileK);
+      if constexpr (PK) tl.load(kts, static_cast<int64_t>(kt + 1) * kTileK);
     }
     if (kt < W.kfull) stats_step(kt, buf, std::false_type{});
     else if (kt < W.kend) stats_step(kt, buf, std::true_type{});
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
       kl.store(ktile[buf ^ 1]);
       if constexpr (PK) tl.store(kttile[buf ^ 1]);
     }
-    __syncthreads();
+    sync_lds();
   }
   const HalfPair lp = halves(l0 + l1);                 // the halves share m
   // re-reference the sum to the exact row maximum: p = 2^(a c - rmax) / rden
@@ -339,7 +340,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
       else step(b, buf, std::true_type{});
     }
     if (b + 1 < nb) stash(buf ^ 1);
-    __syncthreads();
+    sync_lds();
   }
   if (key_ok && h == 0) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
 }
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
     for (int n = 0; n < 2; ++n) {
       const int64_t key0 = static_cast<int64_t>(2 * st + n) * kTileK;
       kl[n].load(ks, key0, P.Tk);
-      vl[n].load(vts, P.tk_pad, key0);
+      vl[n].load(vts, key0);
     }
   };
   auto stash = [&](int buf) {
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
       }
     }
     if (st + 1 < nst) stash(buf ^ 1);
-    __syncthreads();
+    sync_lds();
   }
 
   // row sums: column 0 of orow, register i of half h <-> row acc_row(i, h)

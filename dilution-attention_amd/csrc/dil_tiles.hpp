@@ -20,10 +20,18 @@ template <int D> constexpr int kDTiles = (D + 31) / 32;
 // ---------------------------------------------------------------------------
 // operand preparation
 
+// Transposed operand copies are stored tile-major: per slice, for each block
+// of 32 rows a contiguous (D, 32) tile, so that one 32-row tile of the
+// transpose is a single contiguous 32 * D element read.  Element (row t,
+// column d) of a slice sits at (t / 32 * D + d) * 32 + t % 32.
+__host__ __device__ inline int64_t tmajor_index(int64_t t, int d, int D) {
+  return ((t >> 5) * D + d) * 32 + (t & 31);
+}
+
 // Rows of `src` (storage dtype dt) in the compute type CT, optionally scaled
 // per row by rscale[(slice, row)] (in fp32, before the rounding to CT): a
-// row-major copy into dst and/or a transposed (D, rows_pad) copy into dst_t,
-// zero-padded past `rows`.
+// row-major copy into dst and/or a tile-major transposed copy (rows_pad rows,
+// slice stride t_sn) into dst_t, zero-padded past `rows`.
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__ src, int64_t src_sn,
                                                         int dt, int64_t rows, CT* __restrict__ dst,
@@ -58,8 +66,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__
   if (dst_t != nullptr) {
     for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
       const int c = idx / 64, r = idx % 64;
-      if (r0 + r < rows_pad) dst_t[slice * t_sn + static_cast<int64_t>(c) * rows_pad + r0 + r] =
-          static_cast<CT>(tile[r][c]);
+      if (r0 + r < rows_pad) dst_t[slice * t_sn + tmajor_index(r0 + r, c, D)] = static_cast<CT>(tile[r][c]);
     }
   }
 }
@@ -108,8 +115,9 @@ struct KTileLoader {
   }
 };
 
-// Copy one transposed tile (rows d in [0, D), columns [key0, key0 + 32)) of a
-// (D, rows_pad) slice into registers.
+// Copy one transposed tile (rows d in [0, D), columns [key0, key0 + 32), key0
+// a multiple of 32) of a tile-major slice into registers: 32 * D contiguous
+// elements.
 template <typename CT, int D>
 struct TTileLoader {
   using T = Tiles<CT, D>;
@@ -117,13 +125,13 @@ struct TTileLoader {
   static constexpr int kPer = (T::kTChunks + kThreads - 1) / kThreads;
   static constexpr int kPerRow = kTileK / T::kChunk;
   V r[kPer];
-  __device__ void load(const CT* base, int64_t rows_pad, int64_t key0) {
+  __device__ void load(const CT* base, int64_t key0) {
+    const CT* tile = base + key0 * D;               // (key0 / 32) * D * 32
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int idx = threadIdx.x + u * kThreads;
-      const int d = idx / kPerRow, c = (idx % kPerRow) * T::kChunk;
       r[u] = V{};
-      if (idx < T::kTChunks) r[u] = *reinterpret_cast<const V*>(base + d * rows_pad + key0 + c);
+      if (idx < T::kTChunks) r[u] = *reinterpret_cast<const V*>(tile + idx * T::kChunk);
     }
   }
   __device__ void store(CT* lds) const {
@@ -177,6 +185,17 @@ __device__ __forceinline__ typename Mma<CT>::frag ident_frag(int l32, int h, int
   } else {
     return (perm_row(s, h) == l32) ? 1.f : 0.f;
   }
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load and store of the wave (its fence covers global
+// memory), which would cut the prefetch of the next tile and put the
+// checkpoint stores on the critical path of every step.  The tile loops
+// exchange data between waves through LDS only, so they synchronise with this.
+__device__ __forceinline__ void sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // 16 per-register values as an accumulator (the initial value of a product).

@@ -1,8 +1,10 @@
 """ctypes binding of libdilution_hip.so (C ABI: include/dilution_hip.h).
 
 The library is built in-tree by ``dilution-attention_amd/csrc/build.py`` (or
-``__graft_entry__.build()``) and loaded from this package directory.  There is
-no fallback: if the library is missing, every entry point raises RuntimeError.
+``__graft_entry__.build()``) and loaded from this package directory, or from
+the path in the environment variable ``DILUTION_HIP_LIB`` when that is set (a
+different build of the same sources).  There is no fallback: if the library is
+missing, every entry point raises RuntimeError.
 """
 
 from __future__ import annotations
@@ -10,7 +12,8 @@ from __future__ import annotations
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdilution_hip.so")
+LIB_PATH = os.environ.get("DILUTION_HIP_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libdilution_hip.so")
 
 _c_int64 = ctypes.c_int64
 _c_int = ctypes.c_int
