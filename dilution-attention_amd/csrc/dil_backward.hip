@@ -119,21 +119,26 @@ __global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ q
 // 32 floats, the second one negated (-dO.o/(S+eps) is the initial value of
 // the dO V^T products).  Rows past the end read +inf from the first array,
 // so that p = 0, and 0 from the others.
-template <int NARR>
+// With CLAMP every thread loads (from a clamped row) and the value is fixed up
+// in store(); without it only the threads that store load.
+template <int NARR, bool CLAMP = true>
 struct RowStatsLoader {
   float r;
+  bool ok;
   __device__ void load(const float* a, const float* b, const float* c, int64_t row0, int64_t T) {
     const int t = threadIdx.x;
-    r = 0.f;
-    if (t < NARR * kTileQ) {
-      const float* src = t < kTileQ ? a : (t < 2 * kTileQ ? b : c);
-      const int64_t row = row0 + (t % kTileQ);
-      const float v = row < T ? src[row] : (t < kTileQ ? INFINITY : 0.f);
-      r = (t >= kTileQ && t < 2 * kTileQ) ? -v : v;
-    }
+    const float* src = t < kTileQ ? a : (t < 2 * kTileQ ? b : c);
+    const int64_t row = row0 + (t % kTileQ);
+    ok = row < T;
+    if (CLAMP) r = src[min(row, T - 1)];
+    else r = (ok && t < NARR * kTileQ) ? src[row] : 0.f;
   }
   __device__ void store(float* lds) const {
-    if (threadIdx.x < NARR * kTileQ) lds[threadIdx.x] = r;
+    const int t = threadIdx.x;
+    if (t < NARR * kTileQ) {
+      const float v = ok ? r : (t < kTileQ ? INFINITY : 0.f);
+      lds[t] = (t >= kTileQ && t < 2 * kTileQ) ? -v : v;
+    }
   }
 };
 
@@ -166,6 +171,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) float st_s[2][2 * kTileQ];   // lse, -dbs
+  __shared__ float cs_s[2][4 * kTileK];                                // demand checkpoints
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
   if (!item.valid) return;
@@ -203,9 +209,15 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   float sufk = 0.f;
   float* sufk_col = P.sufk + slice * P.nb * P.T + key;
 
+  // a stage: the Q and dO' row tiles, their transposes, the row statistics and
+  // the demand checkpoints of the workgroup's 128 keys entering the tile
   KTileLoader<CT, D> ql, dl;
   TTileLoader<CT, D> qtl, dtl;
   RowStatsLoader<2> sl;
+  const int64_t ck = static_cast<int64_t>(kb0) * kTileK + (threadIdx.x & (4 * kTileK - 1));
+  const bool ck_ok = ck < P.T;
+  const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
+  float cr = 0.f;
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
@@ -213,6 +225,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     qtl.load(qts, row0);
     dtl.load(dots, row0);
     sl.load(lse, dbs, dbs, row0, P.T);
+    cr = ccol[static_cast<int64_t>(qt) * P.T];
   };
   auto stash = [&](int buf) {
     ql.store(q_s[buf]);
@@ -220,17 +233,14 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     qtl.store(qt_s[buf]);
     dtl.store(dot_s[buf]);
     sl.store(st_s[buf]);
+    if (threadIdx.x < 4 * kTileK) cs_s[buf][threadIdx.x] = ck_ok ? cr : 0.f;
   };
   constexpr int kSteps = kTileQ / Mma<CT>::kStep;
 
-  // demand checkpoint of this lane's key at query tile qt, loaded one tile ahead
-  auto carry_at = [&](int qt) -> float {
-    return (active && qt >= kb && key < P.T) ? P.carry[(slice * P.nb + qt) * P.T + key] : 0.f;
-  };
-
-  auto step = [&](int qt, int buf, float cin, auto diag_tag) {
+  auto step = [&](int qt, int buf, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     const float* st = st_s[buf];
+    const float cin = cs_s[buf][wave * kTileK + l32];   // demand entering the tile
     RowFrag<CT, D> qf, dof;
     lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
     lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
@@ -285,22 +295,17 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     }
   };
 
-  float cin_next = carry_at(nq - 1);
   fetch(nq - 1);
   stash(0);
   __syncthreads();
   int it = 0;
   for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
     const int buf = it & 1;
-    const float cin = cin_next;
-    if (qt - 1 >= kb0) {
-      fetch(qt - 1);
-      cin_next = carry_at(qt - 1);
-    }
+    fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
     if (active && qt >= kb) {
       const float sufk_in = sufk;                // suffix entering this tile from below
-      if (qt > kb) step(qt, buf, cin, std::false_type{});
-      else step(qt, buf, cin, std::true_type{});
+      if (qt > kb) step(qt, buf, std::false_type{});
+      else step(qt, buf, std::true_type{});
       if (h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     }
     if (qt - 1 >= kb0) stash(buf ^ 1);
@@ -442,34 +447,34 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     }
   };
 
-  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
-  KTileLoader<CT, D> kl, vl;
+  KTileLoader<CT, D, false> kl, vl;
   TTileLoader<CT, D> ktl;
-  kl.load(ks, 0, P.T);
-  vl.load(vs, 0, P.T);
-  ktl.load(kts, 0);
-  kl.store(k_s[0]);
-  vl.store(v_s[0]);
-  ktl.store(kt_s[0]);
+  auto fetch = [&](int kt) {
+    const int64_t key0 = static_cast<int64_t>(kt) * kTileK;
+    kl.load(ks, key0, P.T);
+    vl.load(vs, key0, P.T);
+    ktl.load(kts, key0);
+  };
+  auto stash = [&](int buf) {
+    kl.store(k_s[buf]);
+    vl.store(v_s[buf]);
+    ktl.store(kt_s[buf]);
+  };
+  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
+  fetch(0);
+  stash(0);
   __syncthreads();
   for (int kt = 0; kt < nkt_wg; ++kt) {
     const int buf = kt & 1;
     const float cin = cin_next, sin = sin_next;
     if (kt + 1 < nkt_wg) {
-      const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
-      kl.load(ks, key0n, P.T);
-      vl.load(vs, key0n, P.T);
-      ktl.load(kts, key0n);
+      fetch(kt + 1);
       cin_next = ckpt_at(kt + 1, crow);
       sin_next = ckpt_at(kt + 1, srow);
     }
     if (kt < qt && kt < nkt_w) step(kt, buf, cin, sin, std::false_type{});
     else if (kt == qt && kt < nkt_w) step(kt, buf, cin, sin, std::true_type{});
-    if (kt + 1 < nkt_wg) {
-      kl.store(k_s[buf ^ 1]);
-      vl.store(v_s[buf ^ 1]);
-      ktl.store(kt_s[buf ^ 1]);
-    }
+    if (kt + 1 < nkt_wg) stash(buf ^ 1);
     sync_lds();
   }
 
@@ -526,9 +531,9 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) dkc[t] = floatx16{};
 
-  KTileLoader<CT, D> ql;
+  KTileLoader<CT, D, false> ql;
   TTileLoader<CT, D> qtl;
-  RowStatsLoader<1> sl;
+  RowStatsLoader<1, false> sl;
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);

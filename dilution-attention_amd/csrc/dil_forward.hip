@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   else zero_row_frag<CT, D>(qf);
   const int my_q = static_cast<int>(W.qa0) + l32;      // query of this lane in sweep 1
 
-  KTileLoader<CT, D> kl;
+  KTileLoader<CT, D, false> kl;
   TTileLoader<CT, D> tl;
 
   // ---- sweep 1: S^T = K Q^T (lane <-> query, registers <-> keys) ----
@@ -198,8 +198,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   for (int kt = 0; kt < nkt_wg; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nkt_wg) {
-      kl.load(ks, static_cast<int64_t>(kt + 1) * kTileK, P.Tk);
-      if constexpr (PK) tl.load(kts, static_cast<int64_t>(kt + 1) * kTileK);
+      const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
+      kl.load(ks, key0n, P.Tk);
+      if constexpr (PK) tl.load(kts, key0n);
     }
     if (kt < W.kfull) stats_step(kt, buf, std::false_type{});
     else if (kt < W.kend) stats_step(kt, buf, std::true_type{});
@@ -278,17 +279,18 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
   float* ccol = P.carry + slice * nb * P.Tk + key;
 
   KTileLoader<CT, D> ql;
-  float lse_r = 0.f;
+  float rmax_r = 0.f, rden_r = 1.f;
+  bool row_ok = false;
   auto fetch = [&](int64_t b) {
     ql.load(qs, b * kTileQ, P.C);
-    if (threadIdx.x < kTileQ) {
-      const int64_t r = b * kTileQ + threadIdx.x;
-      lse_r = r < P.C ? rmax[r] + __log2f(rden[r]) : INFINITY;
-    }
+    const int64_t r = b * kTileQ + (threadIdx.x & (kTileQ - 1));
+    row_ok = r < P.C;
+    rmax_r = rmax[min(r, P.C - 1)];
+    rden_r = rden[min(r, P.C - 1)];
   };
   auto stash = [&](int buf) {
     ql.store(q_s[buf]);
-    if (threadIdx.x < kTileQ) st_s[buf][threadIdx.x] = lse_r;
+    if (threadIdx.x < kTileQ) st_s[buf][threadIdx.x] = row_ok ? rmax_r + __log2f(rden_r) : INFINITY;
   };
 
   auto step = [&](int64_t b, int buf, auto diag_tag) {
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
   int it = 0;
   for (int64_t b = b_wg; b < nb; ++b, ++it) {
     const int buf = it & 1;
-    if (b + 1 < nb) fetch(b + 1);
+    fetch(min(b + 1, nb - 1));                  // the last step reloads its own block, unused
     // wave-uniform condition: every lane must feed the MFMAs of the step
     if (b >= b_w && key0 < P.Tk) {
       if (h == 0 && key_ok) ccol[b * P.Tk] = static_cast<float>(run);   // demand entering block b
@@ -356,6 +358,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   __shared__ __attribute__((aligned(16))) CT vttile[2][2][D * T::kTStride];
   __shared__ __attribute__((aligned(16))) float lse_s[4][kTileQ];
   __shared__ float ssum_s[4][kTileQ];
+  __shared__ float cs_s[2][4][2 * kTileK];             // demand checkpoints per stage and wave
 
   const WorkItem item = xcd_work_item(P.groups, P.n, true);
   if (!item.valid) return;
@@ -395,18 +398,23 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   floatx16 orow = floatx16{};
   const auto ones = ones_col_frag<CT>(l32);
 
-  const float* crow = P.carry + (slice * P.nb + W.r0 / kTileQ) * P.Tk;
-  // demand checkpoint of this lane's key, loaded one stage ahead
-  auto carry_at = [&](int kt) -> float {
-    const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
-    return (kt < W.kend && key < P.Tk) ? crow[key] : 0.f;
-  };
+  // The demand checkpoints of a stage (each wave's rows, the stage's 64 keys)
+  // are staged through LDS with the tiles: thread t loads the one of wave
+  // t >> 6, key 32 * ((t >> 5) & 1) + (t & 31) of the stage.
+  const int cw = threadIdx.x >> 6, cj = threadIdx.x & 63;
+  const int64_t c_rb = min(static_cast<int64_t>(g) * 4 + cw, P.nb - 1);
+  const float* c_row = P.carry + (slice * P.nb + c_rb) * P.Tk;
+  float cr = 0.f;
+  bool cr_ok = false;
 
   // N consecutive key tiles kt0 .. kt0 + N - 1 of stage buffer `buf`, their
   // phases interleaved so that one tile's MFMAs overlap the other's VALU work
-  auto out_tiles = [&](auto n_tag, auto diag_tag, int kt0, int slot0, int buf, const float* cin) {
+  auto out_tiles = [&](auto n_tag, auto diag_tag, int kt0, int slot0, int buf) {
     constexpr int N = decltype(n_tag)::value;
     constexpr bool DIAG = decltype(diag_tag)::value;
+    float cin[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) cin[n] = cs_s[buf][wave][(slot0 + n) * kTileK + rho(l32)];
     floatx16 acc[N];
 #pragma unroll
     for (int n = 0; n < N; ++n) {
@@ -480,6 +488,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
       kl[n].load(ks, key0, P.Tk);
       vl[n].load(vts, key0);
     }
+    const int64_t key = static_cast<int64_t>(st) * 2 * kTileK + cj;
+    cr_ok = key < P.Tk;
+    cr = c_row[min(key, P.Tk - 1)];
   };
   auto stash = [&](int buf) {
 #pragma unroll
@@ -487,29 +498,24 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
       kl[n].store(ktile[buf][n]);
       vl[n].store(vttile[buf][n]);
     }
+    cs_s[buf][cw][cj] = cr_ok ? cr : 0.f;
   };
-  float cnext[2] = {carry_at(0), carry_at(1)};
   fetch(0);
   stash(0);
   __syncthreads();
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
     const int kt0 = 2 * st;
-    const float cin[2] = {cnext[0], cnext[1]};
-    if (st + 1 < nst) {
-      fetch(st + 1);
-      cnext[0] = carry_at(kt0 + 2);
-      cnext[1] = carry_at(kt0 + 3);
-    }
+    fetch(min(st + 1, nst - 1));                       // the last stage reloads itself, unused
     if (kt0 + 1 < W.kfull) {
-      out_tiles(std::integral_constant<int, 2>{}, std::false_type{}, kt0, 0, buf, cin);
+      out_tiles(std::integral_constant<int, 2>{}, std::false_type{}, kt0, 0, buf);
     } else {
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
         if (kt0 + n < W.kfull)
-          out_tiles(std::integral_constant<int, 1>{}, std::false_type{}, kt0 + n, n, buf, cin + n);
+          out_tiles(std::integral_constant<int, 1>{}, std::false_type{}, kt0 + n, n, buf);
         else if (kt0 + n < W.kend)
-          out_tiles(std::integral_constant<int, 1>{}, std::true_type{}, kt0 + n, n, buf, cin + n);
+          out_tiles(std::integral_constant<int, 1>{}, std::true_type{}, kt0 + n, n, buf);
       }
     }
     if (st + 1 < nst) stash(buf ^ 1);

@@ -87,30 +87,53 @@ struct Tiles {
 template <typename CT> struct Vec16 { typedef floatx4 type; };
 template <> struct Vec16<__bf16> { typedef bf16x8 type; };
 
-// Copy one K tile (rows [key0, key0+32) of a row-major (rows, D) slice) into
-// registers: each thread owns kKChunks / kThreads 16-byte chunks.
-template <typename CT, int D>
+// The tile loaders below split a copy global -> LDS into load() at the start
+// of a step and store() at its end.  Every thread issues its global loads
+// unconditionally, from addresses clamped into the slice, and the masking of
+// rows past the end happens in store(): with no branch around a load, the
+// compiler waits for the loads only where store() consumes them, so they
+// overlap the whole step instead of being waited for right after issue.
+
+// Copy one K tile (rows [key0, key0+32) of a row-major (rows, D) slice,
+// nkeys >= 1 rows) into registers: each thread owns kKChunks / kThreads
+// 16-byte chunks.  CLAMP selects the branch-free form above; without it the
+// loads of rows past the end are skipped (cheaper where a step's compute is
+// short and more waves hide the load latency).
+template <typename CT, int D, bool CLAMP = true>
 struct KTileLoader {
   using T = Tiles<CT, D>;
   using V = typename Vec16<CT>::type;
   static constexpr int kPer = (T::kKChunks + kThreads - 1) / kThreads;
+  static constexpr int kPerRow = D / T::kChunk;
   V r[kPer];
+  int nrows;                                        // rows of the tile inside the slice
   __device__ void load(const CT* base, int64_t key0, int64_t nkeys) {
+    // slices hold fewer than 2^31 rows
+    const int k0 = static_cast<int>(key0), last = static_cast<int>(nkeys) - 1;
+    nrows = min(max(last + 1 - k0, 0), kTileK);
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int idx = threadIdx.x + u * kThreads;
-      const int row = idx / (D / T::kChunk), c = (idx % (D / T::kChunk)) * T::kChunk;
-      r[u] = V{};
-      if (idx < T::kKChunks && key0 + row < nkeys)
-        r[u] = *reinterpret_cast<const V*>(base + (key0 + row) * D + c);
+      if constexpr (CLAMP) {
+        const int idx = min(static_cast<int>(threadIdx.x) + u * kThreads, T::kKChunks - 1);
+        const int row = min(k0 + idx / kPerRow, last);
+        r[u] = *reinterpret_cast<const V*>(base + static_cast<int64_t>(row) * D + (idx % kPerRow) * T::kChunk);
+      } else {
+        const int idx = threadIdx.x + u * kThreads;
+        const int row = idx / kPerRow;
+        r[u] = V{};
+        if (idx < T::kKChunks && row < nrows)
+          r[u] = *reinterpret_cast<const V*>(base + (key0 + row) * D + (idx % kPerRow) * T::kChunk);
+      }
     }
   }
   __device__ void store(CT* lds) const {
+    const bool full = !CLAMP || nrows == kTileK;    // workgroup-uniform
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int idx = threadIdx.x + u * kThreads;
-      const int row = idx / (D / T::kChunk), c = (idx % (D / T::kChunk)) * T::kChunk;
-      if (idx < T::kKChunks) *reinterpret_cast<V*>(lds + row * T::kKStride + c) = r[u];
+      const int row = idx / kPerRow, c = (idx % kPerRow) * T::kChunk;
+      if (idx < T::kKChunks)
+        *reinterpret_cast<V*>(lds + row * T::kKStride + c) = (full || row < nrows) ? r[u] : V{};
     }
   }
 };
@@ -129,9 +152,8 @@ struct TTileLoader {
     const CT* tile = base + key0 * D;               // (key0 / 32) * D * 32
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int idx = threadIdx.x + u * kThreads;
-      r[u] = V{};
-      if (idx < T::kTChunks) r[u] = *reinterpret_cast<const V*>(tile + idx * T::kChunk);
+      const int idx = min(static_cast<int>(threadIdx.x) + u * kThreads, T::kTChunks - 1);
+      r[u] = *reinterpret_cast<const V*>(tile + idx * T::kChunk);
     }
   }
   __device__ void store(CT* lds) const {
