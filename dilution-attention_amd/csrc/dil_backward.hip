@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
 
   // a stage: the Q and dO' row tiles, their transposes, the row statistics and
   // the demand checkpoints of the workgroup's 128 keys entering the tile
-  KTileLoader<CT, D> ql, dl;
+  KTileLoader<CT, D, true, true> ql, dl;        // row tiles in query-split slot order
   TTileLoader<CT, D> qtl, dtl;
   RowStatsLoader<2> sl;
   const int64_t ck = static_cast<int64_t>(kb0) * kTileK + (threadIdx.x & (4 * kTileK - 1));
@@ -242,8 +242,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     const float* st = st_s[buf];
     const float cin = cs_s[buf][wave * kTileK + l32];   // demand entering the tile
     RowFrag<CT, D> qf, dof;
-    lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
-    lds_row_frag<CT, D>(dof, do_s[buf], qsig(l32), h);
+    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
+    lds_row_frag<CT, D>(dof, do_s[buf], l32, h);
     float lz[16], ndb[16];
     lds_read16(st + kTileQ + 16 * h, ndb);
     // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
@@ -531,7 +531,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) dkc[t] = floatx16{};
 
-  KTileLoader<CT, D, false> ql;
+  KTileLoader<CT, D, false, true> ql;            // row tile in query-split slot order
   TTileLoader<CT, D> qtl;
   RowStatsLoader<1, false> sl;
   auto fetch = [&](int qt) {
@@ -550,7 +550,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   auto step = [&](int buf, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     RowFrag<CT, D> qf;
-    lds_row_frag<CT, D>(qf, q_s[buf], qsig(l32), h);
+    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
     float lz[16], p[16];
     lds_read16(st_s[buf] + 16 * h, lz);

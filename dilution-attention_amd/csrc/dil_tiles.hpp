@@ -94,12 +94,19 @@ template <> struct Vec16<__bf16> { typedef bf16x8 type; };
 // compiler waits for the loads only where store() consumes them, so they
 // overlap the whole step instead of being waited for right after issue.
 
+// Slot of row r when a 32-row tile is stored in the query-split order of
+// qsig() (slot m holds row qsig(m)): the inverse of qsig.
+__device__ __forceinline__ int qs_slot(int r) { return (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3); }
+
 // Copy one K tile (rows [key0, key0+32) of a row-major (rows, D) slice,
 // nkeys >= 1 rows) into registers: each thread owns kKChunks / kThreads
 // 16-byte chunks.  CLAMP selects the branch-free form above; without it the
 // loads of rows past the end are skipped (cheaper where a step's compute is
-// short and more waves hide the load latency).
-template <typename CT, int D, bool CLAMP = true>
+// short and more waves hide the load latency).  QS stores the rows in
+// query-split order (row r at slot qs_slot(r)): lanes that read rows qsig(l)
+// then read consecutive slots, which keeps their 16-byte LDS reads free of
+// bank conflicts (rows r and r + 16 of the natural order share banks).
+template <typename CT, int D, bool CLAMP = true, bool QS = false>
 struct KTileLoader {
   using T = Tiles<CT, D>;
   using V = typename Vec16<CT>::type;
@@ -132,8 +139,9 @@ struct KTileLoader {
     for (int u = 0; u < kPer; ++u) {
       const int idx = threadIdx.x + u * kThreads;
       const int row = idx / kPerRow, c = (idx % kPerRow) * T::kChunk;
+      const int slot = QS ? qs_slot(row) : row;
       if (idx < T::kKChunks)
-        *reinterpret_cast<V*>(lds + row * T::kKStride + c) = (full || row < nrows) ? r[u] : V{};
+        *reinterpret_cast<V*>(lds + slot * T::kKStride + c) = (full || row < nrows) ? r[u] : V{};
     }
   }
 };
