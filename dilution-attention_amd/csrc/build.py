@@ -21,6 +21,9 @@ PKG = os.path.join(os.path.dirname(HERE), "dilution")
 OUT = os.path.join(PKG, "libdilution_hip.so")
 BUILD = os.path.join(HERE, "_build")
 SOURCES = ["dil_api.hip", "dil_decode.hip", "dil_forward.hip", "dil_backward.hip", "dil_timing.hip"]
+# (object stem, source, extra flags): the ablation variants of each bid
+# function are one object each, built from the same source
+VARIANT_OBJECTS = [(f"dil_variants_b{b}", "dil_variants.hip", [f"-DDIL_VARIANT_BID={b}"]) for b in range(8)]
 ARCH = "gfx950"
 
 FLAGS = [
@@ -42,20 +45,22 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libdilution_hip.so)")
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+def _compile(unit) -> str:
+    stem, src, extra = unit
+    obj = os.path.join(BUILD, stem + ".o")
+    cmd = [hipcc(), *FLAGS, *extra, "-c", os.path.join(HERE, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
+        raise RuntimeError(f"hipcc failed for {stem}:\n{proc.stderr}")
     return obj
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    units = [(os.path.splitext(src)[0], src, []) for src in SOURCES] + VARIANT_OBJECTS
+    jobs = jobs or min(len(units), os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, SOURCES))
+        objs = list(pool.map(_compile, units))
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -5,6 +5,7 @@
 
 #include "../../include/dilution_hip.h"
 #include "dil_internal.hpp"
+#include "dil_variant.hpp"
 
 namespace {
 
@@ -13,6 +14,17 @@ bool valid_dtype(int t) { return t == 0 || t == 1 || t == 2; }
 bool valid_precision(int p) { return p == 0 || p == 1 || p == 2; }
 
 }  // namespace
+
+namespace dil {
+
+int check_variant(const Variant& v, int head_dim) {
+  if (v.bid < 0 || v.bid >= kNumBids || v.share < SHARE_NONE || v.share > SHARE_EXCL || !(v.shift > 0.f))
+    return kErrVariant;
+  if ((v.bid != BID_SOFTMAX || v.share != SHARE_INCL) && head_dim != kVariantHeadDim) return kErrVariant;
+  return 0;
+}
+
+}  // namespace dil
 
 extern "C" {
 
@@ -26,6 +38,9 @@ const char* dil_status_string(int status) {
     case dil::kErrWorkspace: return "workspace smaller than the size query returned";
     case dil::kErrShape: return "invalid shape or length";
     case dil::kErrPrecision: return "dot_precision must be one of ieee, tf32, bf16";
+    case dil::kErrVariant:
+      return "operator variant out of range (bid 0-7, share 0-2, shift > 0) or not built for this "
+             "head_dim (the ablation variants are built for head_dim 64)";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -36,9 +51,10 @@ int64_t dil_decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
   return dil::decode_workspace_bytes(n, length, head_dim);
 }
 
-int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, float* committed,
-                    void* out, int64_t n, int64_t capacity, int64_t length, int head_dim,
-                    int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_cache,
+                            float* committed, void* out, int64_t n, int64_t capacity,
+                            int64_t length, int head_dim, int dtype, int bid, int share,
+                            float shift, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (n < 1 || length < 1 || length > capacity) return dil::kErrShape;
@@ -59,8 +75,16 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
   a.length = length;
   a.head_dim = head_dim;
   a.dtype = dtype;
+  a.var = dil::Variant{bid, share, shift};
   a.stream = stream;
   return dil::decode_step(a);
+}
+
+int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, float* committed,
+                    void* out, int64_t n, int64_t capacity, int64_t length, int head_dim,
+                    int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  return dil_decode_step_variant(q1, k_cache, v_cache, committed, out, n, capacity, length,
+                                 head_dim, dtype, 0, 1, 1.f, workspace, workspace_bytes, stream);
 }
 
 int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
@@ -68,10 +92,11 @@ int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dt
   return dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision == 2, want_pk);
 }
 
-int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
-                int head_dim, int dtype, int precision, float* out, float* rmax, float* rden,
-                float* ssum, float* carry, float* committed_total, float* pk, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
+                        int head_dim, int dtype, int precision, int bid, int share, float shift,
+                        float* out, float* rmax, float* rden, float* ssum, float* carry,
+                        float* committed_total, float* pk, void* workspace, int64_t workspace_bytes,
+                        void* stream) {
   if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
@@ -103,10 +128,20 @@ int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t 
   a.total = committed_total;
   a.tot_sn = seq;
   a.pk = pk;
+  a.var = dil::Variant{bid, share, shift};
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
   a.stream = stream;
   return dil::forward(a);
+}
+
+int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
+                int head_dim, int dtype, int precision, float* out, float* rmax, float* rden,
+                float* ssum, float* carry, float* committed_total, float* pk, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  return dil_forward_variant(q, k, v, n, seq, head_dim, dtype, precision, 0, 1, 1.f, out, rmax,
+                             rden, ssum, carry, committed_total, pk, workspace, workspace_bytes,
+                             stream);
 }
 
 int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
@@ -161,11 +196,12 @@ int64_t dil_backward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int d
   return dil::backward_workspace_bytes(n, seq, head_dim, dtype, precision == 2);
 }
 
-int dil_backward(const void* q, const void* k, const void* v, const void* dout,
-                 const float* out, const float* rmax, const float* rden, const float* ssum,
-                 const float* carry, const float* pk, int64_t n, int64_t seq, int head_dim,
-                 int dtype, int dout_dtype, int grad_dtype, int precision, void* dq, void* dk,
-                 void* dv, void* workspace, int64_t workspace_bytes, void* stream) {
+int dil_backward_variant(const void* q, const void* k, const void* v, const void* dout,
+                         const float* out, const float* rmax, const float* rden,
+                         const float* ssum, const float* carry, const float* pk, int64_t n,
+                         int64_t seq, int head_dim, int dtype, int dout_dtype, int grad_dtype,
+                         int precision, int bid, int share, float shift, void* dq, void* dk,
+                         void* dv, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
   if (!valid_dtype(dtype) || !valid_dtype(dout_dtype) || !valid_dtype(grad_dtype))
     return dil::kErrDtype;
@@ -194,10 +230,21 @@ int dil_backward(const void* q, const void* k, const void* v, const void* dout,
   a.dout_dtype = dout_dtype;
   a.grad_dtype = grad_dtype;
   a.lowp = precision == 2;
+  a.var = dil::Variant{bid, share, shift};
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
   a.stream = stream;
   return dil::backward(a);
+}
+
+int dil_backward(const void* q, const void* k, const void* v, const void* dout,
+                 const float* out, const float* rmax, const float* rden, const float* ssum,
+                 const float* carry, const float* pk, int64_t n, int64_t seq, int head_dim,
+                 int dtype, int dout_dtype, int grad_dtype, int precision, void* dq, void* dk,
+                 void* dv, void* workspace, int64_t workspace_bytes, void* stream) {
+  return dil_backward_variant(q, k, v, dout, out, rmax, rden, ssum, carry, pk, n, seq, head_dim,
+                              dtype, dout_dtype, grad_dtype, precision, 0, 1, 1.f, dq, dk, dv,
+                              workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -1,724 +1,11 @@
-// Backward of the dilution-attention operator.
-//
-// Reference behaviour: _DilutionAttentionFn.backward,
-// /root/reference/src/dilution/kernels.py:851-903, and the decomposition in
-// /root/reference/docs/kernels.md:62-84.  With s = 1/sqrt(d), C the inclusive
-// column demand (c + p) and S the row sum of shares:
-//
-//   ds_ij  = (dO_i . v_j - dO_i . o_i) / (S_i + eps) = dO'_i . v_j - dbs_i,
-//            dO'_i = dO_i sinv_i (the rows of dO prescaled once), sinv_i = 1/(S_i+eps)
-//   inv_ij = 1 / (C_ij + eps),   sh_ij = p_ij inv_ij
-//   g_ij   = ds_ij sh_ij inv_ij                  (adjoint flowing into the demand)
-//   G_ij   = sum_{i' >= i} g_i'j                 (inclusive reverse column scan)
-//   dp_ij  = ds_ij inv_ij - G_ij,   p dp = ds_ij sh_ij - p_ij G_ij
-//   ghat_i = sum_j (p dp)_ij,   da_ij = (p dp)_ij - p_ij ghat_i
-//   dq = s da K,   dk = s da^T Q,   dv = sh^T dO' 
-//
-// Kernels (gfx950, deterministic, no atomics; tiles in the query-split layout
-// of dil_tiles.hpp, causal diagonal tiles peeled out of the main loops):
-//   bwd_rows    per row: lse = rmax + log2 rden, sinv = 1/(S + eps),
-//               dbs = (dO . o) sinv.
-//   bwd_key     one wave per 32-key tile, query tiles walked in reverse:
-//               dv += sh^T dO' and dk_main += (p dp)^T Q on MFMA with
-//               keys in lanes; the running suffix G per key is stored at every
-//               tile boundary for bwd_query.
-//   bwd_query   one wave per 32-row tile over its causal key tiles: the same
-//               chain with G from the checkpoints; (p dp) transposed by an
-//               identity MFMA so dq += (p dp) K runs with queries in lanes,
-//               ghat (the row sums of p dp) riding on it as a ones column;
-//               dq = s dq_main - ghat pk.
-//   prep_ghat_q (ghat * Q)^T tiles for the correction.
-//   bwd_dkcorr  one wave per key tile: dk = s dk_main - s sum_i p_ij (ghat_i q_i).
-#include "dil_common.hpp"
-#include "dil_internal.hpp"
-#include "dil_tiles.hpp"
-
-#include <type_traits>
+// Entry points of the backward: the production operator for every head_dim;
+// the ablation variants are built in dil_variants.hip (head_dim 64) and
+// reached through backward_bid<BID>.
+#include "dil_backward_impl.hpp"
 
 namespace dil {
 
 namespace {
-
-struct BwdParams {
-  const void* q;      // CT rows (n, T, D)
-  const void* k;
-  const void* v;
-  const void* dout;   // CT rows
-  const void* qt;     // CT transposed copies, tile-major (T_pad rows per slice)
-  const void* kt;
-  const void* dot;
-  const void* qgt;    // CT (ghat * q)^T, tile-major
-  int64_t T, t_pad, nb;
-  int64_t n;          // slices
-  int kgroups;        // groups of 4 tiles (128 keys or rows) per slice
-  float c, scale;
-  const float* lse;   // (n, T)
-  const float* sinv;
-  const float* dbs;
-  float* ghat;        // (n, T)
-  const float* carry; // (n, nb, T)
-  float* sufk;        // (n, nb, T)
-  float* dkm;         // (n, T, D) fp32: sum_i (p dp)_ij q_i
-  const float* pk;    // (n, T, D)
-  void* dq;
-  void* dk;
-  void* dv;
-  int gdt;            // grad dtype
-};
-
-// ---------------------------------------------------------------------------
-// per-row prologue
-
-template <int D>
-__global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, int ddt,
-                                                const float* __restrict__ out,
-                                                const float* __restrict__ rmax,
-                                                const float* __restrict__ rden,
-                                                const float* __restrict__ ssum, float* __restrict__ lse,
-                                                float* __restrict__ sinv, float* __restrict__ dbs,
-                                                int64_t rows) {
-  constexpr int LPR = D / 8;                    // lanes per row, 8 elements each
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t row = gid / LPR;
-  const int sub = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (row < rows) {
-    float a[8], b[8];
-    load8_f32(dout, row * D + sub * 8, ddt, a);
-    load8_f32(out, row * D + sub * 8, DT_F32, b);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf(a[e], b[e], acc);
-  }
-#pragma unroll
-  for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
-  if (row < rows && sub == 0) {
-    const float si = 1.f / (ssum[row] + kEps);
-    lse[row] = rmax[row] + __log2f(rden[row]);
-    sinv[row] = si;
-    dbs[row] = acc * si;
-  }
-}
-
-// (ghat * q)^T in the compute type from the tile-major transposed copy Q^T
-// (n, t_pad rows), whose padding rows are zero.  One workgroup per 32-row tile.
-template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ qt,
-                                                        const float* __restrict__ ghat, int64_t T,
-                                                        int64_t t_pad, CT* __restrict__ dst) {
-  const int64_t slice = blockIdx.y;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 32;
-  const int64_t base = slice * D * t_pad + row0 * D;
-  for (int e = threadIdx.x; e < 32 * D; e += kThreads) {
-    const int64_t row = row0 + (e & 31);
-    const float gr = row < T ? ghat[slice * T + row] : 0.f;
-    dst[base + e] = static_cast<CT>(static_cast<float>(qt[base + e]) * gr);
-  }
-}
-
-// Per-row statistics of one 32-row tile staged in LDS: up to three arrays of
-// 32 floats, the second one negated (-dO.o/(S+eps) is the initial value of
-// the dO V^T products).  Rows past the end read +inf from the first array,
-// so that p = 0, and 0 from the others.
-// With CLAMP every thread loads (from a clamped row) and the value is fixed up
-// in store(); without it only the threads that store load.
-template <int NARR, bool CLAMP = true>
-struct RowStatsLoader {
-  float r;
-  bool ok;
-  __device__ void load(const float* a, const float* b, const float* c, int64_t row0, int64_t T) {
-    const int t = threadIdx.x;
-    const float* src = t < kTileQ ? a : (t < 2 * kTileQ ? b : c);
-    const int64_t row = row0 + (t % kTileQ);
-    ok = row < T;
-    if (CLAMP) r = src[min(row, T - 1)];
-    else r = (ok && t < NARR * kTileQ) ? src[row] : 0.f;
-  }
-  __device__ void store(float* lds) const {
-    const int t = threadIdx.x;
-    if (t < NARR * kTileQ) {
-      const float v = ok ? r : (t < kTileQ ? INFINITY : 0.f);
-      lds[t] = (t >= kTileQ && t < 2 * kTileQ) ? -v : v;
-    }
-  }
-};
-
-// 16 consecutive floats of LDS into registers (four 16-byte reads).
-__device__ __forceinline__ void lds_read16(const float* src, float (&v)[16]) {
-  const floatx4* p = reinterpret_cast<const floatx4*>(src);
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const floatx4 x = p[u];
-    v[4 * u] = x[0];
-    v[4 * u + 1] = x[1];
-    v[4 * u + 2] = x[2];
-    v[4 * u + 3] = x[3];
-  }
-}
-
-template <typename CT, int D>
-constexpr int bwd_occupancy() {
-  return (sizeof(CT) == 2 && D <= 64) ? 2 : 1;
-}
-
-// ---------------------------------------------------------------------------
-// key-parallel reverse pass: dv, dk_main, suffix checkpoints
-
-template <typename CT, int D>
-__global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(BwdParams P) {
-  using TL = Tiles<CT, D>;
-  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float st_s[2][2 * kTileQ];   // lse, -dbs
-  __shared__ float cs_s[2][4 * kTileK];                                // demand checkpoints
-
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
-  if (!item.valid) return;
-  const int64_t slice = item.slice;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const float hf = static_cast<float>(h);
-  const int kb0 = item.idx * 4;
-  const int kb = kb0 + wave;                     // key tile of this wave
-  const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
-  const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
-  const bool active = static_cast<int64_t>(kb) * kTileK < P.T;
-
-  const CT* qs = static_cast<const CT*>(P.q) + slice * P.T * D;
-  const CT* dos = static_cast<const CT*>(P.dout) + slice * P.T * D;
-  const CT* qts = static_cast<const CT*>(P.qt) + slice * D * P.t_pad;
-  const CT* dots = static_cast<const CT*>(P.dot) + slice * D * P.t_pad;
-  const float* lse = P.lse + slice * P.T;
-  const float* dbs = P.dbs + slice * P.T;
-
-  // this wave's keys as B operands (lane <-> key)
-  RowFrag<CT, D> kf, vf;
-  if (key < P.T) {
-    load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
-    load_row_frag<CT, D>(vf, static_cast<const CT*>(P.v) + (slice * P.T + key) * D + h * (D / 2));
-  } else {
-    zero_row_frag<CT, D>(kf);
-    zero_row_frag<CT, D>(vf);
-  }
-  floatx16 dka[kDTiles<D>], dva[kDTiles<D>];
-#pragma unroll
-  for (int t = 0; t < kDTiles<D>; ++t) {
-    dka[t] = floatx16{};
-    dva[t] = floatx16{};
-  }
-  float sufk = 0.f;
-  float* sufk_col = P.sufk + slice * P.nb * P.T + key;
-
-  // a stage: the Q and dO' row tiles, their transposes, the row statistics and
-  // the demand checkpoints of the workgroup's 128 keys entering the tile
-  KTileLoader<CT, D, true, true> ql, dl;        // row tiles in query-split slot order
-  TTileLoader<CT, D> qtl, dtl;
-  RowStatsLoader<2> sl;
-  const int64_t ck = static_cast<int64_t>(kb0) * kTileK + (threadIdx.x & (4 * kTileK - 1));
-  const bool ck_ok = ck < P.T;
-  const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
-  float cr = 0.f;
-  auto fetch = [&](int qt) {
-    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-    ql.load(qs, row0, P.T);
-    dl.load(dos, row0, P.T);
-    qtl.load(qts, row0);
-    dtl.load(dots, row0);
-    sl.load(lse, dbs, dbs, row0, P.T);
-    cr = ccol[static_cast<int64_t>(qt) * P.T];
-  };
-  auto stash = [&](int buf) {
-    ql.store(q_s[buf]);
-    dl.store(do_s[buf]);
-    qtl.store(qt_s[buf]);
-    dtl.store(dot_s[buf]);
-    sl.store(st_s[buf]);
-    if (threadIdx.x < 4 * kTileK) cs_s[buf][threadIdx.x] = ck_ok ? cr : 0.f;
-  };
-  constexpr int kSteps = kTileQ / Mma<CT>::kStep;
-
-  auto step = [&](int qt, int buf, auto diag_tag) {
-    constexpr bool DIAG = decltype(diag_tag)::value;
-    const float* st = st_s[buf];
-    const float cin = cs_s[buf][wave * kTileK + l32];   // demand entering the tile
-    RowFrag<CT, D> qf, dof;
-    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
-    lds_row_frag<CT, D>(dof, do_s[buf], l32, h);
-    float lz[16], ndb[16];
-    lds_read16(st + kTileQ + 16 * h, ndb);
-    // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
-    // and runs under the p / demand chain
-    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
-    lds_read16(st + 16 * h, lz);
-    float p[16], x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
-    if constexpr (DIAG) {
-      const int dk = l32 - 16 * h;               // key - row(i) = dk - i on the diagonal tile
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (dk > i) p[i] = 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = p[i];
-    scan_incl_qs(x, cin + kEps, hf);
-    float sh[16], w[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x[i] = fast_rcp(x[i]);                     // inv
-      sh[i] = p[i] * x[i];
-    }
-    // dv^T += dO'^T sh  (keys in lanes; dO' carries the 1/(S+eps) of A)
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const auto bfr = acc_frag<CT>(sh, s);
-#pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      w[i] = dov[i];                             // ds
-      x[i] = w[i] * (sh[i] * x[i]);              // g = ds sh inv
-    }
-    sufk += scan_suffix_qs(x, sufk, hf);         // x = G
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = fmaf(w[i], sh[i], -p[i] * x[i]);   // p dp
-    // dk_main^T += Q^T (p dp)
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const auto bfr = acc_frag<CT>(w, s);
-#pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dka[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
-    }
-  };
-
-  fetch(nq - 1);
-  stash(0);
-  __syncthreads();
-  int it = 0;
-  for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
-    const int buf = it & 1;
-    fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
-    if (active && qt >= kb) {
-      const float sufk_in = sufk;                // suffix entering this tile from below
-      if (qt > kb) step(qt, buf, std::false_type{});
-      else step(qt, buf, std::true_type{});
-      if (h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
-    }
-    if (qt - 1 >= kb0) stash(buf ^ 1);
-    sync_lds();
-  }
-
-  if (key < P.T) {
-    float* dkrow = P.dkm + (slice * P.T + key) * D;
-    const int64_t dvrow = (slice * P.T + key) * D;
-#pragma unroll
-    for (int t = 0; t < kDTiles<D>; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * t + acc_row(i, h);
-        if (d < D) {
-          dkrow[d] = dka[t][i];
-          store_as(P.dv, dvrow + d, P.gdt, dva[t][i]);
-        }
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// row-parallel dq pass
-
-template <typename CT, int D>
-__global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(BwdParams P) {
-  using TL = Tiles<CT, D>;
-  __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float rs_s[4][2 * kTileQ];   // per wave: lse, -dbs
-  __shared__ float g_s[4][kTileQ];
-
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
-  if (!item.valid) return;
-  const int64_t slice = item.slice;
-  const int g = item.idx;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const float hf = static_cast<float>(h);
-  const int qt = g * 4 + wave;
-  const int64_t r0 = static_cast<int64_t>(qt) * kTileQ;
-  const int64_t wg_last = min(static_cast<int64_t>(g * 4 + 4) * kTileQ, P.T);
-  const int nkt_wg = static_cast<int>((wg_last + kTileK - 1) / kTileK);
-  const int nkt_w = r0 < P.T ? qt + 1 : 0;
-
-  const CT* ks = static_cast<const CT*>(P.k) + slice * P.T * D;
-  const CT* vs = static_cast<const CT*>(P.v) + slice * P.T * D;
-  const CT* kts = static_cast<const CT*>(P.kt) + slice * D * P.t_pad;
-
-  // this wave's rows in QS order: register i of half h <-> row r0 + 16 h + i
-  RowFrag<CT, D> qf, dof;
-  const int64_t my_row = r0 + qsig(l32);
-  if (my_row < P.T) {
-    load_row_frag<CT, D>(qf, static_cast<const CT*>(P.q) + (slice * P.T + my_row) * D + h * (D / 2));
-    load_row_frag<CT, D>(dof, static_cast<const CT*>(P.dout) + (slice * P.T + my_row) * D + h * (D / 2));
-  } else {
-    zero_row_frag<CT, D>(qf);
-    zero_row_frag<CT, D>(dof);
-  }
-  if (h == 0) {
-    const int64_t r = r0 + l32;
-    const bool ok = r < P.T;
-    rs_s[wave][l32] = ok ? P.lse[slice * P.T + r] : INFINITY;
-    rs_s[wave][kTileQ + l32] = ok ? -P.dbs[slice * P.T + r] : 0.f;
-  }
-  constexpr int kSteps = kTileK / Mma<CT>::kStep;
-  typename Mma<CT>::frag ident[kSteps];
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) ident[s] = ident_qs<CT>(l32, h, s);
-  floatx16 dqa[kDTiles<D>];
-#pragma unroll
-  for (int t = 0; t < kDTiles<D>; ++t) dqa[t] = floatx16{};
-  // ghat rides on the dq products as a ones column: column 0 of this tile
-  floatx16 gacc = floatx16{};
-  const auto ones = ones_col_frag<CT>(l32);
-  const float* crow = P.carry + (slice * P.nb + qt) * P.T;
-  const float* srow = P.sufk + (slice * P.nb + qt) * P.T;
-  // demand and suffix checkpoints of this lane's key, loaded one key tile ahead
-  auto ckpt_at = [&](int kt, const float* row) -> float {
-    const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
-    return (kt < nkt_w && key < P.T) ? row[key] : 0.f;
-  };
-
-  auto step = [&](int kt, int buf, float cin, float sin, auto diag_tag) {
-    constexpr bool DIAG = decltype(diag_tag)::value;
-    const float* st = rs_s[wave];
-    RowFrag<CT, D> kf, vf;
-    lds_row_frag<CT, D>(kf, k_s[buf], rho(l32), h);
-    lds_row_frag<CT, D>(vf, v_s[buf], rho(l32), h);
-    float lz[16], ndb[16];
-    lds_read16(st + kTileQ + 16 * h, ndb);
-    // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
-    // and runs under the p / demand chain
-    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
-    lds_read16(st + 16 * h, lz);
-    float p[16], x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
-    if constexpr (DIAG) {
-      const int dk = rho(l32) - 16 * h;          // key - row(i) = dk - i on the diagonal tile
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (dk > i) p[i] = 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = p[i];
-    scan_incl_qs(x, cin + kEps, hf);
-    float sh[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x[i] = fast_rcp(x[i]);                     // inv
-      sh[i] = p[i] * x[i];
-    }
-    float ds[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      ds[i] = dov[i];
-      x[i] = ds[i] * (sh[i] * x[i]);             // g
-    }
-    scan_suffix_qs(x, sin, hf);                  // x = G
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ds[i] = fmaf(ds[i], sh[i], -p[i] * x[i]);   // p dp
-    // transpose (p dp): queries in lanes, keys (natural order) in registers
-    floatx16 xt = floatx16{};
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(ds, s), ident[s], xt);
-    float xv[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) xv[i] = xt[i];
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const auto af = acc_frag<CT>(xv, s);
-#pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
-      gacc = Mma<CT>::mma(af, ones, gacc);
-    }
-  };
-
-  KTileLoader<CT, D, false> kl, vl;
-  TTileLoader<CT, D> ktl;
-  auto fetch = [&](int kt) {
-    const int64_t key0 = static_cast<int64_t>(kt) * kTileK;
-    kl.load(ks, key0, P.T);
-    vl.load(vs, key0, P.T);
-    ktl.load(kts, key0);
-  };
-  auto stash = [&](int buf) {
-    kl.store(k_s[buf]);
-    vl.store(v_s[buf]);
-    ktl.store(kt_s[buf]);
-  };
-  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt_wg; ++kt) {
-    const int buf = kt & 1;
-    const float cin = cin_next, sin = sin_next;
-    if (kt + 1 < nkt_wg) {
-      fetch(kt + 1);
-      cin_next = ckpt_at(kt + 1, crow);
-      sin_next = ckpt_at(kt + 1, srow);
-    }
-    if (kt < qt && kt < nkt_w) step(kt, buf, cin, sin, std::false_type{});
-    else if (kt == qt && kt < nkt_w) step(kt, buf, cin, sin, std::true_type{});
-    if (kt + 1 < nkt_wg) stash(buf ^ 1);
-    sync_lds();
-  }
-
-  // ghat: column 0 of gacc, register i of half h <-> row acc_row(i, h)
-  if (l32 == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) g_s[wave][acc_row(i, h)] = gacc[i];
-  }
-  __syncthreads();
-  if (h == 0 && r0 + l32 < P.T) P.ghat[slice * P.T + r0 + l32] = g_s[wave][l32];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int row = acc_row(i, h);
-    if (r0 + row < P.T) {
-      const float gr = g_s[wave][row];
-      const int64_t base = (slice * P.T + r0 + row) * D;
-#pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t) {
-        const int d = 32 * t + l32;
-        if (d < D) store_as(P.dq, base + d, P.gdt, dqa[t][i] * P.scale - gr * P.pk[base + d]);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// softmax-Jacobian correction of dk
-
-template <typename CT, int D>
-__global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) void bwd_dkcorr(BwdParams P) {
-  using TL = Tiles<CT, D>;
-  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT qgt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float st_s[2][kTileQ];   // lse
-
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);
-  if (!item.valid) return;
-  const int64_t slice = item.slice;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const int kb0 = item.idx * 4;
-  const int kb = kb0 + wave;
-  const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
-  const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
-  const bool active = static_cast<int64_t>(kb) * kTileK < P.T;
-
-  const CT* qs = static_cast<const CT*>(P.q) + slice * P.T * D;
-  const CT* qgts = static_cast<const CT*>(P.qgt) + slice * D * P.t_pad;
-  const float* lse = P.lse + slice * P.T;
-
-  RowFrag<CT, D> kf;
-  if (key < P.T) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
-  else zero_row_frag<CT, D>(kf);
-  floatx16 dkc[kDTiles<D>];
-#pragma unroll
-  for (int t = 0; t < kDTiles<D>; ++t) dkc[t] = floatx16{};
-
-  KTileLoader<CT, D, false, true> ql;            // row tile in query-split slot order
-  TTileLoader<CT, D> qtl;
-  RowStatsLoader<1, false> sl;
-  auto fetch = [&](int qt) {
-    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-    ql.load(qs, row0, P.T);
-    qtl.load(qgts, row0);
-    sl.load(lse, lse, lse, row0, P.T);
-  };
-  auto stash = [&](int buf) {
-    ql.store(q_s[buf]);
-    qtl.store(qgt_s[buf]);
-    sl.store(st_s[buf]);
-  };
-  constexpr int kSteps = kTileQ / Mma<CT>::kStep;
-
-  auto step = [&](int buf, auto diag_tag) {
-    constexpr bool DIAG = decltype(diag_tag)::value;
-    RowFrag<CT, D> qf;
-    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
-    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    float lz[16], p[16];
-    lds_read16(st_s[buf] + 16 * h, lz);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
-    if constexpr (DIAG) {
-      const int dk = l32 - 16 * h;
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (dk > i) p[i] = 0.f;
-    }
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const auto bfr = acc_frag<CT>(p, s);
-#pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dkc[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qgt_s[buf], 32 * t + l32, h, s), bfr, dkc[t]);
-    }
-  };
-
-  fetch(kb0);
-  stash(0);
-  __syncthreads();
-  int it = 0;
-  for (int qt = kb0; qt < nq; ++qt, ++it) {
-    const int buf = it & 1;
-    if (qt + 1 < nq) fetch(qt + 1);
-    if (active) {
-      if (qt > kb) step(buf, std::false_type{});
-      else if (qt == kb) step(buf, std::true_type{});
-    }
-    if (qt + 1 < nq) stash(buf ^ 1);
-    sync_lds();
-  }
-
-  if (key < P.T) {
-    const int64_t base = (slice * P.T + key) * D;
-#pragma unroll
-    for (int t = 0; t < kDTiles<D>; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * t + acc_row(i, h);
-        if (d < D) store_as(P.dk, base + d, P.gdt, (P.dkm[base + d] - dkc[t][i]) * P.scale);
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// host side
-
-struct BwdWorkspace {
-  size_t lse, sinv, dbs, ghat, sufk, dkm, qt, kt, dot, qgt, qc, kc, vc, doc, total;
-};
-
-BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int lowp) {
-  const size_t ct = lowp ? 2 : 4;
-  const int ctc = lowp ? DT_BF16 : DT_F32;
-  const bool convert = dtype != ctc;
-  const bool convert_do = dout_dtype != ctc;
-  const int64_t nb = (T + kTileQ - 1) / kTileQ;
-  const size_t rowf = align_up(4 * n * T);
-  const size_t tsz = align_up(ct * n * D * pad64(T));
-  const size_t rsz = align_up(ct * n * T * D);
-  BwdWorkspace w{};
-  w.lse = 0;
-  w.sinv = w.lse + rowf;
-  w.dbs = w.sinv + rowf;
-  w.ghat = w.dbs + rowf;
-  w.sufk = w.ghat + rowf;
-  w.dkm = w.sufk + align_up(4 * n * nb * T);
-  w.qt = w.dkm + align_up(4 * n * T * D);
-  w.kt = w.qt + tsz;
-  w.dot = w.kt + tsz;
-  w.qgt = w.dot + tsz;
-  w.qc = w.qgt + tsz;
-  w.kc = w.qc + (convert ? rsz : 0);
-  w.vc = w.kc + (convert ? rsz : 0);
-  w.doc = w.vc + (convert ? rsz : 0);
-  w.total = w.doc + rsz;                      // dO' (dO scaled by sinv) is always built
-  (void)convert_do;
-  return w;
-}
-
-template <typename CT, int D>
-int launch_backward(const BackwardArgs& a) {
-  // the workspace is sized for the worst case (dout converted), so that the
-  // size query need not know dout's dtype
-  const int ctc = sizeof(CT) == 2 ? DT_BF16 : DT_F32;
-  const BwdWorkspace w = bwd_layout(a.n, a.T, D, a.dtype, ctc == DT_BF16 ? DT_F32 : DT_BF16, a.lowp);
-  char* ws = static_cast<char*>(a.workspace);
-  hipStream_t st = static_cast<hipStream_t>(a.stream);
-  const bool convert = a.dtype != ctc;
-  const int64_t t_pad = pad64(a.T);
-  const unsigned n = static_cast<unsigned>(a.n);
-  const int64_t sn = a.T * D;
-
-  CT* qt = reinterpret_cast<CT*>(ws + w.qt);
-  CT* kt = reinterpret_cast<CT*>(ws + w.kt);
-  CT* dot = reinterpret_cast<CT*>(ws + w.dot);
-  CT* qgt = reinterpret_cast<CT*>(ws + w.qgt);
-  CT* qc = convert ? reinterpret_cast<CT*>(ws + w.qc) : nullptr;
-  CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
-  CT* vc = convert ? reinterpret_cast<CT*>(ws + w.vc) : nullptr;
-  CT* doc = reinterpret_cast<CT*>(ws + w.doc);
-
-  const dim3 gp(static_cast<unsigned>(t_pad / 64), n);
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt, D * t_pad,
-                                                        t_pad, nullptr));
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt, D * t_pad,
-                                                        t_pad, nullptr));
-  if (convert)
-    DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn, nullptr, 0,
-                                                          t_pad, nullptr));
-
-  BwdParams P{};
-  P.q = convert ? static_cast<const void*>(qc) : a.q;
-  P.k = convert ? static_cast<const void*>(kc) : a.k;
-  P.v = convert ? static_cast<const void*>(vc) : a.v;
-  P.dout = doc;
-  P.qt = qt;
-  P.kt = kt;
-  P.dot = dot;
-  P.qgt = qgt;
-  P.T = a.T;
-  P.t_pad = t_pad;
-  P.nb = (a.T + kTileQ - 1) / kTileQ;
-  P.scale = 1.f / sqrtf(static_cast<float>(D));
-  P.c = kLog2e * P.scale;
-  float* lse = reinterpret_cast<float*>(ws + w.lse);
-  float* sinv = reinterpret_cast<float*>(ws + w.sinv);
-  float* dbs = reinterpret_cast<float*>(ws + w.dbs);
-  P.lse = lse;
-  P.sinv = sinv;
-  P.dbs = dbs;
-  P.ghat = reinterpret_cast<float*>(ws + w.ghat);
-  P.carry = a.carry;
-  P.sufk = reinterpret_cast<float*>(ws + w.sufk);
-  P.dkm = reinterpret_cast<float*>(ws + w.dkm);
-  P.pk = a.pk;
-  P.dq = a.dq;
-  P.dk = a.dk;
-  P.dv = a.dv;
-  P.gdt = a.grad_dtype;
-
-  const int64_t rows = a.n * a.T;
-  const int64_t threads = rows * (D / 8);
-  DIL_TIMED("bwd_rows", st,
-            bwd_rows<D><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
-                a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbs, rows));
-  // dO' = dO / (S + eps), row-major and transposed, in the compute type
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot,
-                                                        D * t_pad, t_pad, sinv));
-  const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
-  P.n = a.n;
-  P.kgroups = (nkt + 3) / 4;
-  const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
-  DIL_TIMED("bwd_key", st, bwd_key<CT, D><<<gkey, kThreads, 0, st>>>(P));
-  DIL_TIMED("bwd_query", st, bwd_query<CT, D><<<gkey, kThreads, 0, st>>>(P));
-  DIL_TIMED("prep", st,
-            prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), n), kThreads, 0, st>>>(
-                qt, P.ghat, a.T, t_pad, qgt));
-  DIL_TIMED("bwd_dkcorr", st, bwd_dkcorr<CT, D><<<gkey, kThreads, 0, st>>>(P));
-  return static_cast<int>(hipGetLastError());
-}
 
 template <int D>
 int dispatch_backward(const BackwardArgs& a) {
@@ -734,6 +21,19 @@ int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, 
 }
 
 int backward(const BackwardArgs& a) {
+  if (const int err = check_variant(a.var, a.head_dim)) return err;
+  if (a.var.bid != BID_SOFTMAX || a.var.share != SHARE_INCL) {
+    switch (a.var.bid) {
+      case 0: return backward_bid<0>(a);
+      case 1: return backward_bid<1>(a);
+      case 2: return backward_bid<2>(a);
+      case 3: return backward_bid<3>(a);
+      case 4: return backward_bid<4>(a);
+      case 5: return backward_bid<5>(a);
+      case 6: return backward_bid<6>(a);
+      default: return backward_bid<7>(a);
+    }
+  }
   switch (a.head_dim) {
     case 16: return dispatch_backward<16>(a);
     case 32: return dispatch_backward<32>(a);

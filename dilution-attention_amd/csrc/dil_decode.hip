@@ -1,305 +1,9 @@
-// Cached decode step: one new query row per (batch, head) slice against
-// `length` cached keys, with the per-key fp32 demand vector advanced in place.
-//
-// Reference behaviour: /root/reference/src/dilution/kernels.py:937-991
-// (_dilution_decode) and :994-1038 (dilution_decode_step).  The reference runs
-// one program per slice; here the keys are split into chunks so the grid fills
-// 256 CUs, in three launches:
-//
-//   dec_stats  (chunks x n): a_j = q.k_j * scale*log2e -> fp32 scratch AFF,
-//                            chunk-local (max, sum 2^(a-max))
-//   dec_apply  (chunks x n): combine the chunk statistics -> lse; for every key
-//                            p = 2^(a-lse), share = p / (committed + p + eps),
-//                            chunk partials sum(share), sum(share * v);
-//                            committed += p stored in place
-//   dec_finish (n):          out = sum(share * v) / (sum(share) + eps) in the
-//                            query dtype (chunk partials summed in chunk order)
-//
-// HBM bytes per key: K and V rows (2*D*elt) + demand read+write (8) + AFF
-// write+read (8).  K and V are streamed once with 16-byte non-temporal loads.
-#include "dil_common.hpp"
-#include "dil_internal.hpp"
+// Entry points of the cached decode step: the production operator for every
+// head_dim and dtype; the ablation variants are built in dil_variants.hip
+// (head_dim 64) and reached through decode_bid<BID>.
+#include "dil_decode_impl.hpp"
 
 namespace dil {
-
-namespace {
-
-// Measured on MI355X at 128K context, B16 H16 d64 bf16 (sweep over 128-1024
-// threads, 1-4 rows in flight, 512-8192-key chunks): 1024-thread workgroups
-// with two rows in flight per lane over 2048-key chunks stream fastest.
-constexpr int kDecThreads = 1024;
-constexpr int kDecWaves = kDecThreads / 64;
-constexpr int kDecUnroll = 2;          // cached rows in flight per lane
-
-template <int D>
-struct DecLayout {
-  static constexpr int kLanesPerRow = D / 8;          // each lane owns 8 consecutive d
-  static constexpr int kRowsPerWave = 64 / kLanesPerRow;
-  static constexpr int kRowsPerBlock = kRowsPerWave * kDecWaves;
-};
-
-// Sum over the kLanesPerRow lanes that share one cached row, with DPP lane
-// moves (no LDS traffic).  The full sum is guaranteed only in the first lane
-// of each row group (lane % LPR == 0), the only lane that consumes it.
-template <int LPR>
-__device__ __forceinline__ float row_reduce(float x) {
-  constexpr int kQuadXor1 = 0xB1;      // quad_perm [1, 0, 3, 2]
-  constexpr int kQuadXor2 = 0x4E;      // quad_perm [2, 3, 0, 1]
-  constexpr int kRowShl4 = 0x104;      // row_shl:4
-  constexpr int kRowShl8 = 0x108;      // row_shl:8
-  if constexpr (LPR >= 2)
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQuadXor1, 0xF, 0xF, true));
-  if constexpr (LPR >= 4)
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQuadXor2, 0xF, 0xF, true));
-  if constexpr (LPR >= 8)
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowShl4, 0xF, 0xF, true));
-  if constexpr (LPR >= 16)
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowShl8, 0xF, 0xF, true));
-  return x;
-}
-
-// 8 consecutive cached elements of storage dtype DT as fp32, read with a
-// non-temporal hint (the cache is streamed once per step).
-template <int DT>
-__device__ __forceinline__ void load8_stream(const void* base, int64_t idx, float (&o)[8]) {
-  if constexpr (DT == DT_F32) {
-    const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + idx);
-    const floatx4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
-    o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
-    o[4] = b[0]; o[5] = b[1]; o[6] = b[2]; o[7] = b[3];
-  } else {
-    const u16x8 r = __builtin_nontemporal_load(
-        reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(base) + idx));
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o[e] = (DT == DT_BF16) ? bf16_bits_to_f32(r[e]) : f16_bits_to_f32(r[e]);
-  }
-}
-
-template <int D, int DT>
-__global__ __launch_bounds__(kDecThreads) void dec_stats(
-    const void* __restrict__ q1, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
-    float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
-    float qscale) {
-  using L = DecLayout<D>;
-  const int64_t slice = blockIdx.y;
-  const int c = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
-  const int64_t j0 = c * chunk;
-  const int64_t j1 = min(j0 + chunk, length);
-
-  float q[8];
-  load8_f32(q1, slice * q_sn + sub * 8, DT, q);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) q[e] *= qscale;
-
-  const int64_t kbase = slice * kv_sn + sub * 8;
-  float* arow = aff + slice * length;
-  float m = -INFINITY, s = 0.f;
-  constexpr int U = kDecUnroll;
-  for (int64_t jb = j0 + wave * L::kRowsPerWave + rw; jb < j1; jb += (int64_t)U * L::kRowsPerBlock) {
-    float kv[U][8];
-    bool ok[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
-      ok[u] = j < j1;
-      if (ok[u]) load8_stream<DT>(kc, kbase + j * D, kv[u]);
-    }
-    float a[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float dot = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dot = fmaf(q[e], ok[u] ? kv[u][e] : 0.f, dot);
-      a[u] = row_reduce<L::kLanesPerRow>(dot);
-    }
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
-      if (ok[u]) {
-        if (sub == 0) arow[j] = a[u];
-        tmax = fmaxf(tmax, a[u]);
-      }
-    }
-    if (tmax > -INFINITY) {
-      const float mn = fmaxf(m, tmax);
-      float add = 0.f;
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (ok[u]) add += fast_exp2(a[u] - mn);
-      s = s * fast_exp2(m - mn) + add;
-      m = mn;
-    }
-  }
-  // Lanes of one row hold identical (m, s); count each row once.
-  if (sub != 0) { m = -INFINITY; s = 0.f; }
-  const float wm = wave_max(m);
-  float ws = wave_sum(m == -INFINITY ? 0.f : s * fast_exp2(m - wm));
-  __shared__ float sm[kDecWaves], ss[kDecWaves];
-  if (lane == 0) { sm[wave] = wm; ss[wave] = ws; }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float bm = -INFINITY;
-    for (int w = 0; w < kDecWaves; ++w) bm = fmaxf(bm, sm[w]);
-    float bs = 0.f;
-    for (int w = 0; w < kDecWaves; ++w)
-      if (sm[w] > -INFINITY) bs += ss[w] * fast_exp2(sm[w] - bm);
-    part[slice * nchunk + c] = make_float2(bm, bs);
-  }
-}
-
-template <int D, int DT>
-__global__ __launch_bounds__(kDecThreads) void dec_apply(
-    const void* __restrict__ vc, int64_t kv_sn, float* __restrict__ committed, int64_t c_sn,
-    const float* __restrict__ aff, const float2* __restrict__ part, float* __restrict__ part_out,
-    int64_t length, int64_t chunk, int nchunk) {
-  using L = DecLayout<D>;
-  const int64_t slice = blockIdx.y;
-  const int c = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
-
-  // Combine the chunk statistics of this slice (every wave redundantly).
-  float m = -INFINITY, s = 0.f;
-  for (int i = lane; i < nchunk; i += 64) {
-    const float2 ps = part[slice * nchunk + i];
-    const float mn = fmaxf(m, ps.x);
-    if (mn > -INFINITY) {
-      s = s * fast_exp2(m - mn) + ps.y * fast_exp2(ps.x - mn);
-      m = mn;
-    }
-  }
-  const float gm = wave_max(m);
-  const float gs = wave_sum(m == -INFINITY ? 0.f : s * fast_exp2(m - gm));
-  const float lse = gm + __log2f(gs);
-
-  const int64_t j0 = c * chunk;
-  const int64_t j1 = min(j0 + chunk, length);
-  const float* arow = aff + slice * length;
-  float* crow = committed + slice * c_sn;
-  const int64_t vbase = slice * kv_sn + sub * 8;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float ssum = 0.f;
-  constexpr int U = kDecUnroll;
-  for (int64_t jb = j0 + wave * L::kRowsPerWave + rw; jb < j1; jb += (int64_t)U * L::kRowsPerBlock) {
-    float vv[U][8], a[U], cm[U];
-    bool ok[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
-      ok[u] = j < j1;
-      if (ok[u]) {
-        load8_stream<DT>(vc, vbase + j * D, vv[u]);
-        a[u] = arow[j];
-        cm[u] = crow[j];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!ok[u]) continue;
-      const int64_t j = jb + (int64_t)u * L::kRowsPerBlock;
-      const float p = fast_exp2(a[u] - lse);
-      const float sh = p * fast_rcp(cm[u] + p + kEps);
-      if (sub == 0) crow[j] = cm[u] + p;
-      ssum += sh;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(sh, vv[u][e], acc[e]);
-    }
-  }
-  // Reduce over lanes holding the same d-slice, then over waves.
-#pragma unroll
-  for (int o = L::kLanesPerRow; o < 64; o <<= 1) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
-    ssum += __shfl_xor(ssum, o, 64);
-  }
-  __shared__ float red[kDecWaves][D + 1];
-  if (rw == 0) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) red[wave][sub * 8 + e] = acc[e];
-    if (sub == 0) red[wave][D] = ssum;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i <= D; i += kDecThreads) {
-    float t = 0.f;
-    for (int w = 0; w < kDecWaves; ++w) t += red[w][i];
-    part_out[(slice * nchunk + c) * (D + 1) + i] = t;
-  }
-}
-
-// One workgroup (256 threads > D) per slice: thread d < D sums column d of
-// the chunk partials, thread D the share totals, four chunks at a time.
-template <int D>
-__global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part_out, int nchunk,
-                                                  void* __restrict__ out, int64_t o_sn, int dt) {
-  const int64_t slice = blockIdx.x;
-  const float* base = part_out + slice * nchunk * (D + 1);
-  __shared__ float tot_s;
-  if (threadIdx.x == D) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-    int c = 0;
-    for (; c + 4 <= nchunk; c += 4) {
-      s0 += base[(c + 0) * (D + 1) + D];
-      s1 += base[(c + 1) * (D + 1) + D];
-      s2 += base[(c + 2) * (D + 1) + D];
-      s3 += base[(c + 3) * (D + 1) + D];
-    }
-    for (; c < nchunk; ++c) s0 += base[c * (D + 1) + D];
-    tot_s = (s0 + s1) + (s2 + s3);
-  }
-  float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
-  const int d = threadIdx.x;
-  if (d < D) {
-    int c = 0;
-    for (; c + 4 <= nchunk; c += 4) {
-      t0 += base[(c + 0) * (D + 1) + d];
-      t1 += base[(c + 1) * (D + 1) + d];
-      t2 += base[(c + 2) * (D + 1) + d];
-      t3 += base[(c + 3) * (D + 1) + d];
-    }
-    for (; c < nchunk; ++c) t0 += base[c * (D + 1) + d];
-  }
-  __syncthreads();
-  if (d < D) store_as(out, slice * o_sn + d, dt, ((t0 + t1) + (t2 + t3)) / (tot_s + kEps));
-}
-
-// Keys per workgroup (see kDecThreads).
-int64_t decode_chunk(int64_t n, int64_t length) {
-  (void)n;
-  (void)length;
-  return 2048;
-}
-
-template <int D, int DT>
-int launch_decode(const DecodeArgs& a) {
-  const int64_t chunk = decode_chunk(a.n, a.length);
-  const int nchunk = static_cast<int>((a.length + chunk - 1) / chunk);
-  char* ws = static_cast<char*>(a.workspace);
-  float* aff = reinterpret_cast<float*>(ws);
-  size_t off = align_up(sizeof(float) * a.n * a.length);
-  float2* part = reinterpret_cast<float2*>(ws + off);
-  off += align_up(sizeof(float2) * a.n * nchunk);
-  float* part_out = reinterpret_cast<float*>(ws + off);
-  const float qscale = kLog2e / sqrtf(static_cast<float>(D));
-  hipStream_t st = static_cast<hipStream_t>(a.stream);
-  dim3 grid(nchunk, static_cast<unsigned>(a.n));
-  DIL_TIMED("dec_stats", st,
-            dec_stats<D, DT><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff,
-                                                           part, a.length, chunk, nchunk, qscale));
-  DIL_TIMED("dec_apply", st,
-            dec_apply<D, DT><<<grid, kDecThreads, 0, st>>>(a.v_cache, a.kv_sn, a.committed, a.c_sn,
-                                                           aff, part, part_out, a.length, chunk,
-                                                           nchunk));
-  DIL_TIMED("dec_finish", st,
-            dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
-                                                                             a.o_sn, a.dtype));
-  return static_cast<int>(hipGetLastError());
-}
-
-}  // namespace
 
 int64_t decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
   const int64_t chunk = decode_chunk(n, length);
@@ -320,6 +24,19 @@ int decode_dtype(const DecodeArgs& a) {
 }
 
 int decode_step(const DecodeArgs& a) {
+  if (const int err = check_variant(a.var, a.head_dim)) return err;
+  if (a.var.bid != BID_SOFTMAX || a.var.share != SHARE_INCL) {
+    switch (a.var.bid) {
+      case 0: return decode_bid<0>(a);
+      case 1: return decode_bid<1>(a);
+      case 2: return decode_bid<2>(a);
+      case 3: return decode_bid<3>(a);
+      case 4: return decode_bid<4>(a);
+      case 5: return decode_bid<5>(a);
+      case 6: return decode_bid<6>(a);
+      default: return decode_bid<7>(a);
+    }
+  }
   switch (a.head_dim) {
     case 16: return decode_dtype<16>(a);
     case 32: return decode_dtype<32>(a);

@@ -1,0 +1,730 @@
+// Forward of the dilution-attention operator (plain forward and chunked
+// prefill share these kernels).
+//
+// Reference behaviour: dilution_attention_forward,
+// /root/reference/src/dilution/kernels.py:328-455, whose row-parallel
+// decomposition (K1 :137-198, block scan :251-264, K2 :267-315) this
+// follows in its statistics and output passes; the kernels are written for
+// gfx950 MFMA layouts:
+//
+//   prep       convert q/k to the MFMA operand type when needed; write V^T
+//              (and K^T for pk) as contiguous (D, 32) tiles per 32 keys,
+//              zero-padded to a multiple of 64 keys.
+//   fwd_stats  row-parallel: one workgroup = 4 waves = 4 tiles of 32 query
+//              rows, key tiles of 32 staged in LDS.  S^T = K Q^T puts one query
+//              per lane: online row max and 2^-sum (log2 domain, lazily moved
+//              offset), and optionally pk^T = K^T p^T on MFMA.
+//   fwd_demand key-parallel: one wave per 32 keys walks the 32-row blocks in
+//              causal order with the fp64 running column sum of p (plus any
+//              incoming prefill demand) in a register, writing the demand that
+//              enters every block (the carry checkpoints) and the totals
+//              (committed_total, the decode accumulator).
+//   fwd_out    row-parallel: S = Q K^T with keys in lanes: p, the in-tile
+//              column scan on registers plus the checkpoint, share = p /
+//              (demand + p + eps), row sums; the share tile is transposed by
+//              one MFMA against an identity operand so that share @ V runs on
+//              MFMA with queries in lanes.  out = (share @ V) / (rowsum + eps).
+//
+// Nothing T x T is stored: scratch is the (n, C/32, Tk) fp32 checkpoint array.
+#pragma once
+
+#include "dil_common.hpp"
+#include "dil_internal.hpp"
+#include "dil_tiles.hpp"
+#include "dil_variant.hpp"
+
+#include <type_traits>
+
+namespace dil {
+
+namespace {
+
+struct FwdParams {
+  const void* q;          // CT rows (n, C, D), slice stride q_sn
+  int64_t q_sn;
+  const void* k;          // CT rows (n, >= Tk, D), slice stride k_sn
+  int64_t k_sn;
+  const void* vt;         // CT V^T, tile-major (Tk_pad rows per slice)
+  const void* kt;         // CT K^T, tile-major, or null
+  int64_t t_sn, tk_pad;
+  int64_t C, Tk, q0, nb;
+  int64_t n;              // slices
+  int groups;             // 128-row groups per slice
+  int kgroups;            // 128-key groups per slice
+  float c;                // log2(e) / sqrt(D)
+  float scale;            // 1 / sqrt(D)
+  float shift, lshift;    // SHIFT of the expshift / sigshift bids and log2(SHIFT)
+  float* out;
+  int64_t o_sn;
+  float* rmax;
+  float* rden;
+  float* ssum;
+  float* carry;           // (n, nb, Tk)
+  const float* demand_in;
+  int64_t din_sn;
+  float* total;
+  int64_t tot_sn;
+  float* pk;
+};
+
+// ---------------------------------------------------------------------------
+// Per-wave tile bounds.  A wave owns query rows [r0, r0 + 32) of the chunk
+// (absolute rows qa0 = q0 + r0 ...).  Key tile kt (keys [32 kt, 32 kt + 32))
+// needs no causal mask when kt < kfull and contributes nothing when
+// kt >= kend.
+
+struct WaveRows {
+  int64_t r0, qa0;
+  int kfull, kend;
+  bool on;
+};
+
+__device__ __forceinline__ WaveRows wave_rows(const FwdParams& P, int g, int wave) {
+  WaveRows w;
+  w.r0 = (static_cast<int64_t>(g) * 4 + wave) * kTileQ;
+  w.qa0 = P.q0 + w.r0;
+  w.on = w.r0 < P.C;
+  const int64_t qlast = min(w.qa0 + kTileQ - 1, P.q0 + P.C - 1);
+  w.kend = w.on ? static_cast<int>(qlast / kTileK) + 1 : 0;
+  w.kfull = w.on ? static_cast<int>((w.qa0 + 1) / kTileK) : 0;
+  return w;
+}
+
+// Key tiles the workgroup (4 consecutive row tiles of group g) has to stage.
+__device__ __forceinline__ int group_key_tiles(const FwdParams& P, int g) {
+  const int64_t qlast = min(P.q0 + (static_cast<int64_t>(g) * 4 + 4) * kTileQ - 1, P.q0 + P.C - 1);
+  return static_cast<int>(qlast / kTileK) + 1;
+}
+
+// Running maximum moves only when a tile exceeds it by this much (in units
+// of the scaled log2 affinity), so the rescaling of the sums is rare; the
+// terms 2^(a - m) then stay below 2^8.
+constexpr float kLazyMax = 8.f;
+
+// ---------------------------------------------------------------------------
+// row statistics (+ pk) and per-32-row-block column sums of p
+
+template <typename CT, int D, bool PK, int BID = BID_SOFTMAX>
+__global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
+  using T = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
+  __shared__ __attribute__((aligned(16))) CT kttile[PK ? 2 : 1][PK ? D * T::kTStride : 1];
+  const WorkItem item = xcd_work_item(P.groups, P.n, true);   // heavy (late) row groups first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int g = item.idx;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const WaveRows W = wave_rows(P, g, wave);
+  const int nkt_wg = group_key_tiles(P, g);
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
+  const CT* ks = static_cast<const CT*>(P.k) + slice * P.k_sn;
+  const CT* kts = PK ? static_cast<const CT*>(P.kt) + slice * P.t_sn : nullptr;
+
+  // Q rows in natural order: the B operand of sweep 1 (lane <-> query) and the
+  // A operand of sweep 2 (register rows <-> queries)
+  RowFrag<CT, D> qf;
+  const bool row_ok = W.r0 + l32 < P.C;
+  if (row_ok) load_row_frag<CT, D>(qf, qs + (W.r0 + l32) * D + h * (D / 2));
+  else zero_row_frag<CT, D>(qf);
+  const int my_q = static_cast<int>(W.qa0) + l32;      // query of this lane in sweep 1
+
+  if constexpr (!bid_normalized<BID>()) {
+    // elementwise bids keep no row statistics (kernels_bid.py:338-349)
+    if (h == 0 && row_ok) {
+      P.rmax[slice * P.C + W.r0 + l32] = 0.f;
+      P.rden[slice * P.C + W.r0 + l32] = BID == BID_EXPSHIFT ? P.shift : 1.f;
+    }
+    return;
+  }
+
+  KTileLoader<CT, D, false> kl;
+  TTileLoader<CT, D> tl;
+
+  // ---- sweep 1: S^T = K Q^T (lane <-> query, registers <-> keys) ----
+  // softmax: m, the offset the sums are taken against (moves lazily), and mx,
+  // the exact max; ratio bids: l = the row sum of the numerators, mn = the
+  // row minimum of a (minshift)
+  float m = -INFINITY, mx = -INFINITY, l0 = 0.f, l1 = 0.f, mn = INFINITY;
+  floatx16 pka[PK ? kDTiles<D> : 1];
+  if constexpr (PK) {
+#pragma unroll
+    for (int t = 0; t < kDTiles<D>; ++t) pka[t] = floatx16{};
+  }
+  const float thresh = kLazyMax / P.c;                 // in raw score units
+  auto stats_step = [&](int kt, int buf, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> kf;
+    lds_row_frag<CT, D>(kf, ktile[buf], rho(l32), h);
+    const floatx16 acc = mma_rows<CT, D>(kf, qf, floatx16{});
+    float a[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a[i] = acc[i];
+    if constexpr (bid_ratio<BID>()) {
+      // numerators f(a) and Jacobian numerators u(a) on the causal window
+      const int dq = kt * kTileK + 8 * h - my_q;
+      float e[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const bool ok = !DIAG || 16 * (i >> 3) + (i & 7) + dq <= 0;
+        const float av = a[i] * P.scale;
+        const float f = ok ? bid_f<BID>(av) : 0.f;
+        if (i & 1) l1 += f;
+        else l0 += f;
+        if constexpr (BID == BID_MINSHIFT) mn = ok ? fminf(mn, av) : mn;
+        e[i] = ok ? bid_u<BID>(av) : 0.f;
+      }
+      if constexpr (PK) {
+#pragma unroll
+        for (int s = 0; s < kTileK / Mma<CT>::kStep; ++s) {
+          const auto bfr = acc_frag<CT>(e, s);
+#pragma unroll
+          for (int t = 0; t < kDTiles<D>; ++t)
+            pka[t] = Mma<CT>::mma(lds_t_frag<CT, D>(kttile[buf], 32 * t + l32, h, s), bfr, pka[t]);
+        }
+      }
+      return;
+    }
+    if constexpr (DIAG) {
+      const int dq = kt * kTileK + 8 * h - my_q;       // key - query for register i: perm_row(i, 0) + dq
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (16 * (i >> 3) + (i & 7) + dq > 0) a[i] = -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(a[0], a[1]), a[2]);
+#pragma unroll
+    for (int i = 3; i < 15; i += 2) tmax = fmaxf(fmaxf(tmax, a[i]), a[i + 1]);
+    tmax = fmaxf(tmax, a[15]);
+    const HalfPair tp = halves(tmax);                  // one running max per query (both halves)
+    tmax = fmaxf(tp.lo, tp.hi);
+    mx = fmaxf(mx, tmax);
+    const bool take = tmax > m + thresh;
+    if (__any(take)) {
+      const float mnew = take ? tmax : m;
+      const float alpha = take ? (m == -INFINITY ? 0.f : fast_exp2((m - mnew) * P.c)) : 1.f;
+      l0 *= alpha;
+      l1 *= alpha;
+      if constexpr (PK) {
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t) pka[t] *= alpha;
+      }
+      m = mnew;
+    }
+    const float mc = m * P.c;
+    float e[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) e[i] = fast_exp2(fmaf(a[i], P.c, -mc));
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      l0 += e[i];
+      l1 += e[i + 1];
+    }
+    if constexpr (PK) {
+#pragma unroll
+      for (int s = 0; s < kTileK / Mma<CT>::kStep; ++s) {
+        const auto bfr = acc_frag<CT>(e, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          pka[t] = Mma<CT>::mma(lds_t_frag<CT, D>(kttile[buf], 32 * t + l32, h, s), bfr, pka[t]);
+      }
+    }
+  };
+
+  kl.load(ks, 0, P.Tk);
+  if constexpr (PK) tl.load(kts, 0);
+  kl.store(ktile[0]);
+  if constexpr (PK) tl.store(kttile[0]);
+  __syncthreads();
+  for (int kt = 0; kt < nkt_wg; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nkt_wg) {
+      const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
+      kl.load(ks, key0n, P.Tk);
+      if constexpr (PK) tl.load(kts, key0n);
+    }
+    if (kt < W.kfull) stats_step(kt, buf, std::false_type{});
+    else if (kt < W.kend) stats_step(kt, buf, std::true_type{});
+    if (kt + 1 < nkt_wg) {
+      kl.store(ktile[buf ^ 1]);
+      if constexpr (PK) tl.store(kttile[buf ^ 1]);
+    }
+    sync_lds();
+  }
+  const HalfPair lp = halves(l0 + l1);                 // the halves share m
+  float ltot, rmax_v, pk_f;
+  if constexpr (bid_ratio<BID>()) {
+    // R = sum of the numerators; minshift: sum(a - min) = sum(a) - window * min
+    ltot = lp.lo + lp.hi;
+    rmax_v = 0.f;
+    if constexpr (BID == BID_MINSHIFT) {
+      const HalfPair mp = halves(mn);
+      rmax_v = fminf(mp.lo, mp.hi);                    // the rmax buffer holds the row minimum
+      ltot = fmaxf(ltot - static_cast<float>(my_q + 1) * rmax_v, 0.f);
+    }
+    pk_f = ltot > 0.f ? P.scale / ltot : 0.f;          // jac = u / R (0 on an empty row)
+  } else {
+    // re-reference the sum to the exact row maximum: p = 2^(a c - rmax) / rden
+    ltot = (lp.lo + lp.hi) * fast_exp2((m - mx) * P.c);
+    rmax_v = mx * P.c;
+    pk_f = P.scale / (lp.lo + lp.hi);                  // pk was accumulated against m
+  }
+  if (h == 0 && row_ok) {
+    P.rmax[slice * P.C + W.r0 + l32] = rmax_v;
+    P.rden[slice * P.C + W.r0 + l32] = ltot;
+  }
+  if constexpr (PK) {
+    if (row_ok) {
+      const float f = pk_f;
+      float* dst = P.pk + (slice * P.C + W.r0 + l32) * D;
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * t + acc_row(i, h) < D) dst[32 * t + acc_row(i, h)] = pka[t][i] * f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// demand checkpoints: key-parallel walk over the chunk's 32-row blocks
+//
+// One wave per 32-key tile (lane <-> key).  Walking the row blocks in causal
+// order it carries each key's demand -- the incoming demand of rows before the
+// chunk plus the column sums of p over the chunk rows seen so far -- in an
+// fp64 register, stores it as the checkpoint of every block (the demand
+// entering the block) and finally as the key's total.
+
+template <typename CT, int D, int BID = BID_SOFTMAX>
+__global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) void fwd_demand(FwdParams P) {
+  using T = Tiles<CT, D>;
+  constexpr int kRP = BID == BID_SOFTMAX ? 1 : 2;                  // per-row parameters
+  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * T::kKStride];
+  __shared__ __attribute__((aligned(16))) float st_s[2][kRP][kTileQ];   // (r0, r1) of the block's rows
+
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int kb = item.idx * 4 + wave;
+  const int64_t key0 = static_cast<int64_t>(kb) * kTileK;
+  const int64_t key = key0 + l32;
+  const bool key_ok = key < P.Tk;
+
+  // Block b holds chunk rows [32 b, 32 b + 32) = absolute rows q0 + 32 b + [0, 32).
+  // A key tile meets block b when the block's last row reaches its first key;
+  // it needs no mask once the block's first row is past its last key.
+  auto first_block = [&](int64_t k0) -> int64_t {
+    const int64_t t = k0 - P.q0 - (kTileQ - 1);
+    return t > 0 ? (t + kTileQ - 1) / kTileQ : 0;
+  };
+  const int64_t b_wg = first_block(static_cast<int64_t>(item.idx) * 4 * kTileK);
+  const int64_t b_w = first_block(key0);
+  const int64_t nb = P.nb;
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
+  const float* rmax = P.rmax + slice * P.C;
+  const float* rden = P.rden + slice * P.C;
+
+  RowFrag<CT, D> kf;
+  if (key_ok) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + slice * P.k_sn + key * D + h * (D / 2));
+  else zero_row_frag<CT, D>(kf);
+
+  double run = (P.demand_in != nullptr && key < P.q0 && key_ok)
+                   ? static_cast<double>(P.demand_in[slice * P.din_sn + key]) : 0.0;
+  float* ccol = P.carry + slice * nb * P.Tk + key;
+
+  KTileLoader<CT, D> ql;
+  float rmax_r = 0.f, rden_r = 1.f;
+  bool row_ok = false;
+  int64_t it_row0 = 0;                       // first chunk row of the fetched block
+  auto fetch = [&](int64_t b) {
+    it_row0 = b * kTileQ;
+    ql.load(qs, b * kTileQ, P.C);
+    const int64_t r = b * kTileQ + (threadIdx.x & (kTileQ - 1));
+    row_ok = r < P.C;
+    rmax_r = rmax[min(r, P.C - 1)];
+    rden_r = rden[min(r, P.C - 1)];
+  };
+  auto stash = [&](int buf) {
+    ql.store(q_s[buf]);
+    if (threadIdx.x < kTileQ) {
+      if constexpr (BID == BID_SOFTMAX) {
+        st_s[buf][0][threadIdx.x] = row_ok ? rmax_r + __log2f(rden_r) : INFINITY;
+      } else {
+        float r0, r1;
+        const float window = static_cast<float>(P.q0 + (it_row0 + threadIdx.x) + 1);
+        bid_row_params<BID>(rmax_r, rden_r, window, row_ok, r0, r1);
+        st_s[buf][0][threadIdx.x] = r0;
+        st_s[buf][1][threadIdx.x] = r1;
+      }
+    }
+  };
+
+  auto step = [&](int64_t b, int buf, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> qf;
+    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);
+    const floatx16 acc = mma_rows<CT, D>(qf, kf, floatx16{});   // register i <-> row acc_row(i, h)
+    float p[16];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const floatx4 r0 = *reinterpret_cast<const floatx4*>(&st_s[buf][0][8 * u + 4 * h]);
+      if constexpr (BID == BID_SOFTMAX) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[4 * u + e] = fast_exp2(fmaf(acc[4 * u + e], P.c, -r0[e]));
+      } else {
+        const floatx4 r1 = *reinterpret_cast<const floatx4*>(&st_s[buf][kRP - 1][8 * u + 4 * h]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[4 * u + e] = bid_p<BID>(acc[4 * u + e], P.c, P.scale, r0[e], r1[e], P.lshift);
+      }
+    }
+    if constexpr (DIAG) {
+      // key - row for register i: dq - (8 (i >> 2) + (i & 3))
+      const int dq = static_cast<int>(key - P.q0 - b * kTileQ) - 4 * h;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dq > 8 * (i >> 2) + (i & 3)) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] += p[i + 8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] += p[i + 4];
+    const HalfPair cp = halves((p[0] + p[1]) + (p[2] + p[3]));
+    run += static_cast<double>(cp.lo + cp.hi);
+  };
+
+  // blocks that end before this wave's first key take nothing from it: their
+  // checkpoints are the incoming demand, which is zero for these keys
+  if (h == 0 && key_ok)
+    for (int64_t b = 0; b < b_w; ++b) ccol[b * P.Tk] = 0.f;
+  if (b_wg < nb) {
+    fetch(b_wg);
+    stash(0);
+  }
+  __syncthreads();
+  int it = 0;
+  for (int64_t b = b_wg; b < nb; ++b, ++it) {
+    const int buf = it & 1;
+    fetch(min(b + 1, nb - 1));                  // the last step reloads its own block, unused
+    // wave-uniform condition: every lane must feed the MFMAs of the step
+    if (b >= b_w && key0 < P.Tk) {
+      if (h == 0 && key_ok) ccol[b * P.Tk] = static_cast<float>(run);   // demand entering block b
+      const int64_t first_row = P.q0 + b * kTileQ;
+      if (key0 + kTileK - 1 <= first_row) step(b, buf, std::false_type{});
+      else step(b, buf, std::true_type{});
+    }
+    if (b + 1 < nb) stash(buf ^ 1);
+    sync_lds();
+  }
+  if (key_ok && h == 0) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
+}
+
+// ---------------------------------------------------------------------------
+// output pass
+
+template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
+__global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
+  using T = Tiles<CT, D>;
+  constexpr int kRP = BID == BID_SOFTMAX ? 1 : 2;                  // per-row parameters
+  // a stage holds two consecutive key tiles; two stages double-buffer them
+  __shared__ __attribute__((aligned(16))) CT ktile[2][2][kTileK * T::kKStride];
+  __shared__ __attribute__((aligned(16))) CT vttile[2][2][D * T::kTStride];
+  __shared__ __attribute__((aligned(16))) float lse_s[4][kRP][kTileQ];
+  __shared__ float ssum_s[4][kTileQ];
+  __shared__ float cs_s[2][4][2 * kTileK];             // demand checkpoints per stage and wave
+
+  const WorkItem item = xcd_work_item(P.groups, P.n, true);
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int g = item.idx;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const float hf = static_cast<float>(h);
+  const WaveRows W = wave_rows(P, g, wave);
+  const int nkt_wg = group_key_tiles(P, g);
+  const int nst = (nkt_wg + 1) / 2;                    // stages of two key tiles
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
+  const CT* ks = static_cast<const CT*>(P.k) + slice * P.k_sn;
+  const CT* vts = static_cast<const CT*>(P.vt) + slice * P.t_sn;
+
+  // Q rows in QS order: accumulator register i of half h <-> row 16 h + i
+  RowFrag<CT, D> qf;
+  const int64_t my_row = W.r0 + qsig(l32);
+  if (my_row < P.C) load_row_frag<CT, D>(qf, qs + my_row * D + h * (D / 2));
+  else zero_row_frag<CT, D>(qf);
+
+  // log2-sum-exp of this wave's rows (the per-row bid parameters of the
+  // variants), read from LDS at every step (keeps registers for occupancy)
+  if (h == 0) {
+    const int64_t r = W.r0 + l32;
+    const int64_t rc = min(r, P.C - 1);
+    if constexpr (BID == BID_SOFTMAX) {
+      lse_s[wave][0][l32] = (r < P.C) ? P.rmax[slice * P.C + r] + __log2f(P.rden[slice * P.C + r]) : INFINITY;
+    } else {
+      float r0, r1;
+      bid_row_params<BID>(P.rmax[slice * P.C + rc], P.rden[slice * P.C + rc],
+                          static_cast<float>(P.q0 + r + 1), r < P.C, r0, r1);
+      lse_s[wave][0][l32] = r0;
+      lse_s[wave][kRP - 1][l32] = r1;
+    }
+  }
+  constexpr int kSteps = kTileK / Mma<CT>::kStep;
+  typename Mma<CT>::frag ident[kSteps];
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) ident[s] = ident_qs<CT>(l32, h, s);
+  floatx16 o[kDTiles<D>];
+#pragma unroll
+  for (int t = 0; t < kDTiles<D>; ++t) o[t] = floatx16{};
+  // row sums of the shares ride on the share @ V products as a ones column:
+  // column 0 of this tile (lanes 0 and 32) accumulates them
+  floatx16 orow = floatx16{};
+  const auto ones = ones_col_frag<CT>(l32);
+
+  // The demand checkpoints of a stage (each wave's rows, the stage's 64 keys)
+  // are staged through LDS with the tiles: thread t loads the one of wave
+  // t >> 6, key 32 * ((t >> 5) & 1) + (t & 31) of the stage.
+  const int cw = threadIdx.x >> 6, cj = threadIdx.x & 63;
+  const int64_t c_rb = min(static_cast<int64_t>(g) * 4 + cw, P.nb - 1);
+  const float* c_row = P.carry + (slice * P.nb + c_rb) * P.Tk;
+  float cr = 0.f;
+  bool cr_ok = false;
+
+  // N consecutive key tiles kt0 .. kt0 + N - 1 of stage buffer `buf`, their
+  // phases interleaved so that one tile's MFMAs overlap the other's VALU work
+  auto out_tiles = [&](auto n_tag, auto diag_tag, int kt0, int slot0, int buf) {
+    constexpr int N = decltype(n_tag)::value;
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    float cin[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) cin[n] = cs_s[buf][wave][(slot0 + n) * kTileK + rho(l32)];
+    floatx16 acc[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      RowFrag<CT, D> kf;
+      lds_row_frag<CT, D>(kf, ktile[buf][slot0 + n], rho(l32), h);
+      acc[n] = mma_rows<CT, D>(qf, kf, floatx16{});
+    }
+    float lse[16], rb1[16];
+    {
+      const floatx4* lp = reinterpret_cast<const floatx4*>(&lse_s[wave][0][16 * h]);
+      const floatx4* lq = reinterpret_cast<const floatx4*>(&lse_s[wave][kRP - 1][16 * h]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const floatx4 v = lp[u];
+        lse[4 * u] = v[0]; lse[4 * u + 1] = v[1]; lse[4 * u + 2] = v[2]; lse[4 * u + 3] = v[3];
+        if constexpr (BID != BID_SOFTMAX) {
+          const floatx4 w = lq[u];
+          rb1[4 * u] = w[0]; rb1[4 * u + 1] = w[1]; rb1[4 * u + 2] = w[2]; rb1[4 * u + 3] = w[3];
+        }
+      }
+    }
+    float p[N][16], x[N][16];
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if constexpr (BID == BID_SOFTMAX) p[n][i] = fast_exp2(fmaf(acc[n][i], P.c, -lse[i]));
+        else p[n][i] = bid_p<BID>(acc[n][i], P.c, P.scale, lse[i], rb1[i], P.lshift);
+      }
+    if constexpr (DIAG) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const int dk = (kt0 + n) * kTileK + rho(l32) - static_cast<int>(W.qa0) - 16 * h;   // key - query(i) = dk - i
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (dk > i) p[n][i] = 0.f;
+      }
+    }
+    if constexpr (SHARE != SHARE_NONE) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[n][i] = p[n][i];
+        if constexpr (SHARE == SHARE_EXCL) scan_excl_qs(x[n], cin[n] + kEps, hf);   // demand + eps
+        else scan_incl_qs(x[n], cin[n] + kEps, hf);                                // demand + p + eps
+      }
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) p[n][i] *= fast_rcp(x[n][i]);                 // share
+    }
+    // transpose each share tile: queries in lanes, keys (natural order) in registers
+    floatx16 xt[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      xt[n] = floatx16{};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) xt[n] = Mma<CT>::mma(acc_frag<CT>(p[n], s), ident[s], xt[n]);
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      float xv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xv[i] = xt[n][i];
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const auto af = acc_frag<CT>(xv, s);
+#pragma unroll
+        for (int t = 0; t < kDTiles<D>; ++t)
+          o[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(vttile[buf][slot0 + n], 32 * t + l32, h, s), o[t]);
+        orow = Mma<CT>::mma(af, ones, orow);
+      }
+    }
+  };
+
+  KTileLoader<CT, D> kl[2];
+  TTileLoader<CT, D> vl[2];
+  auto fetch = [&](int st) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int64_t key0 = static_cast<int64_t>(2 * st + n) * kTileK;
+      kl[n].load(ks, key0, P.Tk);
+      vl[n].load(vts, key0);
+    }
+    const int64_t key = static_cast<int64_t>(st) * 2 * kTileK + cj;
+    cr_ok = key < P.Tk;
+    cr = c_row[min(key, P.Tk - 1)];
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      kl[n].store(ktile[buf][n]);
+      vl[n].store(vttile[buf][n]);
+    }
+    cs_s[buf][cw][cj] = cr_ok ? cr : 0.f;
+  };
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    const int kt0 = 2 * st;
+    fetch(min(st + 1, nst - 1));                       // the last stage reloads itself, unused
+    if (kt0 + 1 < W.kfull) {
+      out_tiles(std::integral_constant<int, 2>{}, std::false_type{}, kt0, 0, buf);
+    } else {
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        if (kt0 + n < W.kfull)
+          out_tiles(std::integral_constant<int, 1>{}, std::false_type{}, kt0 + n, n, buf);
+        else if (kt0 + n < W.kend)
+          out_tiles(std::integral_constant<int, 1>{}, std::true_type{}, kt0 + n, n, buf);
+      }
+    }
+    if (st + 1 < nst) stash(buf ^ 1);
+    sync_lds();
+  }
+
+  // row sums: column 0 of orow, register i of half h <-> row acc_row(i, h)
+  if (l32 == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ssum_s[wave][acc_row(i, h)] = orow[i];
+  }
+  __syncthreads();
+  if (h == 0 && W.r0 + l32 < P.C) P.ssum[slice * P.C + W.r0 + l32] = ssum_s[wave][l32];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = acc_row(i, h);
+    if (W.r0 + row < P.C) {
+      const float inv = 1.f / (ssum_s[wave][row] + kEps);
+      float* dst = P.out + slice * P.o_sn + (W.r0 + row) * D;
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        if (32 * t + l32 < D) dst[32 * t + l32] = o[t][i] * inv;
+    }
+  }
+}
+// ---------------------------------------------------------------------------
+// host side
+
+struct FwdWorkspace {
+  size_t vt, kt, qc, kc, total;
+};
+
+FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int lowp, int want_pk) {
+  const size_t ct = lowp ? 2 : 4;
+  const bool convert = lowp ? dtype != DT_BF16 : dtype != DT_F32;
+  FwdWorkspace w{};
+  const size_t tsz = align_up(ct * n * D * pad64(Tk));
+  w.vt = 0;
+  w.kt = w.vt + tsz;
+  w.qc = w.kt + (want_pk ? tsz : 0);
+  w.kc = w.qc + (convert ? align_up(ct * n * C * D) : 0);
+  w.total = w.kc + (convert ? align_up(ct * n * Tk * D) : 0);
+  return w;
+}
+
+template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
+int launch_forward(const ForwardArgs& a) {
+  const FwdWorkspace w = fwd_layout(a.n, a.C, a.Tk, D, a.dtype, a.lowp, a.pk != nullptr);
+  char* ws = static_cast<char*>(a.workspace);
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+  const bool convert = sizeof(CT) == 2 ? a.dtype != DT_BF16 : a.dtype != DT_F32;
+  const int64_t tk_pad = pad64(a.Tk);
+  const unsigned n = static_cast<unsigned>(a.n);
+
+  CT* vt = reinterpret_cast<CT*>(ws + w.vt);
+  CT* kt = a.pk ? reinterpret_cast<CT*>(ws + w.kt) : nullptr;
+  CT* qc = convert ? reinterpret_cast<CT*>(ws + w.qc) : nullptr;
+  CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
+
+  // operands in the compute type; V^T (and K^T) tiles
+  const dim3 gk(static_cast<unsigned>(tk_pad / 64), n);
+  DIL_TIMED("prep", st,
+            prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr, 0, vt,
+                                                        D * tk_pad, tk_pad, nullptr));
+  if (convert || kt != nullptr)
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc, a.Tk * D,
+                                                          kt, D * tk_pad, tk_pad, nullptr));
+  if (convert) {
+    const dim3 gq(static_cast<unsigned>(pad64(a.C) / 64), n);
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<gq, kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc, a.C * D,
+                                                          nullptr, 0, 0, nullptr));
+  }
+
+  FwdParams P{};
+  P.q = convert ? static_cast<const void*>(qc) : a.q;
+  P.q_sn = convert ? a.C * D : a.q_sn;
+  P.k = convert ? static_cast<const void*>(kc) : a.k;
+  P.k_sn = convert ? a.Tk * D : a.kv_sn;
+  P.vt = vt;
+  P.kt = kt;
+  P.t_sn = D * tk_pad;
+  P.tk_pad = tk_pad;
+  P.C = a.C;
+  P.Tk = a.Tk;
+  P.q0 = a.q0;
+  P.nb = (a.C + kTileQ - 1) / kTileQ;
+  P.scale = 1.f / sqrtf(static_cast<float>(D));
+  P.c = kLog2e * P.scale;
+  P.out = a.out;
+  P.o_sn = a.o_sn;
+  P.rmax = a.rmax;
+  P.rden = a.rden;
+  P.ssum = a.ssum;
+  P.carry = a.carry;
+  P.demand_in = a.demand_in;
+  P.din_sn = a.din_sn;
+  P.total = a.total;
+  P.tot_sn = a.tot_sn;
+  P.pk = a.pk;
+  P.shift = a.var.shift;
+  P.lshift = log2f(a.var.shift);
+
+  P.n = a.n;
+  P.groups = static_cast<int>((a.C + 4 * kTileQ - 1) / (4 * kTileQ));
+  const dim3 grid(static_cast<unsigned>(xcd_grid(P.groups * a.n)));
+  if (a.pk) DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, true, BID><<<grid, kThreads, 0, st>>>(P)));
+  else DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, false, BID><<<grid, kThreads, 0, st>>>(P)));
+  P.kgroups = static_cast<int>((a.Tk + 4 * kTileK - 1) / (4 * kTileK));
+  DIL_TIMED("fwd_demand", st,
+            (fwd_demand<CT, D, BID><<<dim3(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n))),
+                                      kThreads, 0, st>>>(P)));
+  DIL_TIMED("fwd_out", st, (fwd_out<CT, D, BID, SHARE><<<grid, kThreads, 0, st>>>(P)));
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+}  // namespace dil

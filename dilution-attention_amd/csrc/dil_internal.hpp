@@ -13,6 +13,19 @@ constexpr int kErrDtype = -2;
 constexpr int kErrWorkspace = -3;
 constexpr int kErrShape = -4;
 constexpr int kErrPrecision = -5;
+constexpr int kErrVariant = -6;
+
+// Operator variant (the reference's kernels_bid ablations): bid function
+// 0..7, share mode 0 (none) / 1 (dilution) / 2 (exclusive), and the SHIFT of
+// the expshift / sigshift bids.  The production operator is {0, 1, 1}; the
+// other variants are built for head_dim 64.
+struct Variant {
+  int bid = 0;
+  int share = 1;
+  float shift = 1.f;
+};
+constexpr int kVariantHeadDim = 64;
+int check_variant(const Variant& v, int head_dim);
 
 inline size_t align_up(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
 
@@ -54,6 +67,7 @@ struct DecodeArgs {
   int64_t workspace_bytes;
   int64_t n, length;
   int head_dim, dtype;
+  Variant var;
   void* stream;
 };
 
@@ -80,7 +94,8 @@ struct ForwardArgs {
   int64_t din_sn;
   float* total;          // (n, Tk) fp32 demand after the last row (may alias demand_in)
   int64_t tot_sn;
-  float* pk;             // (n, C, D) fp32 scale * p @ k, or null
+  float* pk;             // (n, C, D) fp32 scale * jac @ k (jac = p for softmax bids), or null
+  Variant var;
   void* workspace;
   int64_t workspace_bytes;
   void* stream;
@@ -101,6 +116,7 @@ struct BackwardArgs {
   const float* ssum;
   const float* carry;    // (n, ceil(T/32), T)
   const float* pk;       // (n, T, D)
+  Variant var;
   void* dq;              // (n, T, D) each in grad_dtype
   void* dk;
   void* dv;
@@ -113,5 +129,11 @@ struct BackwardArgs {
 
 int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int lowp);
 int backward(const BackwardArgs& a);
+
+// The ablation variants of one bid function (any share mode), head_dim 64;
+// each is built in its own object from dil_variants.hip.
+template <int BID> int forward_bid(const ForwardArgs& a);
+template <int BID> int backward_bid(const BackwardArgs& a);
+template <int BID> int decode_bid(const DecodeArgs& a);
 
 }  // namespace dil

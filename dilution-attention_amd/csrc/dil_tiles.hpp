@@ -347,6 +347,24 @@ __device__ __forceinline__ float scan_incl_qs(float (&x)[16], float base, float 
   return tot.lo + tot.hi;
 }
 
+// Exclusive column scan of a QS-layout tile: x[i] becomes base + the sum of
+// the column's entries at rows < 16 h + i (no subtraction, so an entry with no
+// earlier mass is exactly `base`).  Returns the column total.
+__device__ __forceinline__ float scan_excl_qs(float (&x)[16], float base, float hf) {
+  float run = 0.f;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const float cur = x[t];
+    x[t] = run;
+    run += cur;
+  }
+  const HalfPair tot = halves(run);
+  const float off = fmaf(hf, tot.lo, base);
+#pragma unroll
+  for (int t = 0; t < 16; ++t) x[t] += off;
+  return tot.lo + tot.hi;
+}
+
 // Inclusive suffix scan of a QS-layout tile: x[i] becomes base + the sum of
 // the column's entries at rows >= 16 h + i.  Returns the column total.
 __device__ __forceinline__ float scan_suffix_qs(float (&x)[16], float base, float hf) {

@@ -33,6 +33,16 @@ SIGNATURES = {
     "dil_backward": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64,
                               _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int64,
                               _vp]),
+    "dil_forward_variant": (_c_int, [_vp, _vp, _vp, _c_int64, _c_int64, _c_int, _c_int, _c_int,
+                                     _c_int, _c_int, ctypes.c_float,
+                                     _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _vp]),
+    "dil_backward_variant": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int64,
+                                      _c_int64, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _c_int, _c_int, ctypes.c_float,
+                                      _vp, _vp, _vp, _vp, _c_int64, _vp]),
+    "dil_decode_step_variant": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64,
+                                         _c_int, _c_int, _c_int, _c_int, ctypes.c_float,
+                                         _vp, _c_int64, _vp]),
     "dil_decode_workspace_bytes": (_c_int64, [_c_int64, _c_int64, _c_int]),
     "dil_decode_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _c_int,
                                  _c_int, _vp, _c_int64, _vp]),

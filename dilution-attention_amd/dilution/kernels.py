@@ -42,6 +42,10 @@ KEY_FORWARD_MIN_SEQ = 256
 CHECKPOINT_ROWS = 32
 
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+# operator variant (bid code, share code, shift); the production operator is
+# softmax bids with the dilution share (the ablation variants are reached
+# through dilution.kernels_bid)
+_PRODUCTION = (0, 1, 1.0)
 _PRECISIONS = {"ieee": 0, "tf32": 1, "bf16": 2}
 _HEAD_DIMS = (16, 32, 64, 128)
 
@@ -130,6 +134,7 @@ def dilution_attention_forward(
     num_stages: int = 2,
     _save_pk: bool = False,
     scratch_budget_gib: float = 16.0,
+    _variant: tuple = _PRODUCTION,
 ):
     """Fused forward; returns fp32 outputs (kernels.py:328-455).
 
@@ -170,11 +175,15 @@ def dilution_attention_forward(
     ws = _workspace(ws_bytes, dev)
     for a in range(0, n, rows):
         b = min(a + rows, n)
-        status = lib.dil_forward(
-            qf[a:b].data_ptr(), kf[a:b].data_ptr(), vf[a:b].data_ptr(), b - a, seq, head_dim,
-            _DTYPES[dt], prec, out[a:b].data_ptr(), rmax[a:b].data_ptr(), rden[a:b].data_ptr(),
-            ssum[a:b].data_ptr(), carry.data_ptr(), total[a:b].data_ptr(),
-            None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+        head = (qf[a:b].data_ptr(), kf[a:b].data_ptr(), vf[a:b].data_ptr(), b - a, seq, head_dim,
+                _DTYPES[dt], prec)
+        tail = (out[a:b].data_ptr(), rmax[a:b].data_ptr(), rden[a:b].data_ptr(),
+                ssum[a:b].data_ptr(), carry.data_ptr(), total[a:b].data_ptr(),
+                None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+        if tuple(_variant) == _PRODUCTION:
+            status = lib.dil_forward(*head, *tail)
+        else:
+            status = lib.dil_forward_variant(*head, *_variant, *tail)
         _hip.check(status, "dil_forward")
 
     result = out.reshape(batch, heads, seq, head_dim)
@@ -211,33 +220,42 @@ class _DilutionAttentionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out, rmax, rden, carry, ssum, pk = ctx.saved_tensors
-        lib = _hip.lib()
-        batch, heads, seq, head_dim = q.shape
-        n = batch * heads
-        prec = _precision_code(ctx.dot_precision)
-        dt = _common_dtype(q, k, v)
-        qf, kf, vf = (_rows(x, n, seq, head_dim, dt) for x in (q, k, v))
-        ddt = dout.dtype if dout.dtype in _DTYPES else torch.float32
-        dof = _rows(dout, n, seq, head_dim, ddt)
-        of = out.reshape(n, seq, head_dim)
-        dev = q.device
-        grads = []
-        gdt = dt
-        dq = torch.empty(n, seq, head_dim, device=dev, dtype=gdt)
-        dk = torch.empty_like(dq)
-        dv = torch.empty_like(dq)
-        ws = _workspace(lib.dil_backward_workspace_bytes(n, seq, head_dim, _DTYPES[dt], prec), dev)
-        status = lib.dil_backward(
-            qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), dof.data_ptr(), of.data_ptr(),
-            rmax.data_ptr(), rden.data_ptr(), ssum.data_ptr(), carry.data_ptr(), pk.data_ptr(),
-            n, seq, head_dim, _DTYPES[dt], _DTYPES[ddt], _DTYPES[gdt], prec,
-            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
-        _hip.check(status, "dil_backward")
-        shape4 = (batch, heads, seq, head_dim)
-        for g, ref in zip((dq, dk, dv), (q, k, v)):
-            grads.append(g.reshape(shape4).to(ref.dtype))
+        grads = _backward(ctx.saved_tensors, dout, ctx.dot_precision, _PRODUCTION)
         return (*grads, None, None, None, None, None, None, None, None, None)
+
+
+def _backward(saved, dout, dot_precision: str, variant: tuple):
+    """dq, dk, dv of the operator (variant) from the forward's saved tensors."""
+    q, k, v, out, rmax, rden, carry, ssum, pk = saved
+    lib = _hip.lib()
+    batch, heads, seq, head_dim = q.shape
+    n = batch * heads
+    prec = _precision_code(dot_precision)
+    dt = _common_dtype(q, k, v)
+    qf, kf, vf = (_rows(x, n, seq, head_dim, dt) for x in (q, k, v))
+    ddt = dout.dtype if dout.dtype in _DTYPES else torch.float32
+    dof = _rows(dout, n, seq, head_dim, ddt)
+    of = out.reshape(n, seq, head_dim)
+    dev = q.device
+    grads = []
+    gdt = dt
+    dq = torch.empty(n, seq, head_dim, device=dev, dtype=gdt)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    ws = _workspace(lib.dil_backward_workspace_bytes(n, seq, head_dim, _DTYPES[dt], prec), dev)
+    head = (qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), dof.data_ptr(), of.data_ptr(),
+            rmax.data_ptr(), rden.data_ptr(), ssum.data_ptr(), carry.data_ptr(), pk.data_ptr(),
+            n, seq, head_dim, _DTYPES[dt], _DTYPES[ddt], _DTYPES[gdt], prec)
+    tail = (dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+    if tuple(variant) == _PRODUCTION:
+        status = lib.dil_backward(*head, *tail)
+    else:
+        status = lib.dil_backward_variant(*head, *variant, *tail)
+    _hip.check(status, "dil_backward")
+    shape4 = (batch, heads, seq, head_dim)
+    for g, ref in zip((dq, dk, dv), (q, k, v)):
+        grads.append(g.reshape(shape4).to(ref.dtype))
+    return tuple(grads)
 
 
 def dilution_attention(
@@ -342,6 +360,7 @@ def dilution_decode_step(
     length: int,
     block_n: int = 512,
     num_warps: int = 8,
+    _variant: tuple = _PRODUCTION,
 ) -> torch.Tensor:
     """Fused decode step; returns the new row's output (B, H, 1, D) in q1.dtype
     (kernels.py:994-1038).
@@ -376,9 +395,13 @@ def dilution_decode_step(
     qf = q1.reshape(n, head_dim).to(dt).contiguous()
     out = torch.empty(n, head_dim, device=q1.device, dtype=dt)
     ws = _workspace(lib.dil_decode_workspace_bytes(n, length, head_dim), q1.device)
-    status = lib.dil_decode_step(qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), cf.data_ptr(),
-                                 out.data_ptr(), n, capacity, length, head_dim, _DTYPES[dt],
-                                 ws.data_ptr(), ws.numel(), _stream())
+    head = (qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), cf.data_ptr(), out.data_ptr(), n,
+            capacity, length, head_dim, _DTYPES[dt])
+    tail = (ws.data_ptr(), ws.numel(), _stream())
+    if tuple(_variant) == _PRODUCTION:
+        status = lib.dil_decode_step(*head, *tail)
+    else:
+        status = lib.dil_decode_step_variant(*head, *_variant, *tail)
     _hip.check(status, "dil_decode_step")
     if out.dtype != q1.dtype:
         out = out.to(q1.dtype)

@@ -124,6 +124,42 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
                     int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Operator variants: the bid and share ablations.  Replace the entry points of
+ * src/dilution/kernels_bid.py -- dilution_attention_forward (:424-489, its
+ * _dilution_k1 :280-360 and _dilution_k2 :362-411), _DilutionAttentionFn.
+ * backward (:756-815, _dilution_b1-_b4 :513-729) and dilution_decode_step
+ * (:962-1010, _dilution_decode :853-960).
+ *
+ * Arguments as for dil_forward / dil_backward / dil_decode_step, plus
+ *   bid:    0 softmax, 1 relu, 2 relu2, 3 softplus, 4 minshift, 5 sigmoid,
+ *           6 expshift, 7 sigshift (kernels_bid.py:4-42);
+ *   share:  1 dilution p/(committed+p+eps), 2 exclusive p/(committed+eps),
+ *           0 none (kernels_bid.py:123-127);
+ *   shift:  SHIFT of expshift / sigshift (> 0).
+ * (bid, share) = (0, 1) is the production operator (any head_dim); the other
+ * variants are built for head_dim 64.  rmax / rden follow kernels_bid: the
+ * row minimum (minshift) or 0 and the row sum of the bid numerators for the
+ * ratio bids (1-4); 0 and 1 (SHIFT for expshift) for the elementwise bids;
+ * pk holds scale * jac @ k, jac = dp/da (p for the softmax bids).  The
+ * workspace sizes are those of the matching base entry point.
+ */
+int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
+                        int head_dim, int dtype, int precision, int bid, int share, float shift,
+                        float* out, float* rmax, float* rden, float* ssum, float* carry,
+                        float* committed_total, float* pk, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+int dil_backward_variant(const void* q, const void* k, const void* v, const void* dout,
+                         const float* out, const float* rmax, const float* rden,
+                         const float* ssum, const float* carry, const float* pk, int64_t n,
+                         int64_t seq, int head_dim, int dtype, int dout_dtype, int grad_dtype,
+                         int precision, int bid, int share, float shift, void* dq, void* dk,
+                         void* dv, void* workspace, int64_t workspace_bytes, void* stream);
+int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_cache,
+                            float* committed, void* out, int64_t n, int64_t capacity,
+                            int64_t length, int head_dim, int dtype, int bid, int share,
+                            float shift, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Kernel timing for measurement harnesses.  No reference counterpart (the
  * reference times its Triton launches with torch.profiler and CUDA events in
  * scripts/step_profile.py:29-47 and scripts/profile_kernels.py:115-144).

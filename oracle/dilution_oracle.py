@@ -18,6 +18,8 @@ code written for this repository:
   prefill demand hand-off       /root/reference/src/dilution/model.py:198-229
   backward decomposition        /root/reference/docs/kernels.md:62-84,
                                 /root/reference/src/dilution/kernels.py:678-775
+  bid / share variants          /root/reference/src/dilution/kernels_bid.py:4-42,
+                                :94-165 (bids, share modes), :853-960 (decode)
 
 Pinning (each function is checked by something other than a retyping of its
 own formula; see tests/test_oracle.py):
@@ -36,6 +38,13 @@ own formula; see tests/test_oracle.py):
                           after token, and the demand == column sums.
   prefill_chunk           the full-sequence rows and demand == column sums.
   pk                      (p @ k) / sqrt(d) via fp64 matmul of torch.softmax.
+  variant_attention_f64   variant_attention_loops (scalar fp64 loops over
+                          rows and keys, written independently), the q = 0
+                          closed forms (uniform bids -> harmonic numbers;
+                          sigmoid bids 1/2 -> 1/(i-j+1) weights; no share ->
+                          window mean), the exclusive share's identity
+                          collapse and softmax first row, and gradcheck.
+  variant_demand_totals   the loops' running demand.
 
 No function here is "parity unpinned".
 """
@@ -299,6 +308,116 @@ def grads_closed_form_f64(q, k, v, dout):
     inter = dict(p=p, committed=c, ssum=ssum[..., 0], dbar=dbar[..., 0], ghat=ghat[..., 0],
                  suffix=suffix, out=o)
     return (dq, dk, dv), inter
+
+
+# ---------------------------------------------------------------------------
+# bid / share variants (kernels_bid.py)
+
+BIDS = ("softmax", "relu", "relu2", "softplus", "minshift", "sigmoid", "expshift", "sigshift")
+SHARES = (True, False, "exclusive")
+
+
+def _variant_bids_f64(aff: torch.Tensor, bid: str, shift: float) -> torch.Tensor:
+    """Bids (.., T, T) from fp64 affinities on the causal window
+    (kernels_bid.py:94-121): row-normalised numerators for the ratio bids,
+    with a uniform row where the numerators carry no mass."""
+    t = aff.shape[-1]
+    causal = torch.ones(t, t, dtype=torch.bool).tril()
+    if bid == "softmax":
+        return torch.softmax(aff.masked_fill(~causal, -math.inf), dim=-1)
+    if bid == "sigmoid":
+        return torch.sigmoid(aff) * causal
+    if bid == "expshift":
+        return torch.exp(aff) / shift * causal
+    if bid == "sigshift":
+        return torch.sigmoid(aff - math.log(shift)) * causal
+    if bid == "relu":
+        num = aff.clamp_min(0.0)
+    elif bid == "relu2":
+        num = aff.clamp_min(0.0) ** 2
+    elif bid == "softplus":
+        num = torch.nn.functional.softplus(aff)
+    elif bid == "minshift":
+        lo = aff.masked_fill(~causal, math.inf).amin(dim=-1, keepdim=True).detach()
+        num = aff - lo
+    else:
+        raise ValueError(bid)
+    num = num * causal
+    mass = num.sum(dim=-1, keepdim=True)
+    window = torch.arange(1, t + 1, dtype=aff.dtype)[:, None]
+    return torch.where(mass > 0, num / mass.clamp_min(1e-300), causal / window)
+
+
+def variant_attention_f64(q, k, v, bid: str = "softmax", share=True, shift: float = 1.0) -> torch.Tensor:
+    """fp64 restatement of kernels_bid.dilution_attention_reference
+    (kernels_bid.py:130-165): any bid, share True / "exclusive" / False.
+    Differentiable (torch autograd) for the gradient checks."""
+    t, d = q.shape[-2], q.shape[-1]
+    q, k, v = (torch.as_tensor(x).double() for x in (q, k, v))
+    aff = torch.matmul(q, k.transpose(-2, -1)) / math.sqrt(d)
+    p = _variant_bids_f64(aff, bid, shift)
+    if share is False:
+        a = p / p.sum(dim=-1, keepdim=True)
+    else:
+        before = torch.cumsum(p, dim=-2) - p
+        denom = before + EPS if share == "exclusive" else before + p + EPS
+        sh = p / denom
+        a = sh / (sh.sum(dim=-1, keepdim=True) + EPS)
+    return torch.matmul(a, v)
+
+
+def variant_demand_totals(q, k, bid: str = "softmax", shift: float = 1.0) -> torch.Tensor:
+    """Column totals of the variant's bids (the decode demand), fp64."""
+    d = q.shape[-1]
+    q, k = (torch.as_tensor(x).double() for x in (q, k))
+    aff = torch.matmul(q, k.transpose(-2, -1)) / math.sqrt(d)
+    return _variant_bids_f64(aff, bid, shift).sum(dim=-2)
+
+
+def variant_attention_loops(q, k, v, bid: str = "softmax", share=True, shift: float = 1.0):
+    """Scalar fp64 loops over (row, key) for one (batch, head) slice: (T, D)
+    arrays q, k, v.  Returns (out (T, D), demand totals (T,)).  Bids from
+    math.exp / comparisons, demand accumulated row by row; tiny T only."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    t, d = q.shape
+    out = np.zeros((t, d))
+    demand = np.zeros(t)
+    for i in range(t):
+        a = [float(np.dot(q[i], k[j])) / math.sqrt(d) for j in range(i + 1)]
+        if bid == "softmax":
+            top = max(a)
+            e = [math.exp(x - top) for x in a]
+            p = [x / sum(e) for x in e]
+        elif bid in ("sigmoid", "sigshift"):
+            off = math.log(shift) if bid == "sigshift" else 0.0
+            p = [1.0 / (1.0 + math.exp(-(x - off))) for x in a]
+        elif bid == "expshift":
+            p = [math.exp(x) / shift for x in a]
+        else:
+            if bid == "relu":
+                num = [x if x > 0 else 0.0 for x in a]
+            elif bid == "relu2":
+                num = [x * x if x > 0 else 0.0 for x in a]
+            elif bid == "softplus":
+                num = [math.log1p(math.exp(x)) if x < 30 else x for x in a]
+            else:
+                lo = min(a)
+                num = [x - lo for x in a]
+            mass = sum(num)
+            p = [x / mass for x in num] if mass > 0 else [1.0 / (i + 1)] * (i + 1)
+        if share is False:
+            w = p
+        elif share == "exclusive":
+            w = [p[j] / (demand[j] + EPS) for j in range(i + 1)]
+        else:
+            w = [p[j] / (demand[j] + p[j] + EPS) for j in range(i + 1)]
+        tot = sum(w) + (0.0 if share is False else EPS)
+        for j in range(i + 1):
+            out[i] += (w[j] / tot) * v[j]
+            demand[j] += p[j]
+    return out, demand
 
 
 # ---------------------------------------------------------------------------

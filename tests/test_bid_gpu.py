@@ -1,0 +1,155 @@
+"""Bid and share variants (dilution.kernels_bid) on the HIP kernels against
+the fp64 oracle.
+
+Reference patterns: tests/test_kernels.py:276-450 (forward and backward of
+every bid with and without the share step, the softmax path equal to the
+production operator, decode rows of every bid, the no-cumsum softmax equal to
+plain attention, the exclusive share's identity collapse and first row).
+Tolerances: fp32 forward 1e-4 max-abs and demand totals 1e-5 (the production
+bounds; relu2 1e-3, the reference's bound for every bid forward: a diagonal key
+with a tiny positive affinity bids relu(a)^2 ~ eps and, with no demand yet,
+takes a share p / (p + eps) that the fp32 score moves by ~1e-3); gradients within the reference's relative bound (2e-3 of the
+largest gradient, 5e-3 for relu2, kernels_bid's own test bounds); bf16
+forward 2e-2 max-abs against the oracle on the bf16-rounded inputs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import max_abs, needs_gpu
+from oracle import dilution_oracle as orc
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+SHIFT = 3.0
+
+
+def _inputs(seq, seed, shape=(2, 4)):
+    return orc.make_inputs((*shape, seq, 64), seed=seed)
+
+
+@pytest.mark.parametrize("bid", orc.BIDS)
+@pytest.mark.parametrize("share", orc.SHARES, ids=str)
+@pytest.mark.parametrize("seq", [64, 257])
+def test_variant_forward_matches_oracle(bid, share, seq):
+    from dilution import kernels_bid as kb
+
+    q, k, v = _inputs(seq, seed=seq)
+    got, aux = kb.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), bid=bid,
+                                             share_cumsum=share, shift=SHIFT, return_aux=True)
+    assert torch.isfinite(got).all()
+    bound = 1e-3 if bid == "relu2" else 1e-4
+    assert max_abs(got, orc.variant_attention_f64(q, k, v, bid, share, SHIFT)) < bound
+    totals = orc.variant_demand_totals(q, k, bid, SHIFT)
+    assert max_abs(aux["committed_total"], totals) < 1e-5 * max(1.0, totals.abs().max().item())
+
+
+@pytest.mark.parametrize("bid", orc.BIDS)
+@pytest.mark.parametrize("share", [True, False], ids=str)
+@pytest.mark.parametrize("seq", [64, 257])
+def test_variant_backward_matches_autograd(bid, share, seq):
+    from dilution import kernels_bid as kb
+
+    q, k, v, do = orc.make_inputs((2, 4, seq, 64), seed=100 + seq, with_dout=True)
+    ref = [x.double().requires_grad_(True) for x in (q, k, v)]
+    orc.variant_attention_f64(*ref, bid, share, SHIFT).backward(do.double())
+    xs = [x.cuda().requires_grad_(True) for x in (q, k, v)]
+    kb.dilution_attention(*xs, dot_precision="ieee", bid=bid, share_cumsum=share,
+                          shift=SHIFT).backward(do.cuda())
+    bound = 5e-3 if bid == "relu2" else 2e-3
+    for name, r, x in zip(("dq", "dk", "dv"), ref, xs):
+        scale = r.grad.abs().max().item() + 1e-6
+        rel = max_abs(x.grad, r.grad) / scale
+        assert rel < bound, f"{bid} {name} relative error {rel}"
+
+
+@pytest.mark.parametrize("bid", ["softmax", "relu", "sigmoid"])
+def test_variant_exclusive_backward_dv(bid):
+    """The exclusive share's dq/dk are fp32 noise on cancelling 1e9-scale terms
+    (the operator's property, kernels_bid tests note); dv is exact."""
+    from dilution import kernels_bid as kb
+
+    q, k, v, do = orc.make_inputs((1, 2, 96, 64), seed=7, with_dout=True)
+    ref = [x.double().requires_grad_(True) for x in (q, k, v)]
+    orc.variant_attention_f64(*ref, bid, "exclusive").backward(do.double())
+    xs = [x.cuda().requires_grad_(True) for x in (q, k, v)]
+    kb.dilution_attention(*xs, dot_precision="ieee", bid=bid, share_cumsum="exclusive").backward(do.cuda())
+    assert max_abs(xs[2].grad, ref[2].grad) / (ref[2].grad.abs().max().item() + 1e-9) < 2e-3
+
+
+@pytest.mark.parametrize("bid", orc.BIDS)
+def test_variant_forward_bf16(bid):
+    from dilution import kernels_bid as kb
+
+    q, k, v = (x.to(torch.bfloat16) for x in _inputs(200, seed=11))
+    got = kb.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision="bf16", bid=bid,
+                                        shift=SHIFT)
+    assert max_abs(got, orc.variant_attention_f64(q, k, v, bid, True, SHIFT)) < 2e-2
+
+
+def test_softmax_dilution_variant_is_the_production_operator():
+    from dilution import kernels
+    from dilution import kernels_bid as kb
+
+    q, k, v = (x.cuda() for x in _inputs(200, seed=3))
+    a = kernels.dilution_attention_forward(q, k, v)
+    b = kb.dilution_attention_forward(q, k, v, bid="softmax", share_cumsum=True)
+    assert torch.equal(a, b)
+
+
+def test_no_share_softmax_is_plain_causal_attention():
+    from dilution import kernels_bid as kb
+
+    q, k, v = _inputs(200, seed=12)
+    got = kb.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), bid="softmax", share_cumsum=False)
+    s = torch.matmul(q.double(), k.double().transpose(-2, -1)) / 8.0
+    causal = torch.ones(200, 200, dtype=torch.bool).tril()
+    want = torch.matmul(torch.softmax(s.masked_fill(~causal, -float("inf")), -1), v.double())
+    assert max_abs(got, want) < 1e-4
+
+
+def test_exclusive_share_collapses_to_the_identity():
+    from dilution import kernels_bid as kb
+
+    q, k, v = _inputs(257, seed=13, shape=(1, 2))
+    got = kb.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), share_cumsum="exclusive")
+    assert max_abs(got, v) < 1e-3
+    assert max_abs(got[:, :, 0], v[:, :, 0]) < 1e-6
+
+
+@pytest.mark.parametrize("bid", orc.BIDS)
+@pytest.mark.parametrize("share", orc.SHARES, ids=str)
+def test_variant_decode_matches_full_rows(bid, share):
+    """Prefix forward -> committed_total, then one decode step per token: each
+    row equals the full-sequence row, the demand the full column totals."""
+    from dilution import kernels_bid as kb
+
+    b, h, t, prefix = 2, 3, 70, 62
+    q, k, v = orc.make_inputs((b, h, t, 64), seed=17)
+    full = orc.variant_attention_f64(q, k, v, bid, share, SHIFT)
+    qg, kg, vg = (x.cuda() for x in (q, k, v))
+    _, aux = kb.dilution_attention_forward(qg[:, :, :prefix], kg[:, :, :prefix], vg[:, :, :prefix],
+                                           return_aux=True, bid=bid, share_cumsum=share, shift=SHIFT)
+    committed = torch.zeros(b, h, t, device="cuda")
+    committed[:, :, :prefix] = aux["committed_total"]
+    for i in range(prefix, t):
+        y = kb.dilution_decode_step(qg[:, :, i:i + 1].contiguous(), kg, vg, committed, i + 1, bid=bid,
+                                    share_cumsum=share, shift=SHIFT)
+        assert max_abs(y[:, :, 0], full[:, :, i]) < 1e-4, i
+    totals = orc.variant_demand_totals(q, k, bid, SHIFT)
+    assert max_abs(committed, totals) < 1e-5 * max(1.0, totals.abs().max().item())
+
+
+def test_variant_argument_errors():
+    from dilution import kernels_bid as kb
+
+    q = torch.zeros(1, 1, 8, 32, device="cuda")
+    with pytest.raises(ValueError):
+        kb.dilution_attention_forward(q, q, q, bid="relu")          # variants are built for d = 64
+    q64 = torch.zeros(1, 1, 8, 64, device="cuda")
+    with pytest.raises(ValueError):
+        kb.dilution_attention_forward(q64, q64, q64, bid="tanh")
+    with pytest.raises(ValueError):
+        kb.dilution_attention_forward(q64, q64, q64, bid="expshift", shift=0.0)

@@ -191,3 +191,98 @@ def test_planted_mistakes_fail_a_pin(kind):
     cf, _ = orc.harmonic_closed_form(20, v.numpy())
     err_cf = np.abs(fwd(z, k, v).numpy() - cf).max()
     assert max(err_loops, err_cf) > 1e-3, (kind, err_loops, err_cf)
+
+
+# ---------------------------------------------------------------------------
+# bid / share variants (kernels_bid.py)
+
+UNIFORM_AT_ZERO = ("softmax", "relu", "relu2", "softplus", "minshift")   # q = 0 -> p = 1/(i+1)
+
+
+@pytest.mark.parametrize("bid", orc.BIDS)
+@pytest.mark.parametrize("share", orc.SHARES, ids=str)
+def test_variant_restatement_matches_scalar_loops(bid, share):
+    q, k, v = orc.make_inputs((1, 1, 13, 8), seed=5)
+    got = orc.variant_attention_f64(q, k, v, bid, share, 3.0)[0, 0].numpy()
+    want, demand = orc.variant_attention_loops(q[0, 0], k[0, 0], v[0, 0], bid, share, 3.0)
+    assert np.abs(got - want).max() < 1e-12
+    assert np.abs(orc.variant_demand_totals(q, k, bid, 3.0)[0, 0].numpy() - demand).max() < 1e-12
+
+
+@pytest.mark.parametrize("bid", UNIFORM_AT_ZERO)
+def test_variant_uniform_bids_closed_forms(bid):
+    """q = 0: the uniform bid 1/(i+1) (softmax, softplus directly; relu, relu2,
+    minshift through their empty-row rule) gives the harmonic closed form with
+    the dilution share and the window mean with no share step."""
+    t = 24
+    _, k, v = orc.make_inputs((1, 1, t, 8), seed=6)
+    q = torch.zeros_like(k)
+    want, totals = orc.harmonic_closed_form(t, v[0, 0])
+    got = orc.variant_attention_f64(q, k, v, bid, True)[0, 0].numpy()
+    assert np.abs(got - want).max() < 1e-12
+    assert np.abs(orc.variant_demand_totals(q, k, bid)[0, 0].numpy() - totals).max() < 1e-12
+    mean = np.cumsum(v[0, 0].double().numpy(), 0) / np.arange(1, t + 1)[:, None]
+    assert np.abs(orc.variant_attention_f64(q, k, v, bid, False)[0, 0].numpy() - mean).max() < 1e-12
+
+
+@pytest.mark.parametrize("bid,c0", [("sigmoid", 0.5), ("sigshift", 1.0 / 4.0), ("expshift", 1.0 / 3.0)])
+def test_variant_constant_bids_closed_form(bid, c0):
+    """q = 0: the elementwise bids are a constant c0, the demand of key j at
+    row i is c0 (i - j), the dilution share is 1/(i - j + 1) (eps aside), so
+    row i averages v_j with weights 1/(i - j + 1) / H_{i+1}."""
+    t = 20
+    shift = 3.0 if bid != "sigmoid" else 1.0
+    if bid == "sigshift":
+        shift = 3.0                                    # 1 / (1 + 3)
+    _, k, v = orc.make_inputs((1, 1, t, 8), seed=7)
+    q = torch.zeros_like(k)
+    i = np.arange(t)[:, None]
+    j = np.arange(t)[None, :]
+    w = np.where(j <= i, 1.0 / (i - j + 1), 0.0)
+    want = (w / w.sum(-1, keepdims=True)) @ v[0, 0].double().numpy()
+    got = orc.variant_attention_f64(q, k, v, bid, True, shift)[0, 0].numpy()
+    assert np.abs(got - want).max() < 1e-7
+    totals = orc.variant_demand_totals(q, k, bid, shift)[0, 0].numpy()
+    assert np.abs(totals - c0 * (t - np.arange(t))).max() < 1e-12
+
+
+def test_variant_exclusive_share_collapses_to_identity():
+    """share = p / (committed + eps): committed[i, i] is exactly 0, so every
+    row's diagonal wins by 1/eps and the output is v itself; the first row is
+    v_0 in every mode (kernels_bid.py's exclusive-history notes)."""
+    q, k, v = orc.make_inputs((1, 2, 40, 8), seed=8)
+    out = orc.variant_attention_f64(q, k, v, "softmax", "exclusive")
+    assert (out - v.double()).abs().max() < 1e-4          # off-diagonal weight ~ eps / committed
+    for share in orc.SHARES:
+        row0 = orc.variant_attention_f64(q, k, v, "relu", share)[:, :, 0]
+        assert (row0 - v[:, :, 0].double()).abs().max() < 1e-8    # eps in the normalisation
+
+
+# minshift holds its row minimum constant in the backward (kernels_bid.py:13-16),
+# which finite differences do not: its forward is pinned above, its backward
+# shares the autograd path of the others
+@pytest.mark.parametrize("bid,share", [("relu", True), ("softplus", "exclusive"), ("relu", False),
+                                       ("sigshift", True), ("expshift", False), ("relu2", True),
+                                       ("sigmoid", "exclusive")])
+def test_variant_gradcheck(bid, share):
+    q, k, v = (x.double().requires_grad_(True) for x in orc.make_inputs((1, 1, 5, 4), seed=9))
+    assert torch.autograd.gradcheck(
+        lambda a, b, c: orc.variant_attention_f64(a, b, c, bid, share, 2.0), (q, k, v), eps=1e-6,
+        atol=1e-5)
+
+
+def test_planted_variant_mistake_fails_a_pin():
+    """A relu bid without the empty-row rule is NaN at q = 0: the closed form
+    catches it."""
+    t = 8
+    _, k, v = orc.make_inputs((1, 1, t, 4), seed=10)
+    q = torch.zeros_like(k)
+    aff = torch.matmul(q.double(), k.double().transpose(-2, -1))
+    causal = torch.ones(t, t, dtype=torch.bool).tril()
+    num = aff.clamp_min(0.0) * causal
+    p = num / num.sum(-1, keepdim=True)                     # no uniform fallback
+    want, _ = orc.harmonic_closed_form(t, v[0, 0])
+    before = torch.cumsum(p, -2) - p
+    sh = p / (before + p + orc.EPS)
+    got = ((sh / (sh.sum(-1, keepdim=True) + orc.EPS)) @ v.double())[0, 0].numpy()
+    assert not np.abs(got - want).max() < 1e-6
