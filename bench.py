@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                     [--decode-steps K] [--decode-context L] [--no-decode]
-                    [--no-sdpa] [--no-lm] [--no-cpu-baseline]
+                    [--no-sdpa] [--no-lm] [--no-variants] [--no-cpu-baseline]
 
 Prints ONE JSON line.  The headline workload (default ``train16k``,
 BASELINE configs[2]) is the operator's training step, fwd+bwd through
@@ -30,6 +30,10 @@ The same line carries
     operator: training-step, prefill and greedy-decode tokens/s with the
     attention kernels' share of each, and the same LM with softmax (SDPA)
     attention as the comparator;
+  * ``variants``: every bid function x share mode of ``dilution.kernels_bid``
+    (the ablation operators), fwd+bwd at the headline shape and the cached
+    decode step at the decode shape, ms per step and TFLOP/s / GB/s on the
+    same algorithmic counts;
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
     formula) timed on this host's cores on one (batch, head) slice of the
     headline workload.
@@ -107,6 +111,8 @@ def parse_args():
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-lm", action="store_true")
+    ap.add_argument("--no-variants", action="store_true")
+    ap.add_argument("--variant-steps", type=int, default=5)
     ap.add_argument("--lm-train-steps", type=int, default=2)
     ap.add_argument("--lm-decode-tokens", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -279,6 +285,56 @@ def bench_decode(args, dev):
                          "algorithmic_bytes_per_launch": dom_bytes,
                          "avg_launch_ms": round(tot_dom / n_dom, 4)},
             "kernels": per_kernel}
+
+
+def bench_variants(args, dev, inputs):
+    """The bid / share ablation operators (kernels_bid) at the headline
+    training shape (fwd+bwd, bf16 operands) and at the decode shape (B16 H16
+    d64 bf16, context ``--decode-context``); SHIFT = 16384, the context length
+    of the ablation configs."""
+    import torch
+
+    from dilution import kernels_bid as kb
+
+    q, k, v, do = inputs
+    batch, heads, seq, d = q.shape
+    xs = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+    flops = 7.0 * batch * heads * seq * seq * d
+    dbatch, dheads, length = 16, 16, args.decode_context
+    g = torch.Generator(device=dev).manual_seed(6)
+    kc = torch.randn(dbatch, dheads, length, d, device=dev, generator=g, dtype=torch.bfloat16)
+    vc = torch.randn(dbatch, dheads, length, d, device=dev, generator=g, dtype=torch.bfloat16)
+    com = torch.zeros(dbatch, dheads, length, device=dev)
+    q1 = torch.randn(dbatch, dheads, 1, d, device=dev, generator=g, dtype=torch.bfloat16)
+    nbytes = dbatch * dheads * length * (4 * d + 8)
+    out = {}
+    for bid in kb.BID_TYPES:
+        for share in (True, "exclusive", False):
+            kw = {"bid": bid, "share_cumsum": share, "shift": 16384.0}
+
+            def train():
+                for x in xs:
+                    x.grad = None
+                kb.dilution_attention(*xs, dot_precision="bf16", **kw).backward(do)
+
+            def decode():
+                kb.dilution_decode_step(q1, kc, vc, com, length, **kw)
+
+            train()
+            t_ms = timed(train, args.variant_steps)
+            com.zero_()
+            for _ in range(2):
+                decode()
+            d_ms = timed(decode, args.variant_steps)
+            out[f"{bid}/{share}"] = {"train_ms": round(t_ms, 3),
+                                     "train_tflops": round(flops / (t_ms * 1e-3) / 1e12, 1),
+                                     "decode_ms": round(d_ms, 4),
+                                     "decode_gbs": round(nbytes / (d_ms * 1e-3) / 1e9, 1)}
+    log(f"variants: {len(out)} operators timed")
+    return {"config": {"train": f"fwd+bwd B{batch} H{heads} T{seq} d{d} bf16",
+                       "decode": f"B{dbatch} H{dheads} L{length} d{d} bf16", "shift": 16384.0,
+                       "steps": args.variant_steps},
+            "operators": out}
 
 
 def bench_prefill(args, dev):
@@ -490,6 +546,9 @@ def main() -> int:
             line["sdpa"] = sd
         except Exception as exc:  # backend unavailable: report, do not fall back
             line["sdpa"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
+    if not args.no_variants:
+        line["variants"] = bench_variants(args, dev, tr["inputs"])
+        torch.cuda.empty_cache()
     del tr["inputs"]
     if not args.no_decode:
         torch.cuda.empty_cache()

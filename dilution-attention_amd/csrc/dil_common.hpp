@@ -35,6 +35,7 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kEps = 1e-9f;                    // reference kernels.py:66-67
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Storage dtypes understood by the C ABI (include/dilution_hip.h).
 enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
@@ -189,5 +190,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 }  // namespace dil

@@ -73,8 +73,9 @@ __device__ __forceinline__ float bid_f(float a) {
     const float r = fmaxf(a, 0.f);
     return r * r;
   } else if constexpr (BID == BID_SOFTPLUS) {
-    // max(a, 0) + log(1 + e^-|a|), the stable softplus
-    return fmaxf(a, 0.f) + log1pf(__expf(-fabsf(a)));
+    // max(a, 0) + log(1 + e^-|a|), the stable softplus (kernels_bid.py:219),
+    // on the hardware exp2 / log2: 1 + e^-|a| lies in (1, 2]
+    return fmaxf(a, 0.f) + kLn2 * fast_log2(1.f + fast_exp2(-kLog2e * fabsf(a)));
   } else {
     return a;                                   // minshift: the row minimum sits in r1
   }

@@ -17,6 +17,10 @@ whole prompt in one forward call, ``begin_cache(..., chunk=C)`` prefills it in
 chunks of C rows through ``dilution_prefill_chunk``, writing K/V and the
 demand straight into the cache buffers; with ``chunk=None`` it runs the
 one-call forward as the reference does.  Both give the same outputs and demand.
+
+The ablation variants (``bid`` / ``share_cumsum`` / ``shift`` keywords, the
+operators of ``kernels_bid``) prefill in one call and decode through the
+variant decode step (model.py:198-241 with ``_bid_kw``).
 """
 
 from __future__ import annotations
@@ -24,6 +28,7 @@ from __future__ import annotations
 import torch
 
 from . import kernels
+from . import kernels_bid
 
 
 def _precision(dtype: torch.dtype) -> str:
@@ -57,16 +62,22 @@ def append_kv(cache: dict, k1: torch.Tensor, v1: torch.Tensor) -> int:
 
 
 def begin_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, capacity: int | None = None,
-                chunk: int | None = None, dot_precision: str | None = None):
+                chunk: int | None = None, dot_precision: str | None = None, **bid_kw):
     """Prefill a prompt: returns (y, cache) with y (B, H, T, D) in q.dtype.
 
     chunk=None runs the one-call forward and copies ``committed_total`` into
     the cache (model.py:202-228); chunk=C prefills C rows at a time with the
-    demand carried in the cache's buffer.
+    demand carried in the cache's buffer.  ``bid_kw`` (bid, share_cumsum,
+    shift) selects an ablation variant, always prefilled in one call.
     """
     prec = dot_precision or _precision(q.dtype)
     seq = q.shape[2]
     cache = alloc_cache(k, v, capacity)
+    if bid_kw:
+        y, aux = kernels_bid.dilution_attention_forward(q, k, v, dot_precision=prec, return_aux=True,
+                                                        **bid_kw)
+        cache["committed"][:, :, :seq] = aux["committed_total"]
+        return y.to(q.dtype), cache
     if chunk is None:
         y, aux = kernels.dilution_attention_forward(q, k, v, dot_precision=prec, return_aux=True)
         cache["committed"][:, :, :seq] = aux["committed_total"]
@@ -81,9 +92,11 @@ def begin_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, capacity: int
     return torch.cat(outs, dim=2).to(q.dtype), cache
 
 
-def step_cache(q1: torch.Tensor, k1: torch.Tensor, v1: torch.Tensor, cache: dict) -> torch.Tensor:
+def step_cache(q1: torch.Tensor, k1: torch.Tensor, v1: torch.Tensor, cache: dict, **bid_kw) -> torch.Tensor:
     """One decode token: append (k1, v1) and return the new row's output
     (B, H, 1, D) in q1.dtype, advancing the cache's demand in place
-    (model.py:231-241)."""
+    (model.py:231-241); ``bid_kw`` as in ``begin_cache``."""
     t = append_kv(cache, k1, v1)
+    if bid_kw:
+        return kernels_bid.dilution_decode_step(q1, cache["k"], cache["v"], cache["committed"], t, **bid_kw)
     return kernels.dilution_decode_step(q1, cache["k"], cache["v"], cache["committed"], t)

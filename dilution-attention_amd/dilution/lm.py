@@ -10,7 +10,9 @@ weights).  It follows the reference's module layout and cache protocol
   projection (model.py:120-257 with ``use_kernel`` on: training forward
   through ``kernels.dilution_attention``, no-grad forward through
   ``kernels.dilution_attention_forward``, prefill and cached decode through
-  ``dilution.cache``);
+  ``dilution.cache``); ``LMConfig.bid`` / ``share_cumsum`` select an ablation
+  variant of the operator, which runs on ``kernels_bid`` with
+  SHIFT = ``context_length`` (model.py:121-156);
 * ``SoftmaxAttention``: the parameter-matched causal softmax control on
   torch SDPA, with a plain KV cache (model.py:96-117), selected per layer by
   ``LMConfig.attention`` / ``layer_attention`` as in the reference's
@@ -37,6 +39,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import cache as dcache
 from . import kernels
+from . import kernels_bid
 
 
 @dataclass
@@ -50,6 +53,9 @@ class LMConfig:
     prefill_chunk: int | None = 2048
     attention: str = "dilution"     # default slot type: "dilution" or "softmax"
     layer_attention: list | None = None
+    bid: str = "softmax"            # bid function of the dilution slots (kernels_bid.BID_TYPES)
+    share_cumsum: bool | str = True # True: dilution share, "exclusive", False: no share step
+    context_length: int = 16384     # the SHIFT of the expshift / sigshift bids (config.py:68-72)
 
     def __post_init__(self):
         if self.d_model % self.n_heads:
@@ -61,6 +67,17 @@ class LMConfig:
         bad = sorted(set(self.layer_kinds()) - set(ATTENTION_TYPES))
         if bad:
             raise ValueError(f"attention kinds must be in {ATTENTION_TYPES}; got {bad}")
+        # config.py:111-116
+        if not (isinstance(self.share_cumsum, bool) or self.share_cumsum == "exclusive"):
+            raise ValueError('share_cumsum must be a boolean or "exclusive"')
+        if self.bid not in kernels_bid.BID_TYPES:
+            raise ValueError(f"bid must be one of {kernels_bid.BID_TYPES}; got {self.bid!r}")
+        if not self.production_operator() and self.d_model // self.n_heads != kernels_bid.VARIANT_HEAD_DIM:
+            raise ValueError(f"the bid / share ablations need head_dim {kernels_bid.VARIANT_HEAD_DIM}")
+
+    def production_operator(self) -> bool:
+        """softmax bids with the dilution share: the operator of ``kernels``."""
+        return self.bid == "softmax" and self.share_cumsum is True
 
     def layer_kinds(self) -> list[str]:
         if self.layer_attention is not None:
@@ -131,29 +148,38 @@ class SoftmaxAttention(_AttentionBase):
 
 
 class DilutionAttention(_AttentionBase):
-    """The dilution operator on the HIP kernels (model.py:120-257)."""
+    """The dilution operator on the HIP kernels (model.py:120-257): the
+    production operator through ``kernels``, an ablation variant (bid,
+    share_cumsum) through ``kernels_bid`` (model.py:142-156)."""
+
+    def __init__(self, cfg: LMConfig):
+        super().__init__(cfg)
+        self.production = cfg.production_operator()
+        self.bid_kw = {} if self.production else {
+            "bid": cfg.bid, "share_cumsum": cfg.share_cumsum, "shift": float(cfg.context_length)}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         batch, seq, _ = x.shape
         q, k, v = self._split_heads(x)
         prec = "bf16" if q.dtype == torch.bfloat16 else "tf32"
+        ops = kernels if self.production else kernels_bid
         if torch.is_grad_enabled():
-            y = kernels.dilution_attention(q, k, v, dot_precision=prec)
+            y = ops.dilution_attention(q, k, v, dot_precision=prec, **self.bid_kw)
         else:
-            y = kernels.dilution_attention_forward(q, k, v, dot_precision=prec)
+            y = ops.dilution_attention_forward(q, k, v, dot_precision=prec, **self.bid_kw)
         return self._merge_heads(y.to(x.dtype), batch, seq)
 
     def begin_cache(self, x: torch.Tensor, capacity: int | None = None):
         batch, seq, _ = x.shape
         q, k, v = self._split_heads(x)
         y, cache = dcache.begin_cache(q, k.contiguous(), v.contiguous(), capacity=capacity,
-                                      chunk=self.prefill_chunk)
+                                      chunk=self.prefill_chunk, **self.bid_kw)
         return self._merge_heads(y.to(x.dtype), batch, seq), cache
 
     def step_cache(self, x1: torch.Tensor, cache: dict) -> torch.Tensor:
         batch = x1.shape[0]
         q1, k1, v1 = self._split_heads(x1)
-        y = dcache.step_cache(q1, k1, v1, cache)
+        y = dcache.step_cache(q1, k1, v1, cache, **self.bid_kw)
         return self._merge_heads(y.to(x1.dtype), batch, 1)
 
 

@@ -7,7 +7,11 @@ the reference's tests/test_model.py:
   (test_model.py:99-110) -- here through chunked prefill and the HIP decode
   step, and through the softmax control's KV cache in mixed stacks;
 * a bf16 training step produces a finite loss and finite gradients in
-  every parameter.
+  every parameter;
+* the bid / share ablations (``LMConfig.bid``, ``share_cumsum``): the model on
+  the variant kernels matches the same model on the plain-torch variant
+  specification (test_kernels.py:360-374, same 5e-2 logit bound), and their
+  cached decode reproduces the full forward.
 """
 
 from __future__ import annotations
@@ -18,11 +22,15 @@ import torch
 from gpu_helpers import needs_gpu
 
 
-def _small(dtype=torch.float32, chunk=16, kinds=None):
+def _small(dtype=torch.float32, chunk=16, kinds=None, **variant):
     from dilution.lm import DilutionLM, LMConfig
 
-    cfg = LMConfig(vocab_size=97, n_layers=2, d_model=64, n_heads=4, prefill_chunk=chunk,
-                   layer_attention=kinds)
+    if variant:                                   # the ablation variants take head_dim 64
+        cfg = LMConfig(vocab_size=97, n_layers=2, d_model=128, n_heads=2, prefill_chunk=chunk,
+                       layer_attention=kinds, context_length=96, **variant)
+    else:
+        cfg = LMConfig(vocab_size=97, n_layers=2, d_model=64, n_heads=4, prefill_chunk=chunk,
+                       layer_attention=kinds)
     torch.manual_seed(0)
     return DilutionLM(cfg).to(device="cuda", dtype=dtype).eval()
 
@@ -40,6 +48,14 @@ def test_config_validation():
         LMConfig(attention="linear")
     assert LMConfig(n_layers=2, layer_attention=["softmax", "dilution"]).layer_kinds() == [
         "softmax", "dilution"]
+    with pytest.raises(ValueError):
+        LMConfig(bid="tanh")
+    with pytest.raises(ValueError):
+        LMConfig(share_cumsum="inclusive")
+    with pytest.raises(ValueError):
+        LMConfig(d_model=256, n_heads=8, bid="relu")             # head_dim 32: no variant build
+    assert LMConfig(d_model=256, n_heads=8).production_operator()
+    assert not LMConfig(d_model=256, n_heads=4, share_cumsum=False).production_operator()
 
 
 @pytest.mark.gpu
@@ -103,3 +119,52 @@ def test_generate_extends_prompt():
     idx = torch.zeros(1, 5, dtype=torch.long, device="cuda")
     out = model.generate(idx, 6)
     assert out.shape == (1, 11) and torch.equal(out[:, :5], idx)
+
+
+@pytest.mark.gpu
+@needs_gpu
+@pytest.mark.parametrize("bid", ["relu", "relu2", "softplus", "minshift", "sigmoid", "expshift", "sigshift"])
+def test_variant_model_matches_torch_specification(bid, monkeypatch):
+    from dilution import kernels_bid as kb
+    from dilution import lm
+
+    model = _small(kinds=["dilution", "softmax"], bid=bid)
+    g = torch.Generator().manual_seed(7)
+    idx = torch.randint(0, 97, (2, 96), generator=g).cuda()
+    with torch.no_grad():
+        fused = model.lm_head(model.ln_f(_hidden(model, idx)))
+        spec = lambda q, k, v, dot_precision, **kw: kb.dilution_attention_reference(q, k, v, **kw)
+        monkeypatch.setattr(lm.kernels_bid, "dilution_attention_forward", spec)
+        eager = model.lm_head(model.ln_f(_hidden(model, idx)))
+    assert (fused - eager).abs().max().item() < 5e-2
+
+
+@pytest.mark.gpu
+@needs_gpu
+@pytest.mark.parametrize("bid,share", [("relu2", True), ("minshift", "exclusive"), ("sigshift", False),
+                                       ("expshift", True)])
+def test_variant_cached_decode_matches_full_forward(bid, share):
+    model = _small(kinds=["dilution", "softmax"], bid=bid, share_cumsum=share)
+    g = torch.Generator().manual_seed(8)
+    idx = torch.randint(0, 97, (2, 50), generator=g).cuda()
+    prompt = 37
+    with torch.no_grad():
+        full = model.lm_head(model.ln_f(_hidden(model, idx)))
+        logits, caches = model.prefill(idx[:, :prompt], capacity=idx.shape[1])
+        assert torch.allclose(logits[:, 0], full[:, prompt - 1], atol=1e-4)
+        for t in range(prompt, idx.shape[1]):
+            logits = model.decode_step(idx[:, t:t + 1], caches)
+            assert torch.allclose(logits[:, 0], full[:, t], atol=1e-4), t
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_variant_training_step_bf16_finite():
+    model = _small(dtype=torch.bfloat16, bid="sigshift", share_cumsum=True).train()
+    g = torch.Generator().manual_seed(9)
+    idx = torch.randint(0, 97, (2, 64), generator=g).cuda()
+    _, loss = model(idx[:, :-1], idx[:, 1:])
+    loss.backward()
+    assert torch.isfinite(loss)
+    for name, p in model.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name
