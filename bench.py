@@ -25,7 +25,7 @@ The same line carries
     configs[3]: B=16 H=16 d=64 bf16), algorithmic TFLOP/s;
   * ``decode``: the cached decode step at 128K context (
     B=16 H=16 d=64 bf16), HBM GB/s over B H L (4d + 8) algorithmic bytes per
-    step, with its own roofline object;
+    step, with its own roofline object, and a ``sweep`` at 16K / 32K / 64K;
   * ``lm``: the whole random-init LM on this
     operator: training-step, prefill and greedy-decode tokens/s with the
     attention kernels' share of each, and the same LM with softmax (SDPA)
@@ -107,6 +107,7 @@ def parse_args():
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--decode-context", type=int, default=131072)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-decode-sweep", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-sdpa", action="store_true")
@@ -337,6 +338,22 @@ def bench_variants(args, dev, inputs):
             "operators": out}
 
 
+def bench_decode_sweep(args, dev) -> list:
+    """The decode bandwidth leg at contexts 16K, 32K, 64K (and the headline
+    128K above): ms per step and GB/s on the same B H L (4d + 8) bytes."""
+    import torch
+
+    out = []
+    for length in (16384, 32768, 65536):
+        sub = argparse.Namespace(**vars(args))
+        sub.decode_context = length
+        r = bench_decode(sub, dev)
+        out.append({"context": length, "ms_per_step": r["ms_per_step"], "value": r["value"],
+                    "pct_of_peak": r["pct_of_peak"]})
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_prefill(args, dev):
     """Chunked prefill: B16 H16 d64 bf16, a 16384-token
     prompt in 2048-token chunks through ``dilution_prefill_chunk`` with the
@@ -553,6 +570,8 @@ def main() -> int:
     if not args.no_decode:
         torch.cuda.empty_cache()
         line["decode"] = bench_decode(args, dev)
+        if not args.no_decode_sweep:
+            line["decode"]["sweep"] = bench_decode_sweep(args, dev)
     if not args.no_prefill:
         torch.cuda.empty_cache()
         line["prefill"] = bench_prefill(args, dev)

@@ -28,6 +28,8 @@ own formula; see tests/test_oracle.py):
                           q = 0 harmonic-number closed form, T = 1, causality,
                           shift invariance, and planted-mistake variants that
                           must fail those checks.
+  attention_blocked_f64   attention_f64 at ragged lengths and block sizes,
+                          and the harmonic closed form at T = 3000.
   attention_loops_f64     the harmonic closed form (independent of softmax
                           and cumsum code) and agreement with attention_fp32.
   row_stats / bids        torch.softmax (a library routine) at fp64.
@@ -93,6 +95,33 @@ def attention_f64(q, k, v) -> torch.Tensor:
     share = p / (demand_before + p + EPS)
     a = share / (share.sum(dim=-1, keepdim=True) + EPS)
     return torch.matmul(a, v)
+
+
+def attention_blocked_f64(q, k, v, block: int = 512) -> tuple[np.ndarray, np.ndarray]:
+    """One (batch, head) slice at any length: q, k, v (T, D) -> (out (T, D),
+    demand totals (T,)), float64, in row blocks of `block` with the demand
+    carried from block to block, so memory is O(block T) rather than O(T^2).
+    The same formula as attention_f64 (kernels.py:40-68), evaluated the way
+    the eager prefill carries demand across prompts (model.py:209-222); what
+    makes the full-size (T = 16384) parity checks affordable on host cores."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    t, d = q.shape
+    out = np.empty((t, v.shape[1]))
+    demand = np.zeros(t)
+    for r0 in range(0, t, block):
+        r1 = min(r0 + block, t)
+        s = (q[r0:r1] @ k[:r1].T) / math.sqrt(d)                 # (rows, keys [0, r1))
+        s[np.arange(r1)[None, :] > np.arange(r0, r1)[:, None]] = -np.inf
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=1, keepdims=True)
+        before = demand[:r1] + np.cumsum(p, axis=0) - p           # exclusive column sums
+        share = p / (before + p + EPS)
+        out[r0:r1] = (share / (share.sum(axis=1, keepdims=True) + EPS)) @ v[:r1]
+        demand[:r1] += p.sum(axis=0)
+    return out, demand
 
 
 def attention_loops_f64(q, k, v) -> np.ndarray:

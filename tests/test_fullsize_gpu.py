@@ -1,0 +1,155 @@
+"""Parity at the benchmark's full sizes (C3 training, C4 prefill + decode,
+decode at 128K), where the dense oracle does not fit: the row-blocked fp64
+oracle on a few (batch, head) slices, plus size-independent properties on
+every slice.
+
+* C3, B1 H16 T16384 d64 bf16 (q, k ~ 0.5 N(0,1), v, dO ~ N(0,1)):
+  - output rows of slices 0 and 15 against ``attention_blocked_f64`` on the
+    bf16-rounded inputs (2e-2 max-abs, 1e-2 mean-rel: the bf16 bounds);
+  - the first 4096 rows are bit-identical to the forward of the 4096-token
+    prefix (causality, test_model.py:46-56);
+  - rows of the attention matrix sum to one, so sum_j dv_j = sum_i dO_i.  The
+    kernel rounds the share tile, dO / (S + eps) and dv to bf16 (relative
+    error <= 2^-9 each), which bounds the gap by 2^-8 (sum |dv| + sum |dO|).
+* The same shape in fp32 operands: sum_j dk_j = 0 (adding a constant to every
+  key leaves each softmax row unchanged) within 1e-4 of sum_j |dk_j|, and the
+  dv identity within 1e-5.
+* C4, B16 H16 d64 bf16: a 16384-token prompt prefilled in 8 chunks of 2048,
+  then 256 decode steps to 16640.  Prefill rows, decode rows and the demand
+  equal the one-call forward of all 16640 rows (2e-2 on bf16 outputs, 1e-5
+  relative on the demand); every row's bids sum to one, so the final demand
+  sums to 16640; slice (0, 0) against the blocked oracle.
+* Decode at 128K (B16 H16 d64 bf16 caches): one step on every slice against
+  a plain torch statement of the step (the output within 2e-2; each demand
+  entry within one fp32 spacing of c + p plus the score's rounding bound),
+  and against the fp64 decode oracle on two slices; positions past
+  ``length`` stay bit-untouched.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import max_abs, mean_rel, needs_gpu
+from oracle import dilution_oracle as orc
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+
+def _blocked(q, k, v):
+    out, tot = orc.attention_blocked_f64(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                         v.float().cpu().numpy())
+    return torch.from_numpy(out), torch.from_numpy(tot)
+
+
+def test_c3_training_bf16_full_size():
+    from dilution import kernels
+
+    q, k, v, do = orc.make_inputs((1, 16, 16384, 64), seed=2, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="bf16")
+    out.backward(do.cuda())
+    out = out.detach()
+    torch.cuda.synchronize()
+    for h in (0, 15):
+        want, _ = _blocked(q[0, h], k[0, h], v[0, h])
+        assert max_abs(out[0, h], want) < 2e-2, h
+        assert mean_rel(out[0, h], want) < 1e-2, h
+
+    prefix = kernels.dilution_attention_forward(*(x.detach()[:, :, :4096] for x in xs), dot_precision="bf16")
+    assert torch.equal(prefix, out[:, :, :4096])
+
+    dv = xs[2].grad.double().cpu()
+    dod = do.double()
+    gap = (dv.sum(2) - dod.sum(2)).abs()
+    bound = 2.0 ** -8 * (dv.abs().sum(2) + dod.abs().sum(2))
+    assert (gap <= bound).all(), (gap / bound).max().item()
+
+
+def test_c3_training_fp32_key_shift_invariance():
+    from dilution import kernels
+
+    q, k, v, do = orc.make_inputs((1, 16, 16384, 64), seed=3, qk_scale=0.5, with_dout=True)
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    kernels.dilution_attention(*xs, dot_precision="ieee").backward(do.cuda())
+    dk = xs[1].grad.double().cpu()
+    assert (dk.sum(2).abs() <= 1e-4 * dk.abs().sum(2)).all()
+    dv = xs[2].grad.double().cpu()
+    gap = (dv.sum(2) - do.double().sum(2)).abs()
+    assert (gap <= 1e-5 * (dv.abs().sum(2) + do.double().abs().sum(2))).all()
+
+
+def test_c4_chunked_prefill_then_256_decode_steps():
+    from dilution import cache as dcache
+    from dilution import kernels
+
+    b, h, d, t0, steps = 16, 16, 64, 16384, 256
+    t1 = t0 + steps
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q, k, v = (torch.randn(b, h, t1, d, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
+    full, aux = kernels.dilution_attention_forward(q, k, v, dot_precision="bf16", return_aux=True)
+    y, cache = dcache.begin_cache(q[:, :, :t0], k[:, :, :t0].contiguous(), v[:, :, :t0].contiguous(),
+                                  capacity=t1, chunk=2048)
+    assert max_abs(y, full[:, :, :t0]) < 2e-2
+    rows = []
+    for t in range(t0, t1):
+        rows.append(dcache.step_cache(q[:, :, t:t + 1], k[:, :, t:t + 1], v[:, :, t:t + 1], cache))
+    dec = torch.cat(rows, dim=2)
+    assert max_abs(dec, full[:, :, t0:]) < 2e-2
+    com = cache["committed"]
+    tot = aux["committed_total"]
+    assert max_abs(com, tot) < 1e-5 * max(1.0, tot.abs().max().item())
+    sums = com.double().sum(-1)
+    assert (sums - t1).abs().max().item() < 1e-5 * t1
+
+    want, want_tot = _blocked(q[0, 0], k[0, 0], v[0, 0])
+    got = torch.cat([y[0, 0], dec[0, 0]], dim=0)
+    assert max_abs(got, want) < 2e-2
+    assert mean_rel(got, want) < 1e-2
+    assert max_abs(com[0, 0], want_tot) < 1e-5 * max(1.0, want_tot.abs().max().item())
+
+
+def test_decode_at_128k_context():
+    from dilution import kernels
+
+    b, h, d, length = 16, 16, 64, 131072
+    cap = length + 64
+    g = torch.Generator(device="cuda").manual_seed(6)
+    kc = torch.randn(b, h, cap, d, device="cuda", generator=g).to(torch.bfloat16)
+    vc = torch.randn(b, h, cap, d, device="cuda", generator=g).to(torch.bfloat16)
+    q1 = torch.randn(b, h, 1, d, device="cuda", generator=g).to(torch.bfloat16)
+    com = torch.rand(b, h, cap, device="cuda", generator=g) * 4.0
+    com[..., length - 1] = 0.0
+    before = com.clone()
+    out = kernels.dilution_decode_step(q1, kc, vc, com, length)
+    torch.cuda.synchronize()
+    assert torch.equal(com[..., length:], before[..., length:])
+
+    # every slice against a plain torch statement of the step (fp64 scores of
+    # the bf16 values, so the reference's own rounding does not count)
+    kd = kc[..., :length, :].double()
+    aff = torch.matmul(q1.double(), kd.transpose(-1, -2).contiguous())[..., 0, :] / 8.0
+    p = torch.softmax(aff, dim=-1)
+    c = before[..., :length].double()
+    share = p / (c + p + 1e-9)
+    want = torch.matmul((share / (share.sum(-1, keepdim=True) + 1e-9))[..., None, :],
+                        vc[..., :length, :].double())
+    assert max_abs(out, want) < 2e-2
+    # committed = fl(c + p_kernel).  The kernel's fp32 score of a 64-term dot
+    # is off by at most 65 * 2^-24 * sum |q_d k_d| / 8 (the gamma_n bound of a
+    # recursive fma sum); p moves by that relative to its own score and to the
+    # row's normaliser, plus a few ulps of exp2 / rcp.
+    err_a = 65 * 2.0 ** -24 * torch.matmul(q1.double().abs(), kd.abs().transpose(-1, -2).contiguous())[..., 0, :] / 8.0
+    rel_p = 2 * err_a + 2 * err_a.amax(-1, keepdim=True) + 8 * 2.0 ** -24
+    after = com[..., :length]
+    spacing = (torch.nextafter(after, torch.full_like(after, float("inf"))) - after).double()
+    assert ((after.double() - (c + p)).abs() <= spacing + p * rel_p).all()
+
+    for bi, hi in ((0, 0), (15, 15)):
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        want64, want_com = orc.decode_step(q1[sl].cpu(), kc[sl].cpu(), vc[sl].cpu(), before[sl].cpu(), length)
+        assert max_abs(out[sl], want64) < 2e-2
+        assert max_abs(com[sl][..., :length], want_com[..., :length]) < 1e-5 * 4.0

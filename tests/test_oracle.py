@@ -50,6 +50,27 @@ def test_harmonic_closed_form(t):
     assert np.abs(tot - totals_cf).max() < 1e-12
 
 
+@pytest.mark.parametrize("t,block", [(1, 4), (300, 64), (257, 100), (130, 512)])
+def test_blocked_restatement_matches_fp64(t, block):
+    """The row-blocked slice oracle (the full-size checker) against the dense
+    fp64 formula, at ragged lengths and block sizes."""
+    q, k, v = _rand((1, 1, t, 16), seed=400 + t)
+    out, tot = orc.attention_blocked_f64(q[0, 0], k[0, 0], v[0, 0], block=block)
+    assert np.abs(out - orc.attention_f64(q, k, v).numpy()[0, 0]).max() < 1e-12
+    assert np.abs(tot - orc.demand_totals(q, k).numpy()[0, 0]).max() < 1e-10
+
+
+def test_blocked_restatement_harmonic_closed_form():
+    t = 3000
+    g = torch.Generator().manual_seed(5)
+    v = torch.randn(t, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(t, 8, generator=g, dtype=torch.float64)
+    out_cf, totals_cf = orc.harmonic_closed_form(t, v.numpy())
+    out, tot = orc.attention_blocked_f64(np.zeros((t, 8)), k, v, block=512)
+    assert np.abs(out - out_cf).max() < 1e-10
+    assert np.abs(tot - totals_cf).max() < 1e-10
+
+
 def test_single_row_returns_first_value():
     """T = 1: share = p/(p+eps) ~ 1, so out_0 = v_0 up to eps."""
     q, k, v = _rand((1, 1, 1, 32), seed=3)
