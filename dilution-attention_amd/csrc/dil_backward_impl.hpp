@@ -153,6 +153,13 @@ struct RowStatsLoader {
       lds[t] = (t >= kTileQ && t < 2 * kTileQ) ? -v : v;
     }
   }
+  // every thread writes (threads past the arrays into padding, lds holding
+  // kThreads floats): no exec-masked branch around the wait for the load
+  __device__ void store_all(float* lds) const {
+    const int t = threadIdx.x;
+    const float v = ok ? r : (t < kTileQ ? pad0 : 0.f);
+    lds[t] = (t >= kTileQ && t < 2 * kTileQ) ? -v : v;
+  }
 };
 
 // 16 consecutive floats of LDS into registers (four 16-byte reads).
@@ -184,8 +191,9 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float st_s[2][kNS * kTileQ];   // lse (r0), -dbs, r1
-  __shared__ float cs_s[2][4 * kTileK];                                // demand checkpoints
+  // lse (r0), -dbs, r1, then padding: every thread of the stash writes a slot
+  __shared__ __attribute__((aligned(16))) float st_s[2][kThreads];
+  __shared__ float cs_s[2][kThreads];             // demand checkpoints of the 128 keys, then padding
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
   if (!item.valid) return;
@@ -247,8 +255,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     dl.store(do_s[buf]);
     qtl.store(qt_s[buf]);
     dtl.store(dot_s[buf]);
-    sl.store(st_s[buf]);
-    if (threadIdx.x < 4 * kTileK) cs_s[buf][threadIdx.x] = ck_ok ? cr : 0.f;
+    sl.store_all(st_s[buf]);
+    cs_s[buf][threadIdx.x] = ck_ok ? cr : 0.f;
   };
   constexpr int kSteps = kTileQ / Mma<CT>::kStep;
 
@@ -359,16 +367,23 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   stash(0);
   __syncthreads();
   int it = 0;
+  // vmcnt counts stores as well as loads, so the compiler must know on every
+  // path how many memory operations follow the fetched data when the stash
+  // waits for it: the stash is unconditional (the last iteration stashes into
+  // the idle buffer), every thread writes LDS in it, and the step's suffix
+  // checkpoint is stored after it (stored inside the conditional step, the
+  // wait would also wait for that store).
   for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
     const int buf = it & 1;
     fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
-    if (active && qt >= kb) {
-      const float sufk_in = sufk;                // suffix entering this tile from below
+    const bool run = active && qt >= kb;
+    const float sufk_in = sufk;                  // suffix entering this tile from below
+    if (run) {
       if (qt > kb) step(qt, buf, std::false_type{});
       else step(qt, buf, std::true_type{});
-      if (h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     }
-    if (qt - 1 >= kb0) stash(buf ^ 1);
+    stash(buf ^ 1);
+    if (run && h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     sync_lds();
   }
 

@@ -299,7 +299,8 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
   using T = Tiles<CT, D>;
   constexpr int kRP = BID == BID_SOFTMAX ? 1 : 2;                  // per-row parameters
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * T::kKStride];
-  __shared__ __attribute__((aligned(16))) float st_s[2][kRP][kTileQ];   // (r0, r1) of the block's rows
+  // (r0, r1) of the block's rows, then padding: every thread of the stash writes
+  __shared__ __attribute__((aligned(16))) float st_s[2][kRP][kThreads];
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
   if (!item.valid) return;
@@ -347,16 +348,16 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
   };
   auto stash = [&](int buf) {
     ql.store(q_s[buf]);
-    if (threadIdx.x < kTileQ) {
-      if constexpr (BID == BID_SOFTMAX) {
-        st_s[buf][0][threadIdx.x] = row_ok ? rmax_r + __log2f(rden_r) : INFINITY;
-      } else {
-        float r0, r1;
-        const float window = static_cast<float>(P.q0 + (it_row0 + threadIdx.x) + 1);
-        bid_row_params<BID>(rmax_r, rden_r, window, row_ok, r0, r1);
-        st_s[buf][0][threadIdx.x] = r0;
-        st_s[buf][1][threadIdx.x] = r1;
-      }
+    // threads past the block's 32 rows write padding (no exec-masked branch
+    // around the wait for the loaded statistics)
+    if constexpr (BID == BID_SOFTMAX) {
+      st_s[buf][0][threadIdx.x] = row_ok ? rmax_r + __log2f(rden_r) : INFINITY;
+    } else {
+      float r0, r1;
+      const float window = static_cast<float>(P.q0 + (it_row0 + (threadIdx.x & (kTileQ - 1))) + 1);
+      bid_row_params<BID>(rmax_r, rden_r, window, row_ok, r0, r1);
+      st_s[buf][0][threadIdx.x] = r0;
+      st_s[buf][1][threadIdx.x] = r1;
     }
   };
 
@@ -402,18 +403,23 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
     stash(0);
   }
   __syncthreads();
+  // vmcnt counts stores as well as loads: the stash is unconditional (the
+  // last iteration stashes into the idle buffer) and the checkpoint is stored
+  // after it, so that the wait for the fetched block never waits for a store
   int it = 0;
   for (int64_t b = b_wg; b < nb; ++b, ++it) {
     const int buf = it & 1;
     fetch(min(b + 1, nb - 1));                  // the last step reloads its own block, unused
     // wave-uniform condition: every lane must feed the MFMAs of the step
-    if (b >= b_w && key0 < P.Tk) {
-      if (h == 0 && key_ok) ccol[b * P.Tk] = static_cast<float>(run);   // demand entering block b
+    const bool on = b >= b_w && key0 < P.Tk;
+    const float entering = static_cast<float>(run);   // demand entering block b
+    if (on) {
       const int64_t first_row = P.q0 + b * kTileQ;
       if (key0 + kTileK - 1 <= first_row) step(b, buf, std::false_type{});
       else step(b, buf, std::true_type{});
     }
-    if (b + 1 < nb) stash(buf ^ 1);
+    stash(buf ^ 1);
+    if (on && h == 0 && key_ok) ccol[b * P.Tk] = entering;
     sync_lds();
   }
   if (key_ok && h == 0) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
