@@ -241,36 +241,20 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   const bool ck_ok = ck < P.T;
   const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
   float cr = 0.f;
-  // bf16 tiles go straight to LDS (buffer_load ... lds into stage `buf`); the
-  // fp32 ones through registers (stored by stash)
-  constexpr bool kDma = TL::kSwz;
-  // slices are far below 2 GB, the range of a buffer resource
-  const int row_bytes = static_cast<int>(P.T * D * static_cast<int64_t>(sizeof(CT)));
-  const int t_bytes = static_cast<int>(P.t_pad * D * static_cast<int64_t>(sizeof(CT)));
-  auto fetch = [&](int qt, int buf) {
+  auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-    // the small loads first: waiting for them in stash does not wait for the DMA
+    ql.load(qs, row0, P.T);
+    dl.load(dos, row0, P.T);
+    qtl.load(qts, row0);
+    dtl.load(dots, row0);
     sl.load(lse, dbs, BID == BID_SOFTMAX ? dbs : P.rb1 + slice * P.T, row0, P.T);
     cr = ccol[static_cast<int64_t>(qt) * P.T];
-    if constexpr (kDma) {
-      DmaRowTile<CT, D, true>::copy(qs, row_bytes, q_s[buf], static_cast<int>(row0));
-      DmaRowTile<CT, D, true>::copy(dos, row_bytes, do_s[buf], static_cast<int>(row0));
-      DmaTTile<CT, D>::copy(qts, t_bytes, qt_s[buf], static_cast<int>(row0));
-      DmaTTile<CT, D>::copy(dots, t_bytes, dot_s[buf], static_cast<int>(row0));
-    } else {
-      ql.load(qs, row0, P.T);
-      dl.load(dos, row0, P.T);
-      qtl.load(qts, row0);
-      dtl.load(dots, row0);
-    }
   };
   auto stash = [&](int buf) {
-    if constexpr (!kDma) {
-      ql.store(q_s[buf]);
-      dl.store(do_s[buf]);
-      qtl.store(qt_s[buf]);
-      dtl.store(dot_s[buf]);
-    }
+    ql.store(q_s[buf]);
+    dl.store(do_s[buf]);
+    qtl.store(qt_s[buf]);
+    dtl.store(dot_s[buf]);
     sl.store_all(st_s[buf]);
     cs_s[buf][threadIdx.x] = ck_ok ? cr : 0.f;
   };
@@ -379,35 +363,29 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     }
   };
 
-  fetch(nq - 1, 0);
+  fetch(nq - 1);
   stash(0);
   __syncthreads();
   int it = 0;
-  // vmcnt counts stores as well as loads (and the LDS DMA, which the barrier
-  // waits for), so the compiler must know on every path how many memory
-  // operations follow the fetched data when the stash waits for it: the stash
-  // is unconditional (the last iteration stashes into the idle buffer), every
-  // thread writes LDS in it, and the step's suffix checkpoint is stored at the
-  // start of the next iteration, under that iteration's step.
-  bool pend = false;
-  float pend_val = 0.f;
-  int64_t pend_at = 0;
+  // vmcnt counts stores as well as loads, so the compiler must know on every
+  // path how many memory operations follow the fetched data when the stash
+  // waits for it: the stash is unconditional (the last iteration stashes into
+  // the idle buffer), every thread writes LDS in it, and the step's suffix
+  // checkpoint is stored after it (stored inside the conditional step, the
+  // wait would also wait for that store).
   for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
     const int buf = it & 1;
-    fetch(max(qt - 1, kb0), buf ^ 1);            // the last step reloads its own tile, unused
-    if (pend) sufk_col[pend_at] = pend_val;
+    fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
     const bool run = active && qt >= kb;
-    pend = run && h == 0 && key < P.T;
-    pend_val = sufk;                             // suffix entering this tile from below
-    pend_at = static_cast<int64_t>(qt) * P.T;
+    const float sufk_in = sufk;                  // suffix entering this tile from below
     if (run) {
       if (qt > kb) step(qt, buf, std::false_type{});
       else step(qt, buf, std::true_type{});
     }
     stash(buf ^ 1);
+    if (run && h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     sync_lds();
   }
-  if (pend) sufk_col[pend_at] = pend_val;
 
   if (key < P.T) {
     float* dkrow = P.dkm + (slice * P.T + key) * D;
