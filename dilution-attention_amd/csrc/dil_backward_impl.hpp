@@ -116,8 +116,8 @@ __global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, i
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ qt,
                                                         const float* __restrict__ ghat, int64_t T,
-                                                        int64_t t_pad, CT* __restrict__ dst) {
-  const int64_t slice = blockIdx.y;
+                                                        int64_t t_pad, CT* __restrict__ dst, int64_t slice0) {
+  const int64_t slice = slice0 + blockIdx.y;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 32;
   const int64_t base = slice * D * t_pad + row0 * D;
   for (int e = threadIdx.x; e < 32 * D; e += kThreads) {
@@ -801,7 +801,6 @@ int launch_backward(const BackwardArgs& a) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const bool convert = a.dtype != ctc;
   const int64_t t_pad = pad64(a.T);
-  const unsigned n = static_cast<unsigned>(a.n);
   const int64_t sn = a.T * D;
 
   CT* qt = reinterpret_cast<CT*>(ws + w.qt);
@@ -813,17 +812,19 @@ int launch_backward(const BackwardArgs& a) {
   CT* vc = convert ? reinterpret_cast<CT*>(ws + w.vc) : nullptr;
   CT* doc = reinterpret_cast<CT*>(ws + w.doc);
 
-  const dim3 gp(static_cast<unsigned>(t_pad / 64), n);
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt, D * t_pad,
-                                                        t_pad, nullptr));
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt, D * t_pad,
-                                                        t_pad, nullptr));
-  if (convert)
+  const unsigned tiles64 = static_cast<unsigned>(t_pad / 64);
+  slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn, nullptr, 0,
-                                                          t_pad, nullptr));
+              prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt,
+                                                                         D * t_pad, t_pad, nullptr, s0));
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt,
+                                                                         D * t_pad, t_pad, nullptr, s0));
+    if (convert)
+      DIL_TIMED("prep", st,
+                prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn,
+                                                                           nullptr, 0, t_pad, nullptr, s0));
+  });
 
   BwdParams P{};
   P.q = convert ? static_cast<const void*>(qc) : a.q;
@@ -864,18 +865,22 @@ int launch_backward(const BackwardArgs& a) {
                 a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbs, rows, a.T,
                 reinterpret_cast<float*>(ws + w.rb1))));
   // dO' = dO / (S + eps), row-major and transposed, in the compute type
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gp, kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc, sn, dot,
-                                                        D * t_pad, t_pad, sinv));
+  slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+    DIL_TIMED("prep", st,
+              prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc,
+                                                                         sn, dot, D * t_pad, t_pad, sinv, s0));
+  });
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
   P.kgroups = (nkt + 3) / 4;
   const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
   DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
-  DIL_TIMED("prep", st,
-            prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), n), kThreads, 0, st>>>(
-                qt, P.ghat, a.T, t_pad, qgt));
+  slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+    DIL_TIMED("prep", st,
+              prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), ns), kThreads, 0, st>>>(
+                  qt, P.ghat, a.T, t_pad, qgt, s0));
+  });
   DIL_TIMED("bwd_dkcorr", st, (bwd_dkcorr<CT, D, BID><<<gkey, kThreads, 0, st>>>(P)));
   return static_cast<int>(hipGetLastError());
 }

@@ -86,9 +86,9 @@ template <int D, int DT, int BID = BID_SOFTMAX>
 __global__ __launch_bounds__(kDecThreads) void dec_stats(
     const void* __restrict__ q1, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
     float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
-    float qscale) {
+    float qscale, int64_t slice0) {
   using L = DecLayout<D>;
-  const int64_t slice = blockIdx.y;
+  const int64_t slice = slice0 + blockIdx.y;
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
@@ -185,9 +185,9 @@ template <int D, int DT, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 __global__ __launch_bounds__(kDecThreads) void dec_apply(
     const void* __restrict__ vc, int64_t kv_sn, float* __restrict__ committed, int64_t c_sn,
     const float* __restrict__ aff, const float2* __restrict__ part, float* __restrict__ part_out,
-    int64_t length, int64_t chunk, int nchunk, float shift) {
+    int64_t length, int64_t chunk, int nchunk, float shift, int64_t slice0) {
   using L = DecLayout<D>;
-  const int64_t slice = blockIdx.y;
+  const int64_t slice = slice0 + blockIdx.y;
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
@@ -337,14 +337,17 @@ int launch_decode(const DecodeArgs& a) {
   // softmax bids keep log2-unit affinities, the others natural units
   const float qscale = (BID == BID_SOFTMAX ? kLog2e : 1.f) / sqrtf(static_cast<float>(D));
   hipStream_t st = static_cast<hipStream_t>(a.stream);
-  dim3 grid(nchunk, static_cast<unsigned>(a.n));
-  DIL_TIMED("dec_stats", st,
-            (dec_stats<D, DT, BID><<<grid, kDecThreads, 0, st>>>(a.q1, a.q_sn, a.k_cache, a.kv_sn, aff,
-                                                                 part, a.length, chunk, nchunk, qscale)));
-  DIL_TIMED("dec_apply", st,
-            (dec_apply<D, DT, BID, SHARE><<<grid, kDecThreads, 0, st>>>(
-                a.v_cache, a.kv_sn, a.committed, a.c_sn, aff, part, part_out, a.length, chunk, nchunk,
-                a.var.shift)));
+  slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+    DIL_TIMED("dec_stats", st,
+              (dec_stats<D, DT, BID><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
+                  a.q1, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length, chunk, nchunk, qscale, s0)));
+  });
+  slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+    DIL_TIMED("dec_apply", st,
+              (dec_apply<D, DT, BID, SHARE><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
+                  a.v_cache, a.kv_sn, a.committed, a.c_sn, aff, part, part_out, a.length, chunk, nchunk,
+                  a.var.shift, s0)));
+  });
   DIL_TIMED("dec_finish", st,
             dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
                                                                              a.o_sn, a.dtype));

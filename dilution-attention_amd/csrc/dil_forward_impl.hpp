@@ -667,7 +667,6 @@ int launch_forward(const ForwardArgs& a) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const bool convert = sizeof(CT) == 2 ? a.dtype != DT_BF16 : a.dtype != DT_F32;
   const int64_t tk_pad = pad64(a.Tk);
-  const unsigned n = static_cast<unsigned>(a.n);
 
   CT* vt = reinterpret_cast<CT*>(ws + w.vt);
   CT* kt = a.pk ? reinterpret_cast<CT*>(ws + w.kt) : nullptr;
@@ -675,20 +674,22 @@ int launch_forward(const ForwardArgs& a) {
   CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
 
   // operands in the compute type; V^T (and K^T) tiles
-  const dim3 gk(static_cast<unsigned>(tk_pad / 64), n);
-  DIL_TIMED("prep", st,
-            prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr, 0, vt,
-                                                        D * tk_pad, tk_pad, nullptr));
-  if (convert || kt != nullptr)
+  const unsigned ktiles = static_cast<unsigned>(tk_pad / 64);
+  const unsigned qtiles = static_cast<unsigned>(pad64(a.C) / 64);
+  slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<gk, kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc, a.Tk * D,
-                                                          kt, D * tk_pad, tk_pad, nullptr));
-  if (convert) {
-    const dim3 gq(static_cast<unsigned>(pad64(a.C) / 64), n);
-    DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<gq, kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc, a.C * D,
-                                                          nullptr, 0, 0, nullptr));
-  }
+              prep_kernel<CT, D><<<dim3(ktiles, ns), kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr,
+                                                                        0, vt, D * tk_pad, tk_pad, nullptr, s0));
+    if (convert || kt != nullptr)
+      DIL_TIMED("prep", st,
+                prep_kernel<CT, D><<<dim3(ktiles, ns), kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc,
+                                                                          a.Tk * D, kt, D * tk_pad, tk_pad,
+                                                                          nullptr, s0));
+    if (convert)
+      DIL_TIMED("prep", st,
+                prep_kernel<CT, D><<<dim3(qtiles, ns), kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc,
+                                                                          a.C * D, nullptr, 0, 0, nullptr, s0));
+  });
 
   FwdParams P{};
   P.q = convert ? static_cast<const void*>(qc) : a.q;

@@ -29,6 +29,15 @@ int check_variant(const Variant& v, int head_dim);
 
 inline size_t align_up(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
 
+// Kernels that put the slice index on grid y (limited to 65535 blocks) are
+// launched once per batch of slices: f(first slice, slices in the batch).
+constexpr int64_t kMaxGridY = 65535;
+template <typename F>
+inline void slice_batches(int64_t n, F&& f) {
+  for (int64_t s0 = 0; s0 < n; s0 += kMaxGridY)
+    f(s0, static_cast<unsigned>(n - s0 < kMaxGridY ? n - s0 : kMaxGridY));
+}
+
 // Brackets one kernel launch with hipEvents on `stream` while kernel timing
 // is enabled (dil_timing_enable); a no-op otherwise.  `name` must be a string
 // literal: it is kept until the timing is read.

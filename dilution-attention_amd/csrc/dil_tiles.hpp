@@ -31,15 +31,16 @@ __host__ __device__ inline int64_t tmajor_index(int64_t t, int d, int D) {
 // Rows of `src` (storage dtype dt) in the compute type CT, optionally scaled
 // per row by rscale[(slice, row)] (in fp32, before the rounding to CT): a
 // row-major copy into dst and/or a tile-major transposed copy (rows_pad rows,
-// slice stride t_sn) into dst_t, zero-padded past `rows`.
+// slice stride t_sn) into dst_t, zero-padded past `rows`.  Grid: (row tiles
+// of 64, slices from slice0).
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__ src, int64_t src_sn,
                                                         int dt, int64_t rows, CT* __restrict__ dst,
                                                         int64_t dst_sn, CT* __restrict__ dst_t,
                                                         int64_t t_sn, int64_t rows_pad,
-                                                        const float* __restrict__ rscale) {
+                                                        const float* __restrict__ rscale, int64_t slice0) {
   __shared__ float tile[64][D + 1];
-  const int64_t slice = blockIdx.y;
+  const int64_t slice = slice0 + blockIdx.y;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
   constexpr int kVecPerRow = D / 8;
   for (int idx = threadIdx.x; idx < 64 * kVecPerRow; idx += kThreads) {
