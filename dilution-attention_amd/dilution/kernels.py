@@ -85,6 +85,26 @@ def _check_device(*ts: torch.Tensor) -> None:
             raise RuntimeError("dilution HIP kernels need tensors on the GPU (no CPU path)")
 
 
+def _check_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 committed: torch.Tensor) -> int:
+    """Shapes of a decode / prefill call against its cache (kernels.py:1003-1021):
+    contiguous (B, H, capacity, D) K and V, a contiguous (B, H, capacity) fp32
+    demand, q of the same (B, H, ., D).  Returns the capacity."""
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must both be (B, H, capacity, D)")
+    batch, heads, capacity, head_dim = k_cache.shape
+    if q.dim() != 4 or (q.shape[0], q.shape[1], q.shape[3]) != (batch, heads, head_dim):
+        raise ValueError(f"queries {tuple(q.shape)} do not match the cache {tuple(k_cache.shape)}")
+    if tuple(committed.shape) != (batch, heads, capacity):
+        raise ValueError(f"committed must be (B, H, capacity) = {(batch, heads, capacity)}, "
+                         f"got {tuple(committed.shape)}")
+    if committed.dtype != torch.float32:
+        raise ValueError("committed must be float32")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous() and committed.is_contiguous()):
+        raise ValueError("k_cache, v_cache and committed must be contiguous")
+    return capacity
+
+
 def _check_head_dim(head_dim: int) -> None:
     if head_dim & (head_dim - 1):
         raise ValueError("head_dim must be a power of two")
@@ -310,15 +330,13 @@ def dilution_prefill_chunk(
     its ``aux["committed_total"]``.
     """
     prec = _precision_code(dot_precision)
-    lib = _hip.lib()
-    _check_device(q, k_cache, v_cache, committed)
+    capacity = _check_cache(q, k_cache, v_cache, committed)
     batch, heads, chunk, head_dim = q.shape
     _check_head_dim(head_dim)
-    capacity = k_cache.shape[2]
     if start < 0 or start + chunk > capacity:
         raise ValueError(f"rows [{start}, {start + chunk}) outside cache capacity {capacity}")
-    if committed.dtype != torch.float32:
-        raise ValueError("committed must be float32")
+    _check_device(q, k_cache, v_cache, committed)
+    lib = _hip.lib()
     n = batch * heads
     dt = k_cache.dtype if k_cache.dtype in _DTYPES else torch.float32
     if v_cache.dtype != dt or k_cache.dtype != dt:
@@ -372,19 +390,17 @@ def dilution_decode_step(
     must be zero).  It is advanced in place to include this row; positions
     >= length are never touched.
     """
-    lib = _hip.lib()
     batch, heads, one, head_dim = q1.shape
     if one != 1:
         raise ValueError("decode step takes exactly one query row per (batch, head)")
     if head_dim & (head_dim - 1):
         raise ValueError("head_dim must be a power of two")
-    capacity = k_cache.shape[2]
+    capacity = _check_cache(q1, k_cache, v_cache, committed)
     if not 1 <= length <= capacity:
         raise ValueError(f"length {length} outside cache capacity {capacity}")
     _check_head_dim(head_dim)
     _check_device(q1, k_cache, v_cache, committed)
-    if committed.dtype != torch.float32:
-        raise ValueError("committed must be float32")
+    lib = _hip.lib()
     n = batch * heads
     dt = k_cache.dtype if k_cache.dtype in _DTYPES else torch.float32
     if v_cache.dtype != dt or k_cache.dtype != dt:

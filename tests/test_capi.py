@@ -81,3 +81,32 @@ def test_python_layer_raises_without_gpu_tensors():
         kernels.dilution_attention_forward(x, x, x)
     with pytest.raises(ValueError):
         kernels.dilution_attention_forward(x, x, x, dot_precision="fp16")
+
+
+def test_cache_shape_errors_before_any_launch():
+    """Decode / prefill reject caches that do not match the queries, a demand
+    of the wrong shape or dtype, and non-contiguous buffers (kernels.py:1003-1021)
+    with ValueError, before touching the device."""
+    import torch
+    from dilution import kernels
+
+    b, h, cap, d = 2, 3, 16, 64
+    q1 = torch.zeros(b, h, 1, d)
+    kc = torch.zeros(b, h, cap, d)
+    com = torch.zeros(b, h, cap)
+    cases = [
+        (q1, kc, torch.zeros(b, h, cap + 1, d), com),                    # V shape differs
+        (torch.zeros(b, h + 1, 1, d), kc, kc, com),                       # heads differ
+        (q1, kc, kc, torch.zeros(b, h, cap - 1)),                         # demand too short
+        (q1, kc, kc, com.double()),                                       # demand not fp32
+        (q1, kc.transpose(1, 2).contiguous().transpose(1, 2), kc, com),  # K not contiguous
+    ]
+    for q, k, v, c in cases:
+        with pytest.raises(ValueError):
+            kernels.dilution_decode_step(q, k, v, c, 4)
+    with pytest.raises(ValueError):
+        kernels.dilution_decode_step(q1, kc, kc, com, cap + 1)             # past capacity
+    with pytest.raises(ValueError):
+        kernels.dilution_prefill_chunk(torch.zeros(b, h, 8, d), kc, kc, com, 12)   # rows past capacity
+    with pytest.raises(RuntimeError):
+        kernels.dilution_decode_step(q1, kc, kc, com, 4)                    # valid, but no GPU tensors
