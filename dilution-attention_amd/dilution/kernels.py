@@ -169,10 +169,13 @@ def dilution_attention_forward(
     identical.
     """
     prec = _precision_code(dot_precision)
-    lib = _hip.lib()
-    _check_device(q, k, v)
+    if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q, k, v must share one (B, H, T, D) shape, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
     batch, heads, seq, head_dim = q.shape
     _check_head_dim(head_dim)
+    _check_device(q, k, v)
+    lib = _hip.lib()
     n = batch * heads
     dt = _common_dtype(q, k, v)
     qf, kf, vf = (_rows(x, n, seq, head_dim, dt) for x in (q, k, v))

@@ -81,6 +81,10 @@ def test_python_layer_raises_without_gpu_tensors():
         kernels.dilution_attention_forward(x, x, x)
     with pytest.raises(ValueError):
         kernels.dilution_attention_forward(x, x, x, dot_precision="fp16")
+    with pytest.raises(ValueError):
+        kernels.dilution_attention_forward(x, torch.zeros(1, 1, 5, 64), x)      # k of another length
+    with pytest.raises(ValueError):
+        kernels.dilution_attention_forward(x, x, torch.zeros(1, 1, 4, 32))      # v of another width
 
 
 def test_cache_shape_errors_before_any_launch():
