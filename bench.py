@@ -11,7 +11,8 @@ T=16384 d=64 bf16 with q,k ~ 0.5 N(0,1), v, dO ~ N(0,1), inputs resident in
 HBM before the timed region.  ``value`` is algorithmic TFLOP/s, 7 B H T^2 d
 per step (the causal flash-attention fwd+bwd count: forward 2 products,
 backward 5 including one recompute), over K steps bracketed by
-torch.cuda.synchronize().
+torch.cuda.synchronize(); ``ms_per_step_median`` is the median of the same K
+steps timed one by one with HIP events in a second pass.
 
 The same line carries
   * ``roofline`` for the step's dominant kernel: its algorithmic FLOPs per
@@ -164,6 +165,23 @@ def timed(step, steps: int) -> float:
     return max(start.elapsed_time(stop) / steps, wall)
 
 
+def step_median(step, steps: int) -> float:
+    """Median milliseconds of one step over `steps` calls, each bracketed by
+    its own pair of events on the current stream."""
+    import statistics
+
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record()
+        step()
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
 def kernel_pass(step, steps: int) -> dict:
     """Per-kernel {name: (launches, total_ms)} over `steps` calls."""
     import torch
@@ -195,6 +213,7 @@ def bench_training(args, dev):
         step()
     ms = timed(step, args.steps)
     log(f"{args.workload}: {args.steps} timed steps, {ms:.3f} ms/step")
+    med = step_median(step, args.steps)
     per = kernel_pass(step, args.steps)
 
     unit = batch * heads * seq * seq * d            # one causal product: B H T^2 d FLOPs
@@ -213,7 +232,7 @@ def bench_training(args, dev):
             "algorithmic_flops_per_launch": dom_flops, "avg_launch_ms": round(dom_ms, 4),
             "note": "per-kernel durations from HIP events in a second pass of the same steps; "
                     "traffic from profiles/hbm_traffic.json"}
-    return dict(ms=ms, value=flops / (ms * 1e-3) / 1e12, roofline=roof, kernels=kernels_out,
+    return dict(ms=ms, ms_median=med, value=flops / (ms * 1e-3) / 1e12, roofline=roof, kernels=kernels_out,
                 shape=(batch, heads, seq, d), inputs=(q, k, v, do))
 
 
@@ -544,6 +563,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(tr["ms"], 4),
+        "ms_per_step_median": round(tr["ms_median"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
