@@ -65,6 +65,28 @@ def test_variant_backward_matches_autograd(bid, share, seq):
         assert rel < bound, f"{bid} {name} relative error {rel}"
 
 
+@pytest.mark.parametrize("bid", orc.BIDS)
+def test_variant_backward_bf16(bid):
+    """bf16 operands (the ablation LM's training mode): gradients against the
+    fp64 autograd oracle on the bf16-rounded inputs, relative to the largest
+    gradient as in the fp32 variant test (minshift's gradients carry the
+    1/eps-scale terms of a zero bid on an undemanded key): 1e-2, relu2 2.5e-2
+    (the reference's 2.5x relu2 relaxation)."""
+    from dilution import kernels_bid as kb
+
+    q, k, v, do = (x.to(torch.bfloat16) for x in orc.make_inputs((1, 4, 200, 64), seed=41, qk_scale=0.5,
+                                                                  with_dout=True))
+    ref = [x.double().requires_grad_(True) for x in (q, k, v)]
+    orc.variant_attention_f64(*ref, bid, True, SHIFT).backward(do.double())
+    xs = [x.cuda().requires_grad_(True) for x in (q, k, v)]
+    kb.dilution_attention(*xs, dot_precision="bf16", bid=bid, shift=SHIFT).backward(do.cuda())
+    bound = 2.5e-2 if bid == "relu2" else 1e-2
+    for name, r, x in zip(("dq", "dk", "dv"), ref, xs):
+        assert x.grad.dtype == torch.bfloat16
+        rel = max_abs(x.grad, r.grad) / (r.grad.abs().max().item() + 1e-6)
+        assert rel < bound, f"{bid} {name} relative error {rel}"
+
+
 @pytest.mark.parametrize("bid", ["softmax", "relu", "sigmoid"])
 def test_variant_exclusive_backward_dv(bid):
     """The exclusive share's dq/dk are fp32 noise on cancelling 1e9-scale terms
