@@ -84,3 +84,37 @@ def test_chunked_and_one_call_prefill_agree():
     assert max_abs(y1, y2) < 1e-5
     assert max_abs(c1["committed"], c2["committed"]) < 1e-5
     assert torch.equal(c1["k"], c2["k"]) and torch.equal(c1["v"], c2["v"])
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_unwritten_cache_positions_are_never_read():
+    """Cache rows past what is written (prefill: past start + C; decode: past
+    length) and the demand past length hold NaN: outputs and demand are
+    bit-identical to a clean cache, and the poisoned tail is left as it was
+    (the reference's future-triangle poisoning, test_kernels.py:19-43)."""
+    from dilution import kernels
+
+    b, h, d, cap, chunk = 2, 3, 64, 96, 40
+    q, k, v = (t.cuda() for t in orc.make_inputs((b, h, cap, d), seed=51))
+    outs = []
+    for poison in (False, True):
+        kc, vc = torch.zeros_like(k), torch.zeros_like(v)
+        com = torch.zeros(b, h, cap, device="cuda")
+        if poison:
+            kc.fill_(float("nan"))
+            vc.fill_(float("nan"))
+            com[..., chunk:] = float("nan")
+        kc[:, :, :chunk] = k[:, :, :chunk]
+        vc[:, :, :chunk] = v[:, :, :chunk]
+        y = kernels.dilution_prefill_chunk(q[:, :, :chunk], kc, vc, com, 0, dot_precision="ieee")
+        t = chunk + 1
+        kc[:, :, t - 1] = k[:, :, t - 1]
+        vc[:, :, t - 1] = v[:, :, t - 1]
+        com[..., t - 1] = 0.0
+        y1 = kernels.dilution_decode_step(q[:, :, t - 1:t].contiguous(), kc, vc, com, t)
+        outs.append((y, y1, com.clone()))
+    (y0, d0, c0), (y1, d1, c1) = outs
+    assert torch.equal(y0, y1) and torch.equal(d0, d1)
+    assert torch.equal(c0[..., :chunk + 1], c1[..., :chunk + 1])
+    assert torch.isnan(c1[..., chunk + 1:]).all()

@@ -58,6 +58,21 @@ def test_config_validation():
     assert not LMConfig(d_model=256, n_heads=4, share_cumsum=False).production_operator()
 
 
+def test_dilution_operator_is_parameter_free():
+    """The dilution slot holds exactly the softmax control's parameters
+    (test_model.py:184-195): the order asymmetry comes from the cumsum alone."""
+    from dilution.lm import DilutionLM, LMConfig
+
+    def count(kind):
+        cfg = LMConfig(vocab_size=97, n_layers=2, d_model=64, n_heads=4, attention=kind)
+        return sum(p.numel() for p in DilutionLM(cfg).parameters())
+
+    assert count("dilution") == count("softmax")
+    cfg = LMConfig(vocab_size=97, n_layers=1, d_model=64, n_heads=4)
+    names = {n for n, _ in DilutionLM(cfg).h[0].attn.named_parameters()}
+    assert names == {"c_attn.weight", "c_proj.weight"}, names
+
+
 @pytest.mark.gpu
 @needs_gpu
 @pytest.mark.parametrize("kinds", [None, ["softmax", "dilution"]])
@@ -142,7 +157,7 @@ def test_variant_model_matches_torch_specification(bid, monkeypatch):
 @pytest.mark.gpu
 @needs_gpu
 @pytest.mark.parametrize("bid,share", [("relu2", True), ("minshift", "exclusive"), ("sigshift", False),
-                                       ("expshift", True)])
+                                       ("expshift", True), ("softmax", "exclusive"), ("softmax", False)])
 def test_variant_cached_decode_matches_full_forward(bid, share):
     model = _small(kinds=["dilution", "softmax"], bid=bid, share_cumsum=share)
     g = torch.Generator().manual_seed(8)
