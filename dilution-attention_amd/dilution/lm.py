@@ -20,7 +20,11 @@ weights).  It follows the reference's module layout and cache protocol
 * ``Block``: pre-norm residual attention + MLP (model.py:317-339);
 * ``DilutionLM``: embedding tied to the LM head, blocks, final norm;
   ``forward(idx, targets)`` -> (logits, loss), ``prefill``, ``decode_step``
-  and greedy ``generate`` (model.py:342-512).
+  and cached greedy / sampled ``generate`` (model.py:342-512, sampling with
+  ``filter_logits``, model.py:289-304);
+* ``continuation_nll``: per-token NLL of continuations given their prompts
+  from one causal forward (sampling.py:297-323), the scoring caller of the
+  operator.
 
 The reference normalises with LayerNorm and sizes SwiGLU at 8/3 d_model; the
 model-level benchmark configuration asks for RMSNorm and a 4x SwiGLU, which
@@ -240,11 +244,18 @@ class DilutionLM(nn.Module):
         if isinstance(module, (nn.Linear, nn.Embedding)):
             nn.init.normal_(module.weight, mean=0.0, std=0.02)
 
-    def forward(self, idx: torch.Tensor, targets: torch.Tensor | None = None):
+    def num_parameters(self) -> int:
+        return sum(p.numel() for p in self.parameters())
+
+    def hidden_states(self, idx: torch.Tensor) -> torch.Tensor:
+        """Final-norm hidden states (B, T, d_model) of one causal forward."""
         x = self.wte(idx)
         for block in self.h:
             x = block(x)
-        x = self.ln_f(x)
+        return self.ln_f(x)
+
+    def forward(self, idx: torch.Tensor, targets: torch.Tensor | None = None):
+        x = self.hidden_states(idx)
         if targets is None:
             return self.lm_head(x[:, [-1], :]), None
         logits = self.lm_head(x)
@@ -269,14 +280,73 @@ class DilutionLM(nn.Module):
         return self.lm_head(self.ln_f(x))
 
     @torch.no_grad()
-    def generate(self, idx: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
-        """Greedy decoding with caches sized prompt + max_new_tokens
-        (model.py:496)."""
+    def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 0.0,
+                 top_k: int | None = None, top_p: float | None = None,
+                 generator: torch.Generator | None = None, vocab_limit: int | None = None) -> torch.Tensor:
+        """Cached generation with caches sized prompt + max_new_tokens
+        (model.py:473-509): temperature 0 is greedy, otherwise a sample of
+        softmax(logits / temperature) after top-k / nucleus truncation;
+        ``generator`` makes sampling reproducible, ``vocab_limit`` keeps the
+        new tokens below that id."""
+        if vocab_limit is not None and not 0 < vocab_limit <= self.cfg.vocab_size:
+            raise ValueError(f"vocab_limit must be in (0, {self.cfg.vocab_size}]")
         logits, caches = self.prefill(idx, capacity=idx.shape[1] + max_new_tokens)
         tokens = idx
         for step in range(max_new_tokens):
-            nxt = logits[:, -1, :].float().argmax(dim=-1, keepdim=True)
+            last = logits[:, -1, :].float()
+            if vocab_limit is not None:
+                last[:, vocab_limit:] = float("-inf")
+            if temperature and temperature > 0.0:
+                probs = filter_logits(last / temperature, top_k=top_k, top_p=top_p).softmax(dim=-1)
+                nxt = torch.multinomial(probs, 1, generator=generator)
+            else:
+                nxt = last.argmax(dim=-1, keepdim=True)
             tokens = torch.cat([tokens, nxt], dim=1)
             if step + 1 < max_new_tokens:
                 logits = self.decode_step(nxt, caches)
         return tokens
+
+
+def filter_logits(logits: torch.Tensor, top_k: int | None = None, top_p: float | None = None) -> torch.Tensor:
+    """Top-k, then nucleus (top-p) truncation of (..., vocab) logits; the
+    dropped entries become -inf.  The nucleus is the shortest run of the most
+    likely tokens whose probability reaches top_p; the most likely token always
+    stays (model.py:289-304)."""
+    out = logits
+    if top_k is not None and top_k > 0:
+        floor = out.topk(min(int(top_k), out.shape[-1]), dim=-1).values[..., -1:]
+        out = out.masked_fill(out < floor, float("-inf"))
+    if top_p is not None and top_p < 1.0:
+        vals, order = out.sort(dim=-1, descending=True)
+        probs = vals.softmax(dim=-1)
+        mass_before = probs.cumsum(dim=-1) - probs
+        vals = vals.masked_fill(mass_before >= top_p, float("-inf"))
+        out = torch.empty_like(out).scatter_(-1, order, vals)
+    return out
+
+
+@torch.no_grad()
+def continuation_nll(model: DilutionLM, prompts: torch.Tensor, conts) -> list[float]:
+    """Mean per-token NLL (nats) of each continuation given its prompt
+    (sampling.py:297-323): prompts (B, L) share one length, conts are token
+    lists (ragged).  One causal forward over prompt + continuation; the LM
+    head runs on the positions that predict continuation tokens only.  Rows
+    are padded after their continuation, which causal attention never lets
+    reach a scored position; an empty continuation scores NaN."""
+    batch, length = prompts.shape
+    width = max(1, max(len(c) for c in conts))
+    idx = torch.zeros(batch, length + width, dtype=torch.long, device=prompts.device)
+    idx[:, :length] = prompts
+    tgt = torch.full((batch, width), -100, dtype=torch.long, device=prompts.device)
+    for r, c in enumerate(conts):
+        c = torch.as_tensor(list(c), dtype=torch.long, device=prompts.device)
+        idx[r, length:length + len(c)] = c
+        tgt[r, :len(c)] = c
+    h = model.hidden_states(idx)[:, length - 1:length - 1 + width]
+    logits = model.lm_head(h).float()
+    nll = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), tgt.reshape(-1), ignore_index=-100,
+                          reduction="none").view(batch, width)
+    valid = (tgt != -100).float()
+    counts = valid.sum(-1)
+    per_row = (nll * valid).sum(-1) / counts.clamp(min=1)
+    return [float(v) if n > 0 else float("nan") for v, n in zip(per_row.tolist(), counts.tolist())]

@@ -183,3 +183,57 @@ def test_variant_training_step_bf16_finite():
     assert torch.isfinite(loss)
     for name, p in model.named_parameters():
         assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name
+
+
+def test_filter_logits():
+    """Top-k keeps the k largest; the nucleus keeps the shortest most-likely
+    prefix reaching top_p; the arg-max always survives."""
+    from dilution.lm import filter_logits
+
+    logits = torch.log(torch.tensor([[0.5, 0.2, 0.15, 0.1, 0.05]]))
+    kept = lambda out: torch.isfinite(out[0]).nonzero().flatten().tolist()
+    assert kept(filter_logits(logits, top_k=2)) == [0, 1]
+    assert kept(filter_logits(logits, top_p=0.6)) == [0, 1]        # 0.5 < 0.6 <= 0.7
+    assert kept(filter_logits(logits, top_p=0.69)) == [0, 1]       # mass before token 2 is 0.7
+    assert kept(filter_logits(logits, top_p=0.01)) == [0]
+    assert kept(filter_logits(logits[:, [3, 0, 4, 1, 2]], top_p=0.8)) == [1, 3, 4]   # order-independent
+    assert kept(filter_logits(logits, top_k=4, top_p=0.99)) == [0, 1, 2, 3]
+    assert torch.equal(filter_logits(logits), logits)
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_generate_sampling():
+    model = _small()
+    idx = torch.zeros(2, 5, dtype=torch.long, device="cuda")
+    greedy = model.generate(idx, 6)
+    assert torch.equal(model.generate(idx, 6, temperature=1.0, top_k=1), greedy)
+    draw = lambda seed: model.generate(idx, 6, temperature=1.3, top_p=0.9,
+                                       generator=torch.Generator(device="cuda").manual_seed(seed))
+    assert torch.equal(draw(3), draw(3))
+    limited = model.generate(idx, 8, temperature=2.0, vocab_limit=10,
+                             generator=torch.Generator(device="cuda").manual_seed(4))
+    assert (limited[:, 5:] < 10).all()
+    with pytest.raises(ValueError):
+        model.generate(idx, 2, vocab_limit=0)
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_continuation_nll_matches_full_forward():
+    from dilution.lm import continuation_nll
+
+    model = _small()
+    g = torch.Generator().manual_seed(6)
+    prompts = torch.randint(1, 97, (3, 20), generator=g).cuda()
+    conts = [[5, 9, 11, 2], [7], []]
+    got = continuation_nll(model, prompts, conts)
+    for r, c in enumerate(conts):
+        if not c:
+            assert got[r] != got[r]                                   # NaN
+            continue
+        seq = torch.cat([prompts[r], torch.tensor(c, device="cuda")])[None]
+        with torch.no_grad():
+            logits, _ = model(seq[:, :-1], seq[:, 1:])
+        want = torch.nn.functional.cross_entropy(logits[0, -len(c):].float(), seq[0, -len(c):])
+        assert abs(got[r] - want.item()) < 1e-4, r
