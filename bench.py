@@ -536,7 +536,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the dilution-attention "
-              "path here runs on a single MI355X, see DESIGN.md for how it would shard",
+              "operator path is built and measured on a single MI355X",
               file=sys.stderr)
         return 2
     import torch

@@ -450,7 +450,7 @@ def variant_attention_loops(q, k, v, bid: str = "softmax", share=True, shift: fl
 
 
 # ---------------------------------------------------------------------------
-# deterministic synthetic inputs (CPU RNG)
+# deterministic synthetic inputs (CPU RNG, so every device sees the same values)
 
 
 def make_inputs(shape, seed: int, qk_scale: float = 1.0, with_dout: bool = False,
