@@ -112,18 +112,40 @@ __global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, i
 }
 
 // (ghat * q)^T in the compute type from the tile-major transposed copy Q^T
-// (n, t_pad rows), whose padding rows are zero.  One workgroup per 32-row tile.
+// (n, t_pad rows), whose padding rows are zero.  One workgroup per 32-row
+// tile; each thread scales 8 consecutive elements (8 rows of one column) with
+// one 16-byte load and store.
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ qt,
                                                         const float* __restrict__ ghat, int64_t T,
                                                         int64_t t_pad, CT* __restrict__ dst, int64_t slice0) {
+  __shared__ float g_s[32];
   const int64_t slice = slice0 + blockIdx.y;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 32;
   const int64_t base = slice * D * t_pad + row0 * D;
-  for (int e = threadIdx.x; e < 32 * D; e += kThreads) {
-    const int64_t row = row0 + (e & 31);
-    const float gr = row < T ? ghat[slice * T + row] : 0.f;
-    dst[base + e] = static_cast<CT>(static_cast<float>(qt[base + e]) * gr);
+  if (threadIdx.x < 32) {
+    const int64_t row = row0 + threadIdx.x;
+    g_s[threadIdx.x] = row < T ? ghat[slice * T + row] : 0.f;
+  }
+  __syncthreads();
+  for (int e8 = threadIdx.x * 8; e8 < 32 * D; e8 += kThreads * 8) {
+    float v[8];
+    if constexpr (sizeof(CT) == 2) {
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qt + base + e8);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = static_cast<float>(x[k]);
+    } else {
+      const floatx4* p = reinterpret_cast<const floatx4*>(qt + base + e8);
+      const floatx4 a = p[0], b = p[1];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = a[k];
+        v[4 + k] = b[k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] *= g_s[(e8 & 31) + k];
+    store8<CT>(dst + base + e8, v);
   }
 }
 

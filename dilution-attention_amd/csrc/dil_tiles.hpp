@@ -28,11 +28,27 @@ __host__ __device__ inline int64_t tmajor_index(int64_t t, int d, int D) {
   return ((t >> 5) * D + d) * 32 + (t & 31);
 }
 
+// Store 8 fp32 values as 8 consecutive CT elements (one 16-byte store for
+// bf16, rounded to nearest even; two for fp32).  dst is 16-byte aligned.
+template <typename CT>
+__device__ __forceinline__ void store8(CT* dst, const float (&v)[8]) {
+  if constexpr (sizeof(CT) == 2) {
+    *reinterpret_cast<bf16x8*>(dst) = Mma<__bf16>::pack(v);
+  } else {
+    const floatx4 a = {v[0], v[1], v[2], v[3]}, b = {v[4], v[5], v[6], v[7]};
+    reinterpret_cast<floatx4*>(dst)[0] = a;
+    reinterpret_cast<floatx4*>(dst)[1] = b;
+  }
+}
+
 // Rows of `src` (storage dtype dt) in the compute type CT, optionally scaled
 // per row by rscale[(slice, row)] (in fp32, before the rounding to CT): a
 // row-major copy into dst and/or a tile-major transposed copy (rows_pad rows,
-// slice stride t_sn) into dst_t, zero-padded past `rows`.  Grid: (row tiles
-// of 64, slices from slice0).
+// a multiple of 64; slice stride t_sn) into dst_t, zero-padded past `rows`.
+// Grid: (row tiles of 64, slices from slice0).  Every thread stores 16-byte
+// runs: 8 columns of a row in the row-major copy, 8 rows of a column in the
+// transposed one (contiguous there, and consecutive threads continue the run
+// through the 32 x D block of a 32-row tile).
 template <typename CT, int D>
 __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__ src, int64_t src_sn,
                                                         int dt, int64_t rows, CT* __restrict__ dst,
@@ -59,15 +75,26 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__
   }
   __syncthreads();
   if (dst != nullptr) {
-    for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
-      const int r = idx / D, c = idx % D;
-      if (r0 + r < rows) dst[slice * dst_sn + (r0 + r) * D + c] = static_cast<CT>(tile[r][c]);
+    for (int idx = threadIdx.x; idx < 64 * kVecPerRow; idx += kThreads) {
+      const int r = idx / kVecPerRow, c8 = (idx % kVecPerRow) * 8;
+      if (r0 + r < rows) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tile[r][c8 + e];
+        store8<CT>(dst + slice * dst_sn + (r0 + r) * D + c8, v);
+      }
     }
   }
   if (dst_t != nullptr) {
-    for (int idx = threadIdx.x; idx < 64 * D; idx += kThreads) {
-      const int c = idx / 64, r = idx % 64;
-      if (r0 + r < rows_pad) dst_t[slice * t_sn + tmajor_index(r0 + r, c, D)] = static_cast<CT>(tile[r][c]);
+    // item idx: 32-row half b, column c, rows r8 .. r8 + 7 of that half
+    for (int idx = threadIdx.x; idx < 8 * D; idx += kThreads) {
+      const int b = idx / (4 * D), c = (idx % (4 * D)) >> 2, r8 = 32 * b + (idx & 3) * 8;
+      if (r0 + r8 < rows_pad) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tile[r8 + e][c];
+        store8<CT>(dst_t + slice * t_sn + tmajor_index(r0 + r8, c, D), v);
+      }
     }
   }
 }
