@@ -62,6 +62,9 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 WORKLOADS = {
     "train16k": (1, 16, 16384, 64),
     "train2k": (8, 16, 2048, 64),
+    # the same 262144 tokens per step at intermediate lengths
+    "train4k": (4, 16, 4096, 64),
+    "train8k": (2, 16, 8192, 64),
 }
 
 # Algorithmic products (each B H T^2 d FLOPs causal) that each kernel of the

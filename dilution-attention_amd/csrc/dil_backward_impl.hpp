@@ -25,8 +25,9 @@
 //   bwd_query   one wave per 32-row tile over its causal key tiles: the same
 //               chain with G from the checkpoints; (p dp) transposed by an
 //               identity MFMA so dq += (p dp) K runs with queries in lanes,
-//               ghat (the row sums of p dp) riding on it as a ones column;
-//               dq = s dq_main - ghat pk.
+//               and ghat (the row sums of p dp) summed from the transposed
+//               registers; dq = s dq_main - ghat pk.  bf16 up to head_dim 64
+//               keeps dO' and the identity in LDS: three workgroups per CU.
 //   prep_ghat_q (ghat * Q)^T tiles for the correction.
 //   bwd_dkcorr  one wave per key tile: dk = s dk_main - s sum_i p_ij (ghat_i q_i).
 #pragma once
@@ -202,6 +203,28 @@ constexpr int bwd_occupancy() {
   return (sizeof(CT) == 2 && D <= 64) ? 2 : 1;
 }
 
+// bwd_query's parked form keeps its dO' operands and the transpose identity
+// in LDS and sums ghat on the VALU, which leaves room for three workgroups per
+// CU (<= 168 VGPRs, 48 KB of LDS each) with bf16 operands up to head_dim 64.
+// It pays where the sweeps are short (T <= kParkMaxT: -10% at T = 2048, -3% at
+// 4096); at longer T the register form (ones-column MFMA for ghat, two
+// workgroups per CU) is as fast or faster, so it runs there.
+template <typename CT, int D>
+constexpr bool query_parks() {
+  return sizeof(CT) == 2 && D <= 64;
+}
+constexpr int64_t kParkMaxT = 4096;
+
+// Sum of 16 values as a depth-4 tree.
+__device__ __forceinline__ float sum16(const float (&v)[16]) {
+  float a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) a[k] = v[k] + v[k + 8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] += a[k + 4];
+  return (a[0] + a[2]) + (a[1] + a[3]);
+}
+
 // ---------------------------------------------------------------------------
 // key-parallel reverse pass: dv, dk_main, suffix checkpoints
 
@@ -255,7 +278,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
 
   // a stage: the Q and dO' row tiles, their transposes, the row statistics and
   // the demand checkpoints of the workgroup's 128 keys entering the tile
-  KTileLoader<CT, D, true, true> ql, dl;        // row tiles in query-split slot order
+  KTileLoader<CT, D, true> ql, dl;        // row tiles in query-split slot order
   TTileLoader<CT, D> qtl, dtl;
   RowStatsLoader<kNS> sl;
   if constexpr (!bid_log2<BID>()) sl.pad0 = 0.f;
@@ -428,21 +451,35 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
 // ---------------------------------------------------------------------------
 // row-parallel dq pass
 
-template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
-__global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(BwdParams P) {
+template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL, bool PARK = false>
+__global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd_occupancy<CT, D>())) void bwd_query(
+    BwdParams P) {
   using TL = Tiles<CT, D>;
+  using Frag = typename Mma<CT>::frag;
   constexpr int kNS = BID == BID_SOFTMAX ? 2 : 3;                // per-row statistics staged
+  constexpr bool kPark = PARK && query_parks<CT, D>();
+  constexpr int kSteps = kTileK / Mma<CT>::kStep;
+  constexpr int kFS = RowFrag<CT, D>::kSteps;
   __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) float rs_s[4][kNS * kTileQ];   // per wave: lse (r0), -dbs, r1
   __shared__ float g_s[4][kTileQ];
+  // parked operands, lane-minor so that one fragment read is conflict-free:
+  // each wave's dO' row fragments, and the identity of the transposes
+  __shared__ __attribute__((aligned(16))) Frag do_park[kPark ? 4 : 1][kPark ? kFS : 1][64];
+  __shared__ __attribute__((aligned(16))) Frag id_park[kPark ? kSteps : 1][64];
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int g = item.idx;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  // The plain wave index, deliberately: stated uniform (readfirstlane), it
+  // turns the choice between the off-diagonal and the diagonal step into
+  // scalar branches, and the compiler then copied the dq accumulators at
+  // every step instead of keeping them in place.
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const float hf = static_cast<float>(h);
   const int qt = g * 4 + wave;
   const int64_t r0 = static_cast<int64_t>(qt) * kTileQ;
@@ -471,22 +508,50 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     rs_s[wave][kTileQ + l32] = ok ? -P.dbs[slice * P.T + r] : 0.f;
     if constexpr (kNS == 3) rs_s[wave][2 * kTileQ + l32] = ok ? P.rb1[slice * P.T + r] : 0.f;
   }
-  constexpr int kSteps = kTileK / Mma<CT>::kStep;
-  typename Mma<CT>::frag ident[kSteps];
+  Frag ident[kSteps];
+  if constexpr (kPark) {
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) ident[s] = ident_qs<CT>(l32, h, s);
+    for (int s = 0; s < kFS; ++s) do_park[wave][s][lane] = dof.f[s];
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) ident[s] = ident_qs<CT>(l32, h, s);
+  }
+  auto ident_at = [&](int s) -> Frag {
+    if constexpr (kPark) return id_park[s][lane];
+    else return ident[s];
+  };
   floatx16 dqa[kDTiles<D>];
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) dqa[t] = floatx16{};
-  // ghat rides on the dq products as a ones column: column 0 of this tile
+  // ghat, parked form: this lane's share of the row sums of p dp, query
+  // r0 + l32 over the keys that the transposed tile holds in this half.
+  // Register form: ghat rides on the dq products as a ones column (column 0
+  // of gacc).
+  float gsum = 0.f;
   floatx16 gacc = floatx16{};
   const auto ones = ones_col_frag<CT>(l32);
+  // demand and suffix checkpoints of this lane's key, loaded one key tile
+  // ahead (steps past the wave's causal range never use them).  Parked form:
+  // through resources that end at the row's last key (keys past T read 0; a
+  // row tile past T has no checkpoint row and reads only zeros).  Register
+  // form: guarded plain loads, as its tiles (measured faster there).
   const float* crow = P.carry + (slice * P.nb + qt) * P.T;
   const float* srow = P.sufk + (slice * P.nb + qt) * P.T;
-  // demand and suffix checkpoints of this lane's key, loaded one key tile ahead
-  auto ckpt_at = [&](int kt, const float* row) -> float {
-    const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
-    return (kt < nkt_w && key < P.T) ? row[key] : 0.f;
+  const int64_t ck_bytes = r0 < P.T ? P.T * 4 : 0;
+  const auto crs = make_rsrc(crow, ck_bytes);
+  const auto srs = make_rsrc(srow, ck_bytes);
+  const uint32_t koff = static_cast<uint32_t>(rho(l32) * 4);
+  auto ckpt_at = [&](int kt, bool suffix) -> float {
+    if constexpr (kPark) {
+      return buffer_load_f32(suffix ? srs : crs, static_cast<uint32_t>(kt * kTileK * 4) + koff, 0);
+    } else {
+      const int64_t key = static_cast<int64_t>(kt) * kTileK + rho(l32);
+      return (kt < nkt_w && key < P.T) ? (suffix ? srow : crow)[key] : 0.f;
+    }
   };
 
   auto step = [&](int kt, int buf, float cin, float sin, auto diag_tag) {
@@ -500,7 +565,15 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
     // and runs under the p / demand chain
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
+    floatx16 dov;
+    if constexpr (kPark) {
+      RowFrag<CT, D> dop;
+#pragma unroll
+      for (int s = 0; s < kFS; ++s) dop.f[s] = do_park[wave][s][lane];
+      dov = mma_rows<CT, D>(dop, vf, as_x16(ndb));
+    } else {
+      dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
+    }
     lds_read16(st + 16 * h, lz);
     float p[16], x[16], jac[16];
     if constexpr (BID == BID_SOFTMAX) {
@@ -579,7 +652,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     // transpose the dq operand (jac dp): queries in lanes, keys (natural order) in registers
     floatx16 xt = floatx16{};
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(ds, s), ident[s], xt);
+    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(ds, s), ident_at(s), xt);
     float xv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) xv[i] = xt[i];
@@ -589,23 +662,32 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
 #pragma unroll
       for (int t = 0; t < kDTiles<D>; ++t)
         dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
-      if constexpr (bid_log2<BID>()) gacc = Mma<CT>::mma(af, ones, gacc);
+      if constexpr (!kPark && bid_log2<BID>()) gacc = Mma<CT>::mma(af, ones, gacc);
     }
+    // the transposed values are exact copies of the dq operand (bf16 operands
+    // in bf16 mode), so these are the row sums of what dq multiplies
+    if constexpr (kPark && bid_log2<BID>()) gsum += sum16(xv);
     if constexpr (!bid_log2<BID>() && bid_normalized<BID>()) {
       // ghat needs the row sums of p dp, a different operand from jac dp here
       floatx16 yt = floatx16{};
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s) yt = Mma<CT>::mma(acc_frag<CT>(x, s), ident[s], yt);
+      for (int s = 0; s < kSteps; ++s) yt = Mma<CT>::mma(acc_frag<CT>(x, s), ident_at(s), yt);
       float yv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) yv[i] = yt[i];
+      if constexpr (kPark) {
+        gsum += sum16(yv);
+      } else {
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s) gacc = Mma<CT>::mma(acc_frag<CT>(yv, s), ones, gacc);
+        for (int s = 0; s < kSteps; ++s) gacc = Mma<CT>::mma(acc_frag<CT>(yv, s), ones, gacc);
+      }
     }
   };
 
-  KTileLoader<CT, D, false> kl, vl;
-  TTileLoader<CT, D> ktl;
+  // buffer loads in the parked form; the register form skips the rows past
+  // the end (both measured best for their form)
+  KTileLoader<CT, D, false, kPark ? kLoadBuffer : kLoadSkip> kl, vl;
+  TTileLoader<CT, D, kPark ? kLoadBuffer : kLoadClamp> ktl;
   auto fetch = [&](int kt) {
     const int64_t key0 = static_cast<int64_t>(kt) * kTileK;
     kl.load(ks, key0, P.T);
@@ -617,7 +699,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     vl.store(v_s[buf]);
     ktl.store(kt_s[buf]);
   };
-  float cin_next = ckpt_at(0, crow), sin_next = ckpt_at(0, srow);
+  float cin_next = ckpt_at(0, false), sin_next = ckpt_at(0, true);
   fetch(0);
   stash(0);
   __syncthreads();
@@ -626,8 +708,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     const float cin = cin_next, sin = sin_next;
     if (kt + 1 < nkt_wg) {
       fetch(kt + 1);
-      cin_next = ckpt_at(kt + 1, crow);
-      sin_next = ckpt_at(kt + 1, srow);
+      cin_next = ckpt_at(kt + 1, false);
+      sin_next = ckpt_at(kt + 1, true);
     }
     if (kt < qt && kt < nkt_w) step(kt, buf, cin, sin, std::false_type{});
     else if (kt == qt && kt < nkt_w) step(kt, buf, cin, sin, std::true_type{});
@@ -635,9 +717,13 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_query(
     sync_lds();
   }
 
-  // ghat: column 0 of gacc, register i of half h <-> row acc_row(i, h); the
-  // elementwise bids have no row normalisation and no ghat term
-  if (l32 == 0) {
+  // ghat per query (the elementwise bids have no row normalisation and no ghat
+  // term).  Parked: the two halves' partial sums of query r0 + l32.  Register
+  // form: column 0 of gacc, register i of half h <-> row acc_row(i, h).
+  if constexpr (kPark) {
+    const HalfPair gp = halves(gsum);
+    if (h == 0) g_s[wave][l32] = bid_normalized<BID>() ? gp.lo + gp.hi : 0.f;
+  } else if (l32 == 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) g_s[wave][acc_row(i, h)] = bid_normalized<BID>() ? gacc[i] : 0.f;
   }
@@ -693,7 +779,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) dkc[t] = floatx16{};
 
-  KTileLoader<CT, D, false, true> ql;            // row tile in query-split slot order
+  KTileLoader<CT, D, true> ql;            // row tile in query-split slot order
   TTileLoader<CT, D> qtl;
   RowStatsLoader<kNS, false> sl;
   if constexpr (!bid_log2<BID>()) sl.pad0 = 0.f;
@@ -897,7 +983,14 @@ int launch_backward(const BackwardArgs& a) {
   P.kgroups = (nkt + 3) / 4;
   const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
-  DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
+  bool parked = false;
+  if constexpr (query_parks<CT, D>() && is_production<BID, SHARE>()) {
+    if (a.T <= kParkMaxT) {
+      DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, true><<<gkey, kThreads, 0, st>>>(P)));
+      parked = true;
+    }
+  }
+  if (!parked) DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, false><<<gkey, kThreads, 0, st>>>(P)));
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("prep", st,
               prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), ns), kThreads, 0, st>>>(

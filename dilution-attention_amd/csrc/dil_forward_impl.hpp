@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
     return;
   }
 
-  KTileLoader<CT, D, false> kl;
+  KTileLoader<CT, D> kl;
   TTileLoader<CT, D> tl;
 
   // ---- sweep 1: S^T = K Q^T (lane <-> query, registers <-> keys) ----
@@ -578,8 +578,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
     }
   };
 
-  KTileLoader<CT, D> kl[2];
-  TTileLoader<CT, D> vl[2];
+  KTileLoader<CT, D, false, kLoadClamp> kl[2];  // clamped global loads: measured faster here
+  TTileLoader<CT, D, kLoadClamp> vl[2];
   auto fetch = [&](int st) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {

@@ -116,53 +116,92 @@ template <typename CT> struct Vec16 { typedef floatx4 type; };
 template <> struct Vec16<__bf16> { typedef bf16x8 type; };
 
 // The tile loaders below split a copy global -> LDS into load() at the start
-// of a step and store() at its end.  Every thread issues its global loads
-// unconditionally, from addresses clamped into the slice, and the masking of
-// rows past the end happens in store(): with no branch around a load, the
+// of a step and store() at its end.  In the buffer and clamp forms every
+// thread issues its loads unconditionally: with no branch around a load the
 // compiler waits for the loads only where store() consumes them, so they
-// overlap the whole step instead of being waited for right after issue.
+// overlap the whole step.  The buffer form loads through a resource whose
+// base is the wave-uniform tile address and whose size ends at the slice's
+// last row, with a 32-bit per-lane offset: chunks past the end read as zeros
+// without touching memory, and no 64-bit per-lane address is kept or advanced
+// across the loop.  The clamp form clamps its addresses into the slice and
+// zeroes the rows past the end in store().  The skip form loads only the rows
+// inside the slice, each under its own condition.
+
+// Raw buffer resource (gfx9: stride 0, word 3 = 0x00020000) over `bytes`
+// bytes at `base`.  Both must be the same in every lane of the wave (every
+// caller passes a tile or row address shared by the workgroup or the wave);
+// readfirstlane states that to the compiler, which then builds the resource
+// in scalar registers instead of looping over the distinct per-lane values.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int64_t n = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  void* ub = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(static_cast<int>(n)), 0x00020000);
+}
+// 16 bytes at byte offset voff (per lane) + soff (uniform); zeros past the end.
+template <typename V>
+__device__ __forceinline__ V buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
 
 // Slot of row r when a 32-row tile is stored in the query-split order of
 // qsig() (slot m holds row qsig(m)): the inverse of qsig.
 __device__ __forceinline__ int qs_slot(int r) { return (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3); }
 
-// Copy one K tile (rows [key0, key0+32) of a row-major (rows, D) slice,
+// How a tile loader reads global memory (see above): through a buffer
+// resource, from addresses clamped into the slice, or (skip) only the rows
+// inside the slice, each load under its own condition.  Which one is fastest
+// depends on the kernel; each kernel uses the one measured best for it.
+enum LoadMode { kLoadBuffer = 0, kLoadClamp = 1, kLoadSkip = 2 };
+
+// Copy one K tile (rows [key0, key0+32) of a row-major (rows, D) slice with
 // nkeys >= 1 rows) into registers: each thread owns kKChunks / kThreads
-// 16-byte chunks.  CLAMP selects the branch-free form above; without it the
-// loads of rows past the end are skipped (cheaper where a step's compute is
-// short and more waves hide the load latency).  QS stores the rows in
+// 16-byte chunks; rows past nkeys end up as zeros.  QS stores the rows in
 // query-split order (row r at slot qs_slot(r)): lanes that read rows qsig(l)
 // then read consecutive slots, which keeps their 16-byte LDS reads free of
 // bank conflicts (rows r and r + 16 of the natural order share banks).
-template <typename CT, int D, bool CLAMP = true, bool QS = false>
+template <typename CT, int D, bool QS = false, int MODE = kLoadBuffer>
 struct KTileLoader {
   using T = Tiles<CT, D>;
   using V = typename Vec16<CT>::type;
   static constexpr int kPer = (T::kKChunks + kThreads - 1) / kThreads;
   static constexpr int kPerRow = D / T::kChunk;
   V r[kPer];
-  int nrows;                                        // rows of the tile inside the slice
+  int nrows;                                        // rows inside the slice (clamp form)
   __device__ void load(const CT* base, int64_t key0, int64_t nkeys) {
-    // slices hold fewer than 2^31 rows
-    const int k0 = static_cast<int>(key0), last = static_cast<int>(nkeys) - 1;
-    nrows = min(max(last + 1 - k0, 0), kTileK);
+    if constexpr (MODE == kLoadBuffer) {
+      const int64_t rows = min(max(nkeys - key0, int64_t{0}), int64_t{kTileK});
+      const auto rs = make_rsrc(base + key0 * D, rows * D * static_cast<int64_t>(sizeof(CT)));
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      if constexpr (CLAMP) {
-        const int idx = min(static_cast<int>(threadIdx.x) + u * kThreads, T::kKChunks - 1);
-        const int row = min(k0 + idx / kPerRow, last);
-        r[u] = *reinterpret_cast<const V*>(base + static_cast<int64_t>(row) * D + (idx % kPerRow) * T::kChunk);
-      } else {
-        const int idx = threadIdx.x + u * kThreads;
-        const int row = idx / kPerRow;
-        r[u] = V{};
-        if (idx < T::kKChunks && row < nrows)
-          r[u] = *reinterpret_cast<const V*>(base + (key0 + row) * D + (idx % kPerRow) * T::kChunk);
+      for (int u = 0; u < kPer; ++u)   // chunks idx >= kKChunks lie past the tile: zeros, never stored
+        r[u] = buffer_load16<V>(rs, static_cast<uint32_t>((threadIdx.x + u * kThreads) * 16), 0);
+    } else {
+      // slices hold fewer than 2^31 rows
+      const int k0 = static_cast<int>(key0), last = static_cast<int>(nkeys) - 1;
+      nrows = min(max(last + 1 - k0, 0), kTileK);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        if constexpr (MODE == kLoadClamp) {
+          const int idx = min(static_cast<int>(threadIdx.x) + u * kThreads, T::kKChunks - 1);
+          const int row = min(k0 + idx / kPerRow, last);
+          r[u] = *reinterpret_cast<const V*>(base + static_cast<int64_t>(row) * D + (idx % kPerRow) * T::kChunk);
+        } else {
+          const int idx = threadIdx.x + u * kThreads;
+          const int row = idx / kPerRow;
+          r[u] = V{};
+          if (idx < T::kKChunks && row < nrows)
+            r[u] = *reinterpret_cast<const V*>(base + (key0 + row) * D + (idx % kPerRow) * T::kChunk);
+        }
       }
     }
   }
   __device__ void store(CT* lds) const {
-    const bool full = !CLAMP || nrows == kTileK;    // workgroup-uniform
+    const bool full = MODE != kLoadClamp || nrows == kTileK;   // workgroup-uniform
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int idx = threadIdx.x + u * kThreads;
@@ -177,7 +216,7 @@ struct KTileLoader {
 // Copy one transposed tile (rows d in [0, D), columns [key0, key0 + 32), key0
 // a multiple of 32) of a tile-major slice into registers: 32 * D contiguous
 // elements.
-template <typename CT, int D>
+template <typename CT, int D, int MODE = kLoadBuffer>
 struct TTileLoader {
   using T = Tiles<CT, D>;
   using V = typename Vec16<CT>::type;
@@ -185,11 +224,18 @@ struct TTileLoader {
   static constexpr int kPerRow = kTileK / T::kChunk;
   V r[kPer];
   __device__ void load(const CT* base, int64_t key0) {
-    const CT* tile = base + key0 * D;               // (key0 / 32) * D * 32
+    const CT* tile = base + key0 * D;               // (key0 / 32) * D * 32: the tile's first element
+    if constexpr (MODE == kLoadBuffer) {
+      const auto rs = make_rsrc(tile, kTileK * D * static_cast<int64_t>(sizeof(CT)));
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int idx = min(static_cast<int>(threadIdx.x) + u * kThreads, T::kTChunks - 1);
-      r[u] = *reinterpret_cast<const V*>(tile + idx * T::kChunk);
+      for (int u = 0; u < kPer; ++u)   // chunks idx >= kTChunks lie past the tile: zeros, never stored
+        r[u] = buffer_load16<V>(rs, static_cast<uint32_t>((threadIdx.x + u * kThreads) * 16), 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int idx = min(static_cast<int>(threadIdx.x) + u * kThreads, T::kTChunks - 1);
+        r[u] = *reinterpret_cast<const V*>(tile + idx * T::kChunk);
+      }
     }
   }
   __device__ void store(CT* lds) const {

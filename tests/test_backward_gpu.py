@@ -62,6 +62,20 @@ def test_backward_bf16_matches_oracle(seq):
         assert err < 5e-2, f"{name} bf16 max abs err {err}"
 
 
+@pytest.mark.parametrize("seq", [4096, 4097])
+def test_backward_bf16_either_side_of_the_parked_query_pass(seq):
+    # the row pass runs in its LDS-parked form (three workgroups per CU) up to
+    # T = 4096 and in its register form beyond; both against the oracle
+    q, k, v, do = orc.make_inputs((1, 1, seq, 64), seed=seq, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    out, grads = _run(q, k, v, do, "bf16")
+    want, _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
+    for name, g, w in zip(("dq", "dk", "dv"), grads, want):
+        assert torch.isfinite(g.float()).all(), name
+        err = max_abs(g, torch.from_numpy(w))
+        assert err < 5e-2, f"{name} bf16 max abs err {err}"
+
+
 def test_backward_fp32_dout_with_bf16_inputs():
     """Under autocast the upstream gradient of the fp32 output is fp32 while
     q/k/v are bf16; gradients come back in the input dtype."""
