@@ -411,15 +411,14 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   fetch(nq - 1);
   stash(0);
   __syncthreads();
-  int it = 0;
   // vmcnt counts stores as well as loads, so the compiler must know on every
   // path how many memory operations follow the fetched data when the stash
   // waits for it: the stash is unconditional (the last iteration stashes into
   // the idle buffer), every thread writes LDS in it, and the step's suffix
   // checkpoint is stored after it (stored inside the conditional step, the
   // wait would also wait for that store).
-  for (int qt = nq - 1; qt >= kb0; --qt, ++it) {
-    const int buf = it & 1;
+  auto iter = [&](int j, int buf) __attribute__((always_inline)) {
+    const int qt = nq - 1 - j;                   // query tiles in reverse
     fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
     const bool run = active && qt >= kb;
     const float sufk_in = sufk;                  // suffix entering this tile from below
@@ -430,7 +429,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     stash(buf ^ 1);
     if (run && h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     sync_lds();
-  }
+  };
+  double_buffered<true>(0, nq - kb0, iter);
 
   if (key < P.T) {
     float* dkrow = P.dkm + (slice * P.T + key) * D;
@@ -703,8 +703,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
   fetch(0);
   stash(0);
   __syncthreads();
-  for (int kt = 0; kt < nkt_wg; ++kt) {
-    const int buf = kt & 1;
+  auto iter = [&](int kt, int buf) __attribute__((always_inline)) {
     const float cin = cin_next, sin = sin_next;
     if (kt + 1 < nkt_wg) {
       fetch(kt + 1);
@@ -715,7 +714,8 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
     else if (kt == qt && kt < nkt_w) step(kt, buf, cin, sin, std::true_type{});
     if (kt + 1 < nkt_wg) stash(buf ^ 1);
     sync_lds();
-  }
+  };
+  double_buffered<!kPark>(0, nkt_wg, iter);      // the parked form has no registers to spare
 
   // ghat per query (the elementwise bids have no row normalisation and no ghat
   // term).  Parked: the two halves' partial sums of query r0 + l32.  Register
@@ -838,9 +838,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
     stash(0);
   }
   __syncthreads();
-  int it = 0;
-  for (int qt = kb0; qt < q_end; ++qt, ++it) {
-    const int buf = it & 1;
+  auto iter = [&](int qt, int buf) __attribute__((always_inline)) {
     if (qt + 1 < nq) fetch(qt + 1);
     if (active) {
       if (qt > kb) step(buf, std::false_type{});
@@ -848,7 +846,8 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
     }
     if (qt + 1 < nq) stash(buf ^ 1);
     sync_lds();
-  }
+  };
+  double_buffered<true>(kb0, q_end, iter);
 
   if (key < P.T) {
     const int64_t base = (slice * P.T + key) * D;

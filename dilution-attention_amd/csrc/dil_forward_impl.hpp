@@ -235,8 +235,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   kl.store(ktile[0]);
   if constexpr (PK) tl.store(kttile[0]);
   __syncthreads();
-  for (int kt = 0; kt < nkt_wg; ++kt) {
-    const int buf = kt & 1;
+  auto iter = [&](int kt, int buf) __attribute__((always_inline)) {
     if (kt + 1 < nkt_wg) {
       const int64_t key0n = static_cast<int64_t>(kt + 1) * kTileK;
       kl.load(ks, key0n, P.Tk);
@@ -249,7 +248,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
       if constexpr (PK) tl.store(kttile[buf ^ 1]);
     }
     sync_lds();
-  }
+  };
+  double_buffered<true>(0, nkt_wg, iter);
   const HalfPair lp = halves(l0 + l1);                 // the halves share m
   float ltot, rmax_v, pk_f;
   if constexpr (bid_ratio<BID>()) {
@@ -406,9 +406,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
   // vmcnt counts stores as well as loads: the stash is unconditional (the
   // last iteration stashes into the idle buffer) and the checkpoint is stored
   // after it, so that the wait for the fetched block never waits for a store
-  int it = 0;
-  for (int64_t b = b_wg; b < nb; ++b, ++it) {
-    const int buf = it & 1;
+  auto iter = [&](int64_t b, int buf) __attribute__((always_inline)) {
     fetch(min(b + 1, nb - 1));                  // the last step reloads its own block, unused
     // wave-uniform condition: every lane must feed the MFMAs of the step
     const bool on = b >= b_w && key0 < P.Tk;
@@ -421,7 +419,8 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
     stash(buf ^ 1);
     if (on && h == 0 && key_ok) ccol[b * P.Tk] = entering;
     sync_lds();
-  }
+  };
+  double_buffered<true>(b_wg, nb, iter);
   if (key_ok && h == 0) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
 }
 
@@ -602,8 +601,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   fetch(0);
   stash(0);
   __syncthreads();
-  for (int st = 0; st < nst; ++st) {
-    const int buf = st & 1;
+  auto iter = [&](int st, int buf) __attribute__((always_inline)) {
     const int kt0 = 2 * st;
     fetch(min(st + 1, nst - 1));                       // the last stage reloads itself, unused
     if (kt0 + 1 < W.kfull) {
@@ -619,7 +617,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
     }
     if (st + 1 < nst) stash(buf ^ 1);
     sync_lds();
-  }
+  };
+  double_buffered<(D <= 64)>(0, nst, iter);      // head_dim 128 has no registers to spare
 
   // row sums: column 0 of orow, register i of half h <-> row acc_row(i, h)
   if (l32 == 0) {

@@ -149,6 +149,26 @@ __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
+// The main loop of a double-buffered kernel: iter(i, buf) for i in [begin,
+// end), with LDS buffer buf = (i - begin) & 1.  UNROLL unrolls it by two so
+// that buf is a constant in each copy and the buffer offsets fold into the
+// LDS instructions (about 10 VALU per step less); kernels whose registers are
+// at their limit keep the plain loop.
+template <bool UNROLL, typename I, typename F>
+__device__ __forceinline__ void double_buffered(I begin, I end, F&& iter) {
+  if constexpr (UNROLL) {
+    I i = begin;
+    for (; i + 1 < end; i += 2) {
+      iter(i, 0);
+      iter(i + 1, 1);
+    }
+    if (i < end) iter(i, 0);
+  } else {
+    int buf = 0;
+    for (I i = begin; i < end; ++i, buf ^= 1) iter(i, buf);
+  }
+}
+
 // Slot of row r when a 32-row tile is stored in the query-split order of
 // qsig() (slot m holds row qsig(m)): the inverse of qsig.
 __device__ __forceinline__ int qs_slot(int r) { return (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3); }
