@@ -62,6 +62,20 @@ def test_backward_bf16_matches_oracle(seq):
         assert err < 5e-2, f"{name} bf16 max abs err {err}"
 
 
+@pytest.mark.parametrize("head_dim", [16, 32, 128])
+def test_backward_bf16_head_dims(head_dim):
+    # head_dim 16 and 32 run the parked row pass, 128 the register form
+    q, k, v, do = orc.make_inputs((1, 2, 200, head_dim), seed=40 + head_dim, qk_scale=0.5,
+                                  with_dout=True, dtype=torch.bfloat16)
+    out, grads = _run(q, k, v, do, "bf16")
+    want, _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
+    assert max_abs(out, orc.attention_f64(q, k, v)) < 2e-2
+    for name, g, w in zip(("dq", "dk", "dv"), grads, want):
+        assert g.dtype == torch.bfloat16
+        err = max_abs(g, torch.from_numpy(w))
+        assert err < 5e-2, f"{name} bf16 max abs err {err}"
+
+
 @pytest.mark.parametrize("seq", [4096, 4097])
 def test_backward_bf16_either_side_of_the_parked_query_pass(seq):
     # the row pass runs in its LDS-parked form (three workgroups per CU) up to
