@@ -254,18 +254,19 @@ def prefill_chunk(q_chunk, k_all, v_all, demand_in, start: int):
     return torch.matmul(a, va), dem + p.sum(-2)
 
 
-def decode_step(q1, k_cache, v_cache, committed, length: int):
+def decode_step(q1, k_cache, v_cache, committed, length: int, dtype=torch.float64):
     """One cached decode row (kernels.py:937-991; eager twin model.py:242-257).
 
     q1: (B, H, 1, D); caches (B, H, cap, D); committed (B, H, cap) holding the
     column totals of p over earlier rows, with committed[..., length-1] == 0.
-    Returns (out (B, H, 1, D) float64, committed_new float64 with the first
-    `length` entries advanced by p and the rest unchanged).
+    Returns (out (B, H, 1, D), committed_new with the first `length` entries
+    advanced by p and the rest unchanged), both in `dtype` (float64 for the
+    parity checks; the bench's CPU baseline times float32).
     """
-    q = torch.as_tensor(q1).double()
-    k = torch.as_tensor(k_cache).double()[..., :length, :]
-    v = torch.as_tensor(v_cache).double()[..., :length, :]
-    com = torch.as_tensor(committed).double().clone()
+    q = torch.as_tensor(q1).to(dtype)
+    k = torch.as_tensor(k_cache).to(dtype)[..., :length, :]
+    v = torch.as_tensor(v_cache).to(dtype)[..., :length, :]
+    com = torch.as_tensor(committed).to(dtype).clone()
     d = q.shape[-1]
     a = torch.matmul(q, k.transpose(-2, -1))[..., 0, :] / math.sqrt(d)
     p = torch.softmax(a, dim=-1)
