@@ -758,7 +758,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   __shared__ __attribute__((aligned(16))) CT qgt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) float st_s[2][kNS * kTileQ];   // lse (r0), (unused), r1
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, false);   // slice by slice: measured faster here
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
