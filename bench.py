@@ -67,6 +67,8 @@ WORKLOADS = {
     # the same 262144 tokens per step at intermediate lengths
     "train4k": (4, 16, 4096, 64),
     "train8k": (2, 16, 8192, 64),
+    # the whole LM's attention call (B4 H16 at 16K)
+    "lm16k": (4, 16, 16384, 64),
 }
 
 # Algorithmic products (each B H T^2 d FLOPs causal) that each kernel of the

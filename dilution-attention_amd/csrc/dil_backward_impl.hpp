@@ -70,6 +70,7 @@ struct BwdParams {
   void* dk;
   void* dv;
   int gdt;            // grad dtype
+  int lpt;            // dispatch longest first (xcd_work_item)
 };
 
 // ---------------------------------------------------------------------------
@@ -205,15 +206,14 @@ constexpr int bwd_occupancy() {
 
 // bwd_query's parked form keeps its dO' operands and the transpose identity
 // in LDS and sums ghat on the VALU, which leaves room for three workgroups per
-// CU (<= 168 VGPRs, 48 KB of LDS each) with bf16 operands up to head_dim 64.
-// It pays where the sweeps are short (T <= kParkMaxT: -10% at T = 2048, -3% at
-// 4096); at longer T the register form (ones-column MFMA for ghat, two
-// workgroups per CU) is as fast or faster, so it runs there.
+// CU (<= 168 VGPRs, 48 KB of LDS each) with bf16 operands up to head_dim 64:
+// -16% at T = 2048, -10% at 4096 and 16384 against the register form (ones
+// column MFMA for ghat, two workgroups per CU), which runs for fp32 operands,
+// head_dim 128 and the operator variants.
 template <typename CT, int D>
 constexpr bool query_parks() {
   return sizeof(CT) == 2 && D <= 64;
 }
-constexpr int64_t kParkMaxT = 4096;
 
 // Sum of 16 values as a depth-4 tree.
 __device__ __forceinline__ float sum16(const float (&v)[16]) {
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   __shared__ __attribute__((aligned(16))) float st_s[2][kThreads];
   __shared__ float cs_s[2][kThreads];             // demand checkpoints of the 128 keys, then padding
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
   __shared__ __attribute__((aligned(16))) Frag do_park[kPark ? 4 : 1][kPark ? kFS : 1][64];
   __shared__ __attribute__((aligned(16))) Frag id_park[kPark ? kSteps : 1][64];
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, true);    // heavy (late) row groups first
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, true, P.lpt != 0);    // heavy (late) row groups first
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int g = item.idx;
@@ -964,6 +964,7 @@ int launch_backward(const BackwardArgs& a) {
   P.dk = a.dk;
   P.dv = a.dv;
   P.gdt = a.grad_dtype;
+  P.lpt = longest_first_for(a.n, a.T);
 
   const int64_t rows = a.n * a.T;
   const int64_t threads = rows * (D / 8);
@@ -982,14 +983,8 @@ int launch_backward(const BackwardArgs& a) {
   P.kgroups = (nkt + 3) / 4;
   const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
-  bool parked = false;
-  if constexpr (query_parks<CT, D>() && is_production<BID, SHARE>()) {
-    if (a.T <= kParkMaxT) {
-      DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, true><<<gkey, kThreads, 0, st>>>(P)));
-      parked = true;
-    }
-  }
-  if (!parked) DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, false><<<gkey, kThreads, 0, st>>>(P)));
+  constexpr bool kParked = query_parks<CT, D>() && is_production<BID, SHARE>();
+  DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, kParked><<<gkey, kThreads, 0, st>>>(P)));
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("prep", st,
               prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), ns), kThreads, 0, st>>>(

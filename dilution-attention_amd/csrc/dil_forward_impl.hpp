@@ -65,6 +65,7 @@ struct FwdParams {
   float* total;
   int64_t tot_sn;
   float* pk;
+  int lpt;                // dispatch longest first (xcd_work_item)
 };
 
 // ---------------------------------------------------------------------------
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   using T = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
   __shared__ __attribute__((aligned(16))) CT kttile[PK ? 2 : 1][PK ? D * T::kTStride : 1];
-  const WorkItem item = xcd_work_item(P.groups, P.n, true);   // heavy (late) row groups first
+  const WorkItem item = xcd_work_item(P.groups, P.n, true, P.lpt != 0);   // heavy (late) row groups first
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int g = item.idx;
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
   // (r0, r1) of the block's rows, then padding: every thread of the stash writes
   __shared__ __attribute__((aligned(16))) float st_s[2][kRP][kThreads];
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false);   // early keys (long walks) first
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   __shared__ float ssum_s[4][kTileQ];
   __shared__ float cs_s[2][4][2 * kTileK];             // demand checkpoints per stage and wave
 
-  const WorkItem item = xcd_work_item(P.groups, P.n, true);
+  const WorkItem item = xcd_work_item(P.groups, P.n, true, P.lpt != 0);
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int g = item.idx;
@@ -703,6 +704,9 @@ int launch_forward(const ForwardArgs& a) {
   P.Tk = a.Tk;
   P.q0 = a.q0;
   P.nb = (a.C + kTileQ - 1) / kTileQ;
+  // longest first pays where the items' weights differ widely: a chunk that
+  // starts before its own length (training, a first prefill chunk)
+  P.lpt = a.q0 < a.C && longest_first_for(a.n, a.Tk);
   P.scale = 1.f / sqrtf(static_cast<float>(D));
   P.c = kLog2e * P.scale;
   P.out = a.out;

@@ -77,9 +77,9 @@ def test_backward_bf16_head_dims(head_dim):
 
 
 @pytest.mark.parametrize("seq", [4096, 4097])
-def test_backward_bf16_either_side_of_the_parked_query_pass(seq):
-    # the row pass runs in its LDS-parked form (three workgroups per CU) up to
-    # T = 4096 and in its register form beyond; both against the oracle
+def test_backward_bf16_long_rows(seq):
+    # 128 and 129 row tiles: the LDS-parked row pass (three workgroups per CU)
+    # over long key sweeps, against the oracle
     q, k, v, do = orc.make_inputs((1, 1, seq, 64), seed=seq, qk_scale=0.5, with_dout=True,
                                   dtype=torch.bfloat16)
     out, grads = _run(q, k, v, do, "bf16")
