@@ -83,6 +83,8 @@ def _check_device(*ts: torch.Tensor) -> None:
     for t in ts:
         if not t.is_cuda:
             raise RuntimeError("dilution HIP kernels need tensors on the GPU (no CPU path)")
+        if t.device != ts[0].device:
+            raise ValueError(f"all tensors must be on one device, got {ts[0].device} and {t.device}")
 
 
 def _check_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -126,8 +128,9 @@ def _rows(x: torch.Tensor, n: int, t: int, d: int, dtype: torch.dtype) -> torch.
     return x.reshape(n, t, d).to(dtype).contiguous()
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+def _stream(dev: torch.device) -> int:
+    """The caller's current stream on the inputs' device; launches go there."""
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -202,11 +205,12 @@ def dilution_attention_forward(
                 _DTYPES[dt], prec)
         tail = (out[a:b].data_ptr(), rmax[a:b].data_ptr(), rden[a:b].data_ptr(),
                 ssum[a:b].data_ptr(), carry.data_ptr(), total[a:b].data_ptr(),
-                None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream())
-        if tuple(_variant) == _PRODUCTION:
-            status = lib.dil_forward(*head, *tail)
-        else:
-            status = lib.dil_forward_variant(*head, *_variant, *tail)
+                None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+        with torch.cuda.device(dev):
+            if tuple(_variant) == _PRODUCTION:
+                status = lib.dil_forward(*head, *tail)
+            else:
+                status = lib.dil_forward_variant(*head, *_variant, *tail)
         _hip.check(status, "dil_forward")
 
     result = out.reshape(batch, heads, seq, head_dim)
@@ -269,11 +273,12 @@ def _backward(saved, dout, dot_precision: str, variant: tuple):
     head = (qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), dof.data_ptr(), of.data_ptr(),
             rmax.data_ptr(), rden.data_ptr(), ssum.data_ptr(), carry.data_ptr(), pk.data_ptr(),
             n, seq, head_dim, _DTYPES[dt], _DTYPES[ddt], _DTYPES[gdt], prec)
-    tail = (dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
-    if tuple(variant) == _PRODUCTION:
-        status = lib.dil_backward(*head, *tail)
-    else:
-        status = lib.dil_backward_variant(*head, *variant, *tail)
+    tail = (dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    with torch.cuda.device(dev):
+        if tuple(variant) == _PRODUCTION:
+            status = lib.dil_backward(*head, *tail)
+        else:
+            status = lib.dil_backward_variant(*head, *variant, *tail)
     _hip.check(status, "dil_backward")
     shape4 = (batch, heads, seq, head_dim)
     for g, ref in zip((dq, dk, dv), (q, k, v)):
@@ -357,10 +362,11 @@ def dilution_prefill_chunk(
     ssum = torch.empty(n, chunk, **f32)
     carry = torch.empty(n, nb, start + chunk, **f32)
     ws = _workspace(lib.dil_prefill_workspace_bytes(n, chunk, start, head_dim, _DTYPES[dt], prec), dev)
-    status = lib.dil_prefill_chunk(
-        qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), n, chunk, start, capacity, head_dim,
-        _DTYPES[dt], prec, cf.data_ptr(), out.data_ptr(), rmax.data_ptr(), rden.data_ptr(),
-        ssum.data_ptr(), carry.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+    with torch.cuda.device(dev):
+        status = lib.dil_prefill_chunk(
+            qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), n, chunk, start, capacity, head_dim,
+            _DTYPES[dt], prec, cf.data_ptr(), out.data_ptr(), rmax.data_ptr(), rden.data_ptr(),
+            ssum.data_ptr(), carry.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
     _hip.check(status, "dil_prefill_chunk")
     result = out.reshape(batch, heads, chunk, head_dim)
     if return_aux:
@@ -416,11 +422,12 @@ def dilution_decode_step(
     ws = _workspace(lib.dil_decode_workspace_bytes(n, length, head_dim), q1.device)
     head = (qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), cf.data_ptr(), out.data_ptr(), n,
             capacity, length, head_dim, _DTYPES[dt])
-    tail = (ws.data_ptr(), ws.numel(), _stream())
-    if tuple(_variant) == _PRODUCTION:
-        status = lib.dil_decode_step(*head, *tail)
-    else:
-        status = lib.dil_decode_step_variant(*head, *_variant, *tail)
+    tail = (ws.data_ptr(), ws.numel(), _stream(q1.device))
+    with torch.cuda.device(q1.device):
+        if tuple(_variant) == _PRODUCTION:
+            status = lib.dil_decode_step(*head, *tail)
+        else:
+            status = lib.dil_decode_step_variant(*head, *_variant, *tail)
     _hip.check(status, "dil_decode_step")
     if out.dtype != q1.dtype:
         out = out.to(q1.dtype)
