@@ -114,3 +114,19 @@ def test_cache_shape_errors_before_any_launch():
         kernels.dilution_prefill_chunk(torch.zeros(b, h, 8, d), kc, kc, com, 12)   # rows past capacity
     with pytest.raises(RuntimeError):
         kernels.dilution_decode_step(q1, kc, kc, com, 4)                    # valid, but no GPU tensors
+
+
+def test_tensors_on_two_devices_are_rejected():
+    """Every launch goes to the inputs' device and that device's current
+    stream; inputs spread over two devices are a ValueError before any launch."""
+    import types
+
+    import torch
+    from dilution import kernels
+
+    on = lambda i: types.SimpleNamespace(is_cuda=True, device=torch.device("cuda", i))  # noqa: E731
+    kernels._check_device(on(0), on(0), on(0))
+    with pytest.raises(ValueError):
+        kernels._check_device(on(0), on(1), on(0))
+    with pytest.raises(RuntimeError):
+        kernels._check_device(on(0), torch.zeros(1))
