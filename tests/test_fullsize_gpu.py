@@ -153,3 +153,64 @@ def test_decode_at_128k_context():
         want64, want_com = orc.decode_step(q1[sl].cpu(), kc[sl].cpu(), vc[sl].cpu(), before[sl].cpu(), length)
         assert max_abs(out[sl], want64) < 2e-2
         assert max_abs(com[sl][..., :length], want_com[..., :length]) < 1e-5 * 4.0
+
+
+def test_sequence_of_131072_far_end_closed_forms():
+    """One slice at T = 131072 (bf16), where (T/32) x T checkpoints and T x d
+    offsets are far past the benchmark's sizes.  The oracle does not fit, but
+    the far end of the sequence has closed forms in one row of scores:
+
+    * the last row's committed demand plus its own bid is the key's demand
+      total (c + p = total_j), so with the kernel's totals its output is
+      sum_j p_j v_j / (total_j + eps), renormalised (kernels.py:59-68);
+    * its suffix term is empty, so dp_j = ds_j (c_j + eps) / (total_j + eps)^2
+      and dq_{T-1} = s sum_j p_j (dp_j - ghat) k_j; key T-1 is seen by row
+      T-1 alone, which gives dk_{T-1} and dv_{T-1}
+      (docs/kernels.md:62-84 restated);
+    * the totals of the last 64 keys are column sums over the last 64 rows;
+    * every row's bids sum to one, so the totals sum to T; the first 4096
+      rows are bit-identical to the forward of the 4096-token prefix.
+    """
+    from dilution import kernels
+
+    seq, d, eps = 131072, 64, 1e-9
+    q, k, v, do = orc.make_inputs((1, 1, seq, d), seed=7, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="bf16")
+    out.backward(do.cuda())
+    _, aux = kernels.dilution_attention_forward(*(x.detach() for x in xs), dot_precision="bf16",
+                                                return_aux=True)
+    prefix = kernels.dilution_attention_forward(*(x.detach()[:, :, :4096] for x in xs),
+                                                dot_precision="bf16")
+    torch.cuda.synchronize()
+    assert torch.equal(prefix, out.detach()[:, :, :4096])
+    out = out.detach()[0, 0].double().cpu().numpy()
+    dq, dk, dv = (x.grad[0, 0].double().cpu().numpy() for x in xs)
+    assert np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    tot = aux["committed_total"][0, 0].double().cpu().numpy()
+    assert abs(tot.sum() - seq) <= 1e-4 * seq
+
+    Q, K, V, dO = (t[0, 0].double().numpy() for t in (q, k, v, do))
+    s = d ** -0.5
+    a = (Q[-64:] @ K.T) * s
+    a[np.arange(64)[:, None] + seq - 64 < np.arange(seq)[None, :]] = -np.inf
+    p64 = np.exp(a - a.max(1, keepdims=True))
+    p64 /= p64.sum(1, keepdims=True)
+    want_tot = p64[:, seq - 64:].sum(0)                     # masked: only rows i >= j
+    assert np.abs(tot[seq - 64:] - want_tot).max() <= 1e-4 * want_tot.max() + 1e-7
+
+    p = p64[-1]
+    share = p / (tot + eps)
+    S = share.sum()
+    A = share / (S + eps)
+    o = A @ V
+    assert np.abs(out[-1] - o).max() < 2e-2
+    ds = (V @ dO[-1] - dO[-1] @ o) / (S + eps)
+    dp = ds * (tot - p + eps) / (tot + eps) ** 2
+    da = p * (dp - (p * dp).sum())
+    g_dq, g_dk, g_dv = s * (da @ K), s * da[-1] * Q[-1], A[-1] * dO[-1]
+    scale = np.abs(g_dq).max()
+    assert np.abs(dq[-1] - g_dq).max() < 5e-2 * max(scale, 1e-3), (np.abs(dq[-1] - g_dq).max(), scale)
+    assert np.abs(dk[-1] - g_dk).max() < 5e-2 * max(np.abs(g_dk).max(), 1e-6) + 1e-6
+    assert np.abs(dv[-1] - g_dv).max() < 5e-2 * max(np.abs(g_dv).max(), 1e-6) + 1e-6
