@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                     [--decode-steps K] [--decode-context L] [--no-decode]
-                    [--no-sdpa] [--no-lm] [--no-variants] [--no-cpu-baseline]
+                    [--no-sdpa] [--no-lm] [--no-variants] [--no-fp32] [--no-cpu-baseline]
 
 Prints ONE JSON line.  The headline workload (default ``train16k``,
 BASELINE configs[2]) is the operator's training step, fwd+bwd through
@@ -35,6 +35,9 @@ The same line carries
     (the ablation operators), fwd+bwd at the headline shape and the cached
     decode step at the decode shape, ms per step and TFLOP/s / GB/s on the
     same algorithmic counts;
+  * ``fp32``: the "ieee" mode (fp32 operands, fp32 MFMA; the reference
+    forward's default) at the headline shape, fwd+bwd and the forward alone
+    (2 B H T^2 d), with the dominant kernel against the fp32 MFMA peak;
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
     formula) timed on this host's cores on one (batch, head) slice of the
     headline workload; ``decode.cpu_baseline``: the oracle's decode step in
@@ -58,6 +61,7 @@ for _p in (os.path.join(ROOT, "dilution-attention_amd"), ROOT):
 
 METRIC = "dilution-attn fwd+bwd TFLOP/s & decode HBM GB/s at T=16K, % of MI355X peak"
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3          # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
 # Training-step workloads: (batch, heads, seq, head_dim)
@@ -121,6 +125,7 @@ def parse_args():
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-lm", action="store_true")
     ap.add_argument("--no-variants", action="store_true")
+    ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--variant-steps", type=int, default=5)
     ap.add_argument("--lm-train-steps", type=int, default=2)
     ap.add_argument("--lm-decode-tokens", type=int, default=512)
@@ -267,6 +272,49 @@ def bench_sdpa(args, inputs):
     log(f"sdpa flash causal fwd+bwd: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")
     return {"backend": "torch SDPA flash, causal, bf16", "ms_per_step": round(ms, 4),
             "value": round(tflops, 2), "unit": "TFLOP/s"}
+
+
+def bench_fp32(args, inputs):
+    """The "ieee" mode (fp32 operands and fp32 MFMA; the reference forward's
+    default precision, kernels.py:328-335) at the training shape: fwd+bwd and
+    the forward alone, priced against the fp32 MFMA peak."""
+    import torch
+
+    from dilution import kernels
+
+    q, k, v, do = (t.detach().float() for t in inputs)
+    xs = [t.clone().requires_grad_(True) for t in (q, k, v)]
+
+    def train():
+        for x in xs:
+            x.grad = None
+        kernels.dilution_attention(*xs, dot_precision="ieee").backward(do)
+
+    def forward():
+        kernels.dilution_attention_forward(q, k, v)
+
+    steps = args.variant_steps
+    for _ in range(2):
+        train()
+    ms_train = timed(train, steps)
+    per = kernel_pass(train, steps)
+    forward()
+    ms_fwd = timed(forward, steps)
+    batch, heads, seq, d = q.shape
+    unit = batch * heads * seq * seq * d
+    dom = max((nm for nm in per if nm in ALGO_PRODUCTS), key=lambda nm: per[nm][1])
+    dom_ms = per[dom][1] / per[dom][0]
+    achieved = ALGO_PRODUCTS[dom] * unit / (dom_ms * 1e-3) / 1e12
+    log(f"fp32 fwd+bwd: {ms_train:.3f} ms/step; forward {ms_fwd:.3f} ms")
+    del xs
+    return {"dot_precision": "ieee", "dtype": "f32", "train_ms": round(ms_train, 4),
+            "train_tflops": round(7.0 * unit / (ms_train * 1e-3) / 1e12, 2),
+            "forward_ms": round(ms_fwd, 4),
+            "forward_tflops": round(2.0 * unit / (ms_fwd * 1e-3) / 1e12, 2),
+            "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                         "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "avg_launch_ms": round(dom_ms, 4)},
+            "kernels": {name: round(tot / max(n, 1), 4) for name, (n, tot) in per.items()}}
 
 
 def bench_decode(args, dev):
@@ -633,6 +681,9 @@ def main() -> int:
             line["sdpa"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
     if not args.no_variants:
         line["variants"] = bench_variants(args, dev, tr["inputs"])
+        torch.cuda.empty_cache()
+    if not args.no_fp32:
+        line["fp32"] = bench_fp32(args, tr["inputs"])
         torch.cuda.empty_cache()
     del tr["inputs"]
     if not args.no_prefill:
