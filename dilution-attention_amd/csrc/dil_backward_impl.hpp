@@ -921,16 +921,12 @@ int launch_backward(const BackwardArgs& a) {
 
   const unsigned tiles64 = static_cast<unsigned>(t_pad / 64);
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
-    DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.q, sn, a.dtype, a.T, qc, sn, qt,
-                                                                         D * t_pad, t_pad, nullptr, s0));
-    DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.k, sn, a.dtype, a.T, kc, sn, kt,
-                                                                         D * t_pad, t_pad, nullptr, s0));
-    if (convert)
-      DIL_TIMED("prep", st,
-                prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.v, sn, a.dtype, a.T, vc, sn,
-                                                                           nullptr, 0, t_pad, nullptr, s0));
+    PrepJobs qkv{};
+    qkv.job[0] = PrepJob{a.q, sn, qc, sn, qt, nullptr};
+    qkv.job[1] = PrepJob{a.k, sn, kc, sn, kt, nullptr};
+    qkv.job[2] = PrepJob{a.v, sn, vc, sn, nullptr, nullptr};
+    DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(tiles64, ns, convert ? 3 : 2), kThreads, 0, st>>>(
+                              qkv, a.dtype, a.T, D * t_pad, t_pad, s0)));
   });
 
   BwdParams P{};
@@ -974,9 +970,10 @@ int launch_backward(const BackwardArgs& a) {
                 reinterpret_cast<float*>(ws + w.rb1))));
   // dO' = dO / (S + eps), row-major and transposed, in the compute type
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
-    DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<dim3(tiles64, ns), kThreads, 0, st>>>(a.dout, sn, a.dout_dtype, a.T, doc,
-                                                                         sn, dot, D * t_pad, t_pad, sinv, s0));
+    PrepJobs dj{};
+    dj.job[0] = PrepJob{a.dout, sn, doc, sn, dot, sinv};
+    DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(tiles64, ns, 1), kThreads, 0, st>>>(
+                              dj, a.dout_dtype, a.T, D * t_pad, t_pad, s0)));
   });
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;

@@ -677,18 +677,17 @@ int launch_forward(const ForwardArgs& a) {
   const unsigned ktiles = static_cast<unsigned>(tk_pad / 64);
   const unsigned qtiles = static_cast<unsigned>(pad64(a.C) / 64);
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
-    DIL_TIMED("prep", st,
-              prep_kernel<CT, D><<<dim3(ktiles, ns), kThreads, 0, st>>>(a.v, a.kv_sn, a.dtype, a.Tk, nullptr,
-                                                                        0, vt, D * tk_pad, tk_pad, nullptr, s0));
-    if (convert || kt != nullptr)
-      DIL_TIMED("prep", st,
-                prep_kernel<CT, D><<<dim3(ktiles, ns), kThreads, 0, st>>>(a.k, a.kv_sn, a.dtype, a.Tk, kc,
-                                                                          a.Tk * D, kt, D * tk_pad, tk_pad,
-                                                                          nullptr, s0));
-    if (convert)
-      DIL_TIMED("prep", st,
-                prep_kernel<CT, D><<<dim3(qtiles, ns), kThreads, 0, st>>>(a.q, a.q_sn, a.dtype, a.C, qc,
-                                                                          a.C * D, nullptr, 0, 0, nullptr, s0));
+    PrepJobs kv{};
+    kv.job[0] = PrepJob{a.v, a.kv_sn, nullptr, 0, vt, nullptr};
+    kv.job[1] = PrepJob{a.k, a.kv_sn, kc, a.Tk * D, kt, nullptr};
+    const unsigned nkv = (convert || kt != nullptr) ? 2 : 1;
+    DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(ktiles, ns, nkv), kThreads, 0, st>>>(
+                              kv, a.dtype, a.Tk, D * tk_pad, tk_pad, s0)));
+    if (convert) {
+      PrepJobs qj{};
+      qj.job[0] = PrepJob{a.q, a.q_sn, qc, a.C * D, nullptr, nullptr};
+      DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(qtiles, ns, 1), kThreads, 0, st>>>(qj, a.dtype, a.C, 0, 0, s0)));
+    }
   });
 
   FwdParams P{};

@@ -41,20 +41,39 @@ __device__ __forceinline__ void store8(CT* dst, const float (&v)[8]) {
   }
 }
 
-// Rows of `src` (storage dtype dt) in the compute type CT, optionally scaled
-// per row by rscale[(slice, row)] (in fp32, before the rounding to CT): a
-// row-major copy into dst and/or a tile-major transposed copy (rows_pad rows,
-// a multiple of 64; slice stride t_sn) into dst_t, zero-padded past `rows`.
-// Grid: (row tiles of 64, slices from slice0).  Every thread stores 16-byte
-// runs: 8 columns of a row in the row-major copy, 8 rows of a column in the
-// transposed one (contiguous there, and consecutive threads continue the run
-// through the 32 x D block of a 32-row tile).
+// One operand preparation: rows of `src` (slice stride src_sn) in the compute
+// type, optionally scaled per row by rscale[(slice, row)] (in fp32, before the
+// rounding): a row-major copy into dst (slice stride dst_sn) and/or a
+// tile-major transposed copy into dst_t.  Null outputs are skipped.
+struct PrepJob {
+  const void* src;
+  int64_t src_sn;
+  void* dst;
+  int64_t dst_sn;
+  void* dst_t;
+  const float* rscale;
+};
+
+// Up to three preparations of one storage dtype dt and one length, run by one
+// launch: blockIdx.z picks the job.
+struct PrepJobs {
+  PrepJob job[3];
+};
+
+// Grid: (row tiles of 64, slices from slice0, jobs).  The transposed copy has
+// rows_pad rows (a multiple of 64, zero past `rows`) and slice stride t_sn.
+// Every thread stores 16-byte runs: 8 columns of a row in the row-major copy,
+// 8 rows of a column in the transposed one (contiguous there, and consecutive
+// threads continue the run through the 32 x D block of a 32-row tile).
 template <typename CT, int D>
-__global__ __launch_bounds__(kThreads) void prep_kernel(const void* __restrict__ src, int64_t src_sn,
-                                                        int dt, int64_t rows, CT* __restrict__ dst,
-                                                        int64_t dst_sn, CT* __restrict__ dst_t,
-                                                        int64_t t_sn, int64_t rows_pad,
-                                                        const float* __restrict__ rscale, int64_t slice0) {
+__global__ __launch_bounds__(kThreads) void prep_kernel(PrepJobs jobs, int dt, int64_t rows, int64_t t_sn,
+                                                        int64_t rows_pad, int64_t slice0) {
+  const PrepJob& job = jobs.job[blockIdx.z];
+  const void* __restrict__ src = job.src;
+  const int64_t src_sn = job.src_sn, dst_sn = job.dst_sn;
+  CT* __restrict__ dst = static_cast<CT*>(job.dst);
+  CT* __restrict__ dst_t = static_cast<CT*>(job.dst_t);
+  const float* __restrict__ rscale = job.rscale;
   __shared__ float tile[64][D + 1];
   const int64_t slice = slice0 + blockIdx.y;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
