@@ -17,7 +17,8 @@
 // Kernels (gfx950, deterministic, no atomics; tiles in the query-split layout
 // of dil_tiles.hpp, causal diagonal tiles peeled out of the main loops):
 //   bwd_rows    per row: lse = rmax + log2 rden, sinv = 1/(S + eps),
-//               dbs = (dO . o) sinv.
+//               dbs = (dO . o) sinv; and dO' = dO sinv in the compute type,
+//               row-major and transposed, from the same read of dO.
 //   bwd_key     one wave per 32-key tile, query tiles walked in reverse:
 //               dv += sh^T dO' and dk_main += (p dp)^T Q on MFMA with
 //               keys in lanes; the running suffix G per key is stored at every
@@ -76,40 +77,78 @@ struct BwdParams {
 // ---------------------------------------------------------------------------
 // per-row prologue
 
-template <int D, int BID = BID_SOFTMAX>
-__global__ __launch_bounds__(256) void bwd_rows(const void* __restrict__ dout, int ddt,
-                                                const float* __restrict__ out,
-                                                const float* __restrict__ rmax,
-                                                const float* __restrict__ rden,
-                                                const float* __restrict__ ssum, float* __restrict__ lse,
-                                                float* __restrict__ sinv, float* __restrict__ dbs,
-                                                int64_t rows, int64_t T, float* __restrict__ rb1) {
-  constexpr int LPR = D / 8;                    // lanes per row, 8 elements each
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t row = gid / LPR;
-  const int sub = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (row < rows) {
-    float a[8], b[8];
-    load8_f32(dout, row * D + sub * 8, ddt, a);
-    load8_f32(out, row * D + sub * 8, DT_F32, b);
+template <typename CT, int D, int BID = BID_SOFTMAX>
+__global__ __launch_bounds__(kThreads) void bwd_rows(const void* __restrict__ dout, int ddt,
+                                                     const float* __restrict__ out,
+                                                     const float* __restrict__ rmax,
+                                                     const float* __restrict__ rden,
+                                                     const float* __restrict__ ssum, float* __restrict__ lse,
+                                                     float* __restrict__ sinv, float* __restrict__ dbs,
+                                                     float* __restrict__ rb1, int64_t T, int64_t t_pad,
+                                                     CT* __restrict__ doc, CT* __restrict__ dot,
+                                                     int64_t slice0) {
+  // Grid: (64-row tiles, slices from slice0).  A row's D / 8 lanes are
+  // consecutive; each holds 8 elements of dO and o.
+  constexpr int kVecPerRow = D / 8;
+  __shared__ float tile[64][D + 1];
+  const int64_t slice = slice0 + blockIdx.y;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+  // 64 * D / 8 items are a whole number of waves: each shuffle below runs on
+  // full waves
+  for (int idx = threadIdx.x; idx < 64 * kVecPerRow; idx += kThreads) {
+    const int r = idx / kVecPerRow, sub = idx % kVecPerRow, c8 = sub * 8;
+    const bool ok = r0 + r < T;
+    const int64_t row = slice * T + r0 + r;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float acc = 0.f;
+    if (ok) {
+      float o[8];
+      load8_f32(dout, row * D + c8, ddt, v);
+      load8_f32(out, row * D + c8, DT_F32, o);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf(a[e], b[e], acc);
-  }
-#pragma unroll
-  for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
-  if (row < rows && sub == 0) {
-    const float si = 1.f / (ssum[row] + kEps);
-    if constexpr (BID == BID_SOFTMAX) {
-      lse[row] = rmax[row] + __log2f(rden[row]);
-    } else {
-      float r0, r1;
-      bid_row_params<BID>(rmax[row], rden[row], static_cast<float>(row % T + 1), true, r0, r1);
-      lse[row] = r0;
-      rb1[row] = r1;
+      for (int e = 0; e < 8; ++e) acc = fmaf(v[e], o[e], acc);
     }
-    sinv[row] = si;
-    dbs[row] = acc * si;
+#pragma unroll
+    for (int m = 1; m < kVecPerRow; m <<= 1) acc += __shfl_xor(acc, m, 64);
+    if (ok) {
+      const float si = 1.f / (ssum[row] + kEps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= si;
+      if (sub == 0) {
+        if constexpr (BID == BID_SOFTMAX) {
+          lse[row] = rmax[row] + __log2f(rden[row]);
+        } else {
+          float a0, a1;
+          bid_row_params<BID>(rmax[row], rden[row], static_cast<float>(r0 + r + 1), true, a0, a1);
+          lse[row] = a0;
+          rb1[row] = a1;
+        }
+        sinv[row] = si;
+        dbs[row] = acc * si;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[r][c8 + e] = v[e];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 64 * kVecPerRow; idx += kThreads) {
+    const int r = idx / kVecPerRow, c8 = (idx % kVecPerRow) * 8;
+    if (r0 + r < T) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = tile[r][c8 + e];
+      store8<CT>(doc + (slice * T + r0 + r) * D + c8, v);
+    }
+  }
+  // transposed: item idx is 32-row half b, column c, rows r8 .. r8 + 7 of it
+  for (int idx = threadIdx.x; idx < 8 * D; idx += kThreads) {
+    const int b = idx / (4 * D), c = (idx % (4 * D)) >> 2, r8 = 32 * b + (idx & 3) * 8;
+    if (r0 + r8 < t_pad) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = tile[r8 + e][c];
+      store8<CT>(dot + slice * D * t_pad + tmajor_index(r0 + r8, c, D), v);
+    }
   }
 }
 
@@ -962,18 +1001,11 @@ int launch_backward(const BackwardArgs& a) {
   P.gdt = a.grad_dtype;
   P.lpt = longest_first_for(a.n, a.T);
 
-  const int64_t rows = a.n * a.T;
-  const int64_t threads = rows * (D / 8);
-  DIL_TIMED("bwd_rows", st,
-            (bwd_rows<D, BID><<<dim3(static_cast<unsigned>((threads + 255) / 256)), 256, 0, st>>>(
-                a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbs, rows, a.T,
-                reinterpret_cast<float*>(ws + w.rb1))));
-  // dO' = dO / (S + eps), row-major and transposed, in the compute type
+  // row statistics and dO' = dO / (S + eps), row-major and transposed
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
-    PrepJobs dj{};
-    dj.job[0] = PrepJob{a.dout, sn, doc, sn, dot, sinv};
-    DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(tiles64, ns, 1), kThreads, 0, st>>>(
-                              dj, a.dout_dtype, a.T, D * t_pad, t_pad, s0)));
+    DIL_TIMED("bwd_rows", st, (bwd_rows<CT, D, BID><<<dim3(tiles64, ns), kThreads, 0, st>>>(
+                                  a.dout, a.dout_dtype, a.out, a.rmax, a.rden, a.ssum, lse, sinv, dbs,
+                                  reinterpret_cast<float*>(ws + w.rb1), a.T, t_pad, doc, dot, s0)));
   });
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
