@@ -22,6 +22,8 @@ The same line carries
   * ``kernels``: per-kernel launches and average milliseconds of that pass;
   * ``sdpa``: torch's causal flash attention fwd+bwd at the same shape and
     dtype on the same GPU, timed the same way (the >= 0.6x comparator);
+  * ``train2k``: the same fwd+bwd at BASELINE configs[1] (B=8 H=16 T=2048),
+    with its own SDPA comparator;
   * ``prefill``: chunked prefill of a 16K prompt in 2K chunks (BASELINE
     configs[3]: B=16 H=16 d=64 bf16), algorithmic TFLOP/s;
   * ``decode``: the cached decode step at 128K context (
@@ -130,6 +132,8 @@ def parse_args():
     ap.add_argument("--lm-train-steps", type=int, default=2)
     ap.add_argument("--lm-decode-tokens", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train2k", action="store_true",
+                    help="skip the BASELINE configs[1] leg (B8 H16 T2048 fwd+bwd and its SDPA comparator)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (3 times): the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -558,6 +562,42 @@ def bench_lm(args, dev):
     return res
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo), reported with every
+    CPU baseline."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def bench_train2k(args, dev):
+    """the operator's fwd+bwd at B8 H16 T2048 d64 bf16,
+    timed like the headline step, with torch SDPA flash fwd+bwd at the same
+    shape beside it."""
+    sub = argparse.Namespace(**vars(args))
+    sub.workload = "train2k"
+    tr = bench_training(sub, dev)
+    res = {"ms_per_step": round(tr["ms"], 4), "ms_per_step_median": round(tr["ms_median"], 4),
+           "value": round(tr["value"], 2), "unit": "TFLOP/s",
+           "pct_of_peak": round(100.0 * tr["value"] / PEAK_BF16_TFLOPS, 2),
+           "config": "operator fwd+bwd B8 H16 T2048 d64 bf16 (BASELINE configs[1])",
+           "kernels": tr["kernels"]}
+    if not args.no_sdpa:
+        try:
+            sd = bench_sdpa(args, tr["inputs"])
+            sd["ratio_dilution_over_sdpa"] = round(tr["value"] / sd["value"], 3)
+            res["sdpa"] = sd
+        except Exception as exc:  # backend unavailable: report, do not fall back
+            res["sdpa"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
+    del tr["inputs"]
+    return res
+
+
 def cpu_baseline(shape):
     """The fp32 CPU oracle, fwd+bwd through torch autograd, on one (batch,
     head) slice of the workload (the slices are independent and identical in
@@ -582,7 +622,7 @@ def cpu_baseline(shape):
     flops = 7.0 * seq * seq * d
     log(f"cpu baseline: one slice T={seq} fwd+bwd in {dt:.2f} s on {threads} threads")
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port", "seconds": round(dt, 2),
+            "cpu_model": cpu_model(), "kind": "port", "seconds": round(dt, 2),
             "sample": f"fp32 torch-eager oracle fwd+bwd on 1 of {shape[0] * shape[1]} (batch, head) "
                       f"slices, T={seq} d={d}"}
 
@@ -611,8 +651,8 @@ def cpu_decode_baseline(context, d, slices=16):
     dt = (time.perf_counter() - t0) / reps
     gbs = slices * context * (4 * d + 8) / dt / 1e9
     log(f"cpu decode baseline: {slices} slices at L={context} in {dt * 1e3:.1f} ms on {threads} threads")
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "seconds": round(dt, 4),
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "cpu_model": cpu_model(),
+            "kind": "port", "seconds": round(dt, 4),
             "sample": f"fp32 torch-eager oracle decode step on {slices} (batch, head) slices at "
                       f"L={context} d={d} (float32 copies of bf16 caches)"}
 
@@ -679,6 +719,10 @@ def main() -> int:
             line["sdpa"] = sd
         except Exception as exc:  # backend unavailable: report, do not fall back
             line["sdpa"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
+    if not args.no_train2k and args.workload != "train2k":
+        torch.cuda.empty_cache()
+        line["train2k"] = bench_train2k(args, dev)
+        torch.cuda.empty_cache()
     if not args.no_variants:
         line["variants"] = bench_variants(args, dev, tr["inputs"])
         torch.cuda.empty_cache()

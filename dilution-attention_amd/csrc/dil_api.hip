@@ -13,6 +13,12 @@ bool valid_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 bool valid_dtype(int t) { return t == 0 || t == 1 || t == 2; }
 bool valid_precision(int p) { return p == 0 || p == 1 || p == 2; }
 
+// True when every pointer is non-null (a required argument).
+template <typename... Ps>
+bool all_set(const Ps*... ps) {
+  return ((ps != nullptr) && ...);
+}
+
 }  // namespace
 
 namespace dil {
@@ -28,7 +34,7 @@ int check_variant(const Variant& v, int head_dim) {
 
 extern "C" {
 
-int dil_abi_version(void) { return 1; }
+int dil_abi_version(void) { return 2; }
 
 const char* dil_status_string(int status) {
   switch (status) {
@@ -53,11 +59,15 @@ int64_t dil_decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
 
 int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_cache,
                             float* committed, void* out, int64_t n, int64_t capacity,
-                            int64_t length, int head_dim, int dtype, int bid, int share,
-                            float shift, void* workspace, int64_t workspace_bytes, void* stream) {
+                            int64_t length, int head_dim, int dtype, int q_dtype, int bid,
+                            int share, float shift, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
   if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
-  if (!valid_dtype(dtype)) return dil::kErrDtype;
+  if (!valid_dtype(dtype) || !valid_dtype(q_dtype)) return dil::kErrDtype;
   if (n < 1 || length < 1 || length > capacity) return dil::kErrShape;
+  if (!all_set(q1, k_cache, v_cache, static_cast<const void*>(committed), static_cast<const void*>(out),
+               static_cast<const void*>(workspace)))
+    return dil::kErrShape;
   if (workspace_bytes < dil::decode_workspace_bytes(n, length, head_dim)) return dil::kErrWorkspace;
   dil::DecodeArgs a{};
   a.q1 = q1;
@@ -75,6 +85,7 @@ int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_c
   a.length = length;
   a.head_dim = head_dim;
   a.dtype = dtype;
+  a.q_dtype = q_dtype;
   a.var = dil::Variant{bid, share, shift};
   a.stream = stream;
   return dil::decode_step(a);
@@ -82,9 +93,10 @@ int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_c
 
 int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, float* committed,
                     void* out, int64_t n, int64_t capacity, int64_t length, int head_dim,
-                    int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+                    int dtype, int q_dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   return dil_decode_step_variant(q1, k_cache, v_cache, committed, out, n, capacity, length,
-                                 head_dim, dtype, 0, 1, 1.f, workspace, workspace_bytes, stream);
+                                 head_dim, dtype, q_dtype, 0, 1, 1.f, workspace, workspace_bytes,
+                                 stream);
 }
 
 int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
@@ -101,6 +113,11 @@ int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, 
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
   if (n < 1 || seq < 1) return dil::kErrShape;
+  if (!all_set(q, k, v, static_cast<const void*>(out), static_cast<const void*>(rmax),
+               static_cast<const void*>(rden), static_cast<const void*>(ssum),
+               static_cast<const void*>(carry), static_cast<const void*>(committed_total),
+               static_cast<const void*>(workspace)))
+    return dil::kErrShape;
   if (workspace_bytes <
       dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision == 2, pk != nullptr))
     return dil::kErrWorkspace;
@@ -158,6 +175,11 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
   if (n < 1 || chunk < 1 || start < 0 || start + chunk > capacity) return dil::kErrShape;
+  if (!all_set(q_chunk, k_cache, v_cache, static_cast<const void*>(committed),
+               static_cast<const void*>(out), static_cast<const void*>(rmax),
+               static_cast<const void*>(rden), static_cast<const void*>(ssum),
+               static_cast<const void*>(carry), static_cast<const void*>(workspace)))
+    return dil::kErrShape;
   if (workspace_bytes <
       dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision == 2, 0))
     return dil::kErrWorkspace;
@@ -206,7 +228,12 @@ int dil_backward_variant(const void* q, const void* k, const void* v, const void
   if (!valid_dtype(dtype) || !valid_dtype(dout_dtype) || !valid_dtype(grad_dtype))
     return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
-  if (n < 1 || seq < 1 || pk == nullptr) return dil::kErrShape;
+  if (n < 1 || seq < 1) return dil::kErrShape;
+  if (!all_set(q, k, v, dout, static_cast<const void*>(out), static_cast<const void*>(rmax),
+               static_cast<const void*>(rden), static_cast<const void*>(ssum),
+               static_cast<const void*>(carry), static_cast<const void*>(pk), dq, dk, dv,
+               static_cast<const void*>(workspace)))
+    return dil::kErrShape;
   if (workspace_bytes < dil::backward_workspace_bytes(n, seq, head_dim, dtype, precision == 2))
     return dil::kErrWorkspace;
   dil::BackwardArgs a{};

@@ -15,6 +15,10 @@
 //   dec_finish (n):          out = sum(share * v) / (sum(share) + eps) in the
 //                            query dtype (chunk partials summed in chunk order)
 //
+// q1 is read in its own dtype and the output stored in it, whatever the
+// caches' dtype (the reference loads q1 as fp32 and stores into q1.dtype,
+// kernels.py:953, 1029).
+//
 // HBM bytes per key: K and V rows (2*D*elt) + demand read+write (8) + AFF
 // write+read (8).  K and V are streamed once with 16-byte non-temporal loads.
 #pragma once
@@ -84,7 +88,7 @@ __device__ __forceinline__ void load8_stream(const void* base, int64_t idx, floa
 // units; none for the elementwise bids.
 template <int D, int DT, int BID = BID_SOFTMAX>
 __global__ __launch_bounds__(kDecThreads) void dec_stats(
-    const void* __restrict__ q1, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
+    const void* __restrict__ q1, int qdt, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
     float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
     float qscale, int64_t slice0) {
   using L = DecLayout<D>;
@@ -96,7 +100,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_stats(
   const int64_t j1 = min(j0 + chunk, length);
 
   float q[8];
-  load8_f32(q1, slice * q_sn + sub * 8, DT, q);
+  load8_f32(q1, slice * q_sn + sub * 8, qdt, q);        // q1 in its own dtype, as fp32
 #pragma unroll
   for (int e = 0; e < 8; ++e) q[e] *= qscale;
 
@@ -340,7 +344,8 @@ int launch_decode(const DecodeArgs& a) {
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("dec_stats", st,
               (dec_stats<D, DT, BID><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
-                  a.q1, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length, chunk, nchunk, qscale, s0)));
+                  a.q1, a.q_dtype, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length, chunk, nchunk,
+                  qscale, s0)));
   });
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("dec_apply", st,
@@ -350,7 +355,7 @@ int launch_decode(const DecodeArgs& a) {
   });
   DIL_TIMED("dec_finish", st,
             dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
-                                                                             a.o_sn, a.dtype));
+                                                                             a.o_sn, a.q_dtype));
   return static_cast<int>(hipGetLastError());
 }
 

@@ -395,10 +395,9 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 4 : 2) voi
     run += static_cast<double>(cp.lo + cp.hi);
   };
 
-  // blocks that end before this wave's first key take nothing from it: their
-  // checkpoints are the incoming demand, which is zero for these keys
-  if (h == 0 && key_ok)
-    for (int64_t b = 0; b < b_w; ++b) ccol[b * P.Tk] = 0.f;
+  // Blocks that end before this wave's first key never see it: their
+  // checkpoints for these keys (the future triangle) are left unwritten, as
+  // the reference leaves them (kernels.py:353-354), and no kernel reads them.
   if (b_wg < nb) {
     fetch(b_wg);
     stash(0);

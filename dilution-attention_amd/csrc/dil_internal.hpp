@@ -63,19 +63,20 @@ class LaunchTimer {
   } while (0)
 
 struct DecodeArgs {
-  const void* q1;        // (n, D) rows, slice stride q_sn elements
+  const void* q1;        // (n, D) rows in `q_dtype`, slice stride q_sn elements
   int64_t q_sn;
   const void* k_cache;   // (n, cap, D), slice stride kv_sn elements
   const void* v_cache;
   int64_t kv_sn;
   float* committed;      // (n, cap) fp32, slice stride c_sn
   int64_t c_sn;
-  void* out;             // (n, D) in `dtype`, slice stride o_sn
+  void* out;             // (n, D) in `q_dtype`, slice stride o_sn
   int64_t o_sn;
   void* workspace;
   int64_t workspace_bytes;
   int64_t n, length;
-  int head_dim, dtype;
+  int head_dim, dtype;   // dtype: the caches'
+  int q_dtype;           // q1's and the output's
   Variant var;
   void* stream;
 };

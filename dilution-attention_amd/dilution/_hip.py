@@ -41,11 +41,11 @@ SIGNATURES = {
                                       _c_int, _c_int, ctypes.c_float,
                                       _vp, _vp, _vp, _vp, _c_int64, _vp]),
     "dil_decode_step_variant": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64,
-                                         _c_int, _c_int, _c_int, _c_int, ctypes.c_float,
+                                         _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_float,
                                          _vp, _c_int64, _vp]),
     "dil_decode_workspace_bytes": (_c_int64, [_c_int64, _c_int64, _c_int]),
     "dil_decode_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _c_int,
-                                 _c_int, _vp, _c_int64, _vp]),
+                                 _c_int, _c_int, _vp, _c_int64, _vp]),
     "dil_timing_enable": (_c_int, [_c_int]),
     "dil_timing_reset": (_c_int, []),
     "dil_timing_count": (_c_int, []),
@@ -53,7 +53,7 @@ SIGNATURES = {
                                  ctypes.POINTER(_c_int64)]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _load_error: str | None = None

@@ -166,7 +166,9 @@ def dilution_attention_forward(
     prefix), as the reference's aux dict: ``pk, rmax, rden, carry, ssum,
     bwd_block_m, block_m, block_n, dot_precision, num_warps,
     committed_total``.  ``carry`` holds the demand entering every 32-row block
-    (``bwd_block_m`` = 32).  Without return_aux the (batch, head) slices are
+    (``bwd_block_m`` = 32) for the block's causal keys ``j < 32 (b + 1)``; the
+    entries past them are left unwritten, as in the reference
+    (kernels.py:353-354; its tests read ``carry[:, b, :end]`` only).  Without return_aux the (batch, head) slices are
     processed in groups sized so the (rows, T/32, T) fp32 checkpoint scratch
     stays under scratch_budget_gib; slices are independent, so results are
     identical.
@@ -417,11 +419,14 @@ def dilution_decode_step(
     kf = k_cache.view(n, capacity, head_dim)
     vf = v_cache.view(n, capacity, head_dim)
     cf = committed.view(n, capacity)
-    qf = q1.reshape(n, head_dim).to(dt).contiguous()
-    out = torch.empty(n, head_dim, device=q1.device, dtype=dt)
+    # q1 keeps its own dtype: the kernels read it as fp32 and store the
+    # output in it (kernels.py:953, 1029)
+    qdt = q1.dtype if q1.dtype in _DTYPES else torch.float32
+    qf = q1.reshape(n, head_dim).to(qdt).contiguous()
+    out = torch.empty(n, head_dim, device=q1.device, dtype=qdt)
     ws = _workspace(lib.dil_decode_workspace_bytes(n, length, head_dim), q1.device)
     head = (qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), cf.data_ptr(), out.data_ptr(), n,
-            capacity, length, head_dim, _DTYPES[dt])
+            capacity, length, head_dim, _DTYPES[dt], _DTYPES[qdt])
     tail = (ws.data_ptr(), ws.numel(), _stream(q1.device))
     with torch.cuda.device(q1.device):
         if tuple(_variant) == _PRODUCTION:

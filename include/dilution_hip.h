@@ -22,7 +22,10 @@
  *     Scratch memory is caller-provided (`workspace`, at least the size the
  *     matching *_workspace_bytes query returns, 256-byte aligned).
  *   - Return value: 0 on success, a positive hipError_t from the launch, or a
- *     negative argument error (see dil_status_string).
+ *     negative argument error (see dil_status_string).  A NULL pointer where
+ *     an argument is required is an argument error (-4); only `pk` of
+ *     dil_forward may be NULL.  Argument errors are returned before any
+ *     launch.
  */
 #ifndef DILUTION_HIP_H
 #define DILUTION_HIP_H
@@ -51,7 +54,10 @@ const char* dil_status_string(int status);
  *            with a_ij = log2(e) * q_i.k_j / sqrt(head_dim).
  * ssum:      (n, seq) float32 row sums of the shares.
  * carry:     (n, ceil(seq/32), seq) float32; carry[:, b, j] = sum of p_ij over
- *            rows i < 32*b (the demand checkpoint at every 32-row block).
+ *            rows i < 32*b (the demand checkpoint at every 32-row block),
+ *            written for the block's causal keys j < 32*(b+1) only: the
+ *            future triangle is left unwritten and never read (as the
+ *            reference leaves it, kernels.py:353-354, test_kernels.py:143-149).
  * committed_total: (n, seq) float32 column totals of p (the decode demand).
  * pk:        (n, seq, head_dim) float32 (p @ k)/sqrt(head_dim), or NULL.
  */
@@ -77,7 +83,8 @@ int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t 
  *            [0, start+chunk) holds the demand of rows < start+chunk.  Entries
  *            at and beyond start+chunk are not touched.
  * out:       (n, chunk, head_dim) float32.
- * rmax, rden, ssum: (n, chunk) float32; carry: (n, ceil(chunk/32), start+chunk).
+ * rmax, rden, ssum: (n, chunk) float32; carry: (n, ceil(chunk/32), start+chunk),
+ *            written for keys j < start + 32*(b+1) of block b only.
  */
 int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
                                     int dtype, int precision);
@@ -110,18 +117,20 @@ int dil_backward(const void* q, const void* k, const void* v, const void* dout,
  * Cached decode step.  Replaces dilution_decode_step
  * (src/dilution/kernels.py:994-1038) and _dilution_decode (:937-991).
  *
- * q1:        (n, head_dim) in `dtype` (the new row).
+ * q1:        (n, head_dim) in `q_dtype` (the new row), read as fp32.
  * k_cache, v_cache: (n, capacity, head_dim) in `dtype`; rows [0, length) valid,
  *            the new token written at length-1.
  * committed: (n, capacity) float32 column totals of p over earlier rows, with
  *            committed[:, length-1] == 0.  Advanced in place over [0, length)
  *            to include this row; [length, capacity) is never touched.
- * out:       (n, head_dim) in `dtype`.
+ * out:       (n, head_dim) in `q_dtype` (kernels.py:953, 1029: q1 loaded in
+ *            its own dtype, the output stored in it).
  */
 int64_t dil_decode_workspace_bytes(int64_t n, int64_t length, int head_dim);
 int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, float* committed,
                     void* out, int64_t n, int64_t capacity, int64_t length, int head_dim,
-                    int dtype, void* workspace, int64_t workspace_bytes, void* stream);
+                    int dtype, int q_dtype, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /*
  * Operator variants: the bid and share ablations.  Replace the entry points of
@@ -156,8 +165,9 @@ int dil_backward_variant(const void* q, const void* k, const void* v, const void
                          void* dv, void* workspace, int64_t workspace_bytes, void* stream);
 int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_cache,
                             float* committed, void* out, int64_t n, int64_t capacity,
-                            int64_t length, int head_dim, int dtype, int bid, int share,
-                            float shift, void* workspace, int64_t workspace_bytes, void* stream);
+                            int64_t length, int head_dim, int dtype, int q_dtype, int bid,
+                            int share, float shift, void* workspace, int64_t workspace_bytes,
+                            void* stream);
 
 /*
  * Kernel timing for measurement harnesses.  No reference counterpart (the

@@ -18,6 +18,7 @@ code written for this repository:
   prefill demand hand-off       /root/reference/src/dilution/model.py:198-229
   backward decomposition        /root/reference/docs/kernels.md:62-84,
                                 /root/reference/src/dilution/kernels.py:678-775
+  row-blocked reverse walk      /root/reference/src/dilution/kernels.py:736-770
   bid / share variants          /root/reference/src/dilution/kernels_bid.py:4-42,
                                 :94-165 (bids, share modes), :853-960 (decode)
 
@@ -36,6 +37,11 @@ own formula; see tests/test_oracle.py):
   demand_totals, carry    harmonic closed form H_T - H_j; fp64 loop sums.
   grads_autograd          torch.autograd.gradcheck (finite differences, fp64).
   grads_closed_form_f64   autograd through attention_fp32 at fp64.
+  grads_blocked_f64       grads_closed_form_f64 at ragged lengths and block
+                          sizes (and, through it, autograd); the key-shift
+                          identity sum_j dk_j = 0; planted mistakes (the
+                          demand or the suffix not carried across blocks)
+                          that must fail the comparison.
   decode_step             the full-sequence rows of attention_loops_f64, token
                           after token, and the demand == column sums.
   prefill_chunk           the full-sequence rows and demand == column sums.
@@ -337,6 +343,90 @@ def grads_closed_form_f64(q, k, v, dout):
     dv = np.matmul(np.swapaxes(attn, -1, -2), do)
     inter = dict(p=p, committed=c, ssum=ssum[..., 0], dbar=dbar[..., 0], ghat=ghat[..., 0],
                  suffix=suffix, out=o)
+    return (dq, dk, dv), inter
+
+
+def grads_blocked_f64(q, k, v, dout, block: int = 512, mutant: str | None = None):
+    """Backward of one (batch, head) slice at any length, float64, in row
+    blocks: q, k, v, dout (T, D) -> ((dq, dk, dv), intermediates).
+
+    The same decomposition as grads_closed_form_f64 (docs/kernels.md:62-84),
+    evaluated the way the reference's backward walks it
+    (src/dilution/kernels.py:736-770): a forward sweep over row blocks that
+    carries the column demand and records the demand entering each block, then
+    a reverse sweep over the blocks that carries, per key, the suffix
+    U_j = sum over later rows i' of ds_i'j p_i'j / (c_i'j + p_i'j + eps)^2.
+    Memory is O(block T) instead of O(T^2), which makes gradient parity at
+    T = 16384 affordable on host cores.  Runs on the device of the inputs
+    (torch ops only), so a test may evaluate it in float64 on the GPU where
+    the host would take too long.
+
+    Intermediates: out, lse (natural log-sum-exp per row), ssum, ghat and the
+    demand totals.  `mutant` plants a named mistake for the tests that show
+    the pins catch it: "no_suffix_carry" drops the suffix carried between
+    blocks, "no_demand_carry" the demand carried into each block.
+    """
+    dev = q.device if isinstance(q, torch.Tensor) else torch.device("cpu")
+    q, k, v, do = (torch.as_tensor(x).to(device=dev, dtype=torch.float64) for x in (q, k, v, dout))
+    t, d = q.shape
+    sc = 1.0 / math.sqrt(d)
+    nb = (t + block - 1) // block
+    kt, vt = k.T.contiguous(), v.T.contiguous()      # right operands stored, not transposed views
+    lse = torch.empty(t, dtype=torch.float64, device=dev)
+    ssum = torch.empty(t, dtype=torch.float64, device=dev)
+    out = torch.empty(t, v.shape[1], dtype=torch.float64, device=dev)
+    carry = torch.zeros(nb, t, dtype=torch.float64, device=dev)   # demand entering block b
+    demand = torch.zeros(t, dtype=torch.float64, device=dev)
+
+    def block_bids(r0, r1):
+        a = (q[r0:r1] @ kt[:, :r1]) * sc
+        rows = torch.arange(r0, r1, device=dev)[:, None]
+        keys = torch.arange(r1, device=dev)[None, :]
+        a = a.masked_fill(keys > rows, -math.inf)
+        m = a.max(dim=1, keepdim=True).values
+        ls = m[:, 0] + torch.log(torch.exp(a - m).sum(dim=1))
+        return torch.exp(a - ls[:, None]), ls
+
+    for b in range(nb):
+        r0, r1 = b * block, min(t, (b + 1) * block)
+        if mutant != "no_demand_carry":
+            carry[b] = demand
+        p, lse[r0:r1] = block_bids(r0, r1)
+        excl = carry[b, :r1] + torch.cumsum(p, dim=0) - p        # demand before each row
+        sh = p / (excl + p + EPS)
+        ssum[r0:r1] = sh.sum(dim=1)
+        out[r0:r1] = (sh / (ssum[r0:r1, None] + EPS)) @ v[:r1]
+        demand[:r1] += p.sum(dim=0)
+
+    dbar = (do * out).sum(dim=1)
+    dq = torch.zeros_like(q)
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    ghat = torch.empty(t, dtype=torch.float64, device=dev)
+    suffix = torch.zeros(t, dtype=torch.float64, device=dev)      # U entering from below
+    for b in reversed(range(nb)):
+        r0, r1 = b * block, min(t, (b + 1) * block)
+        a = (q[r0:r1] @ kt[:, :r1]) * sc
+        rows = torch.arange(r0, r1, device=dev)[:, None]
+        keys = torch.arange(r1, device=dev)[None, :]
+        causal = keys <= rows
+        p = torch.exp(a.masked_fill(~causal, -math.inf) - lse[r0:r1, None])
+        excl = carry[b, :r1] + torch.cumsum(p, dim=0) - p
+        inv = 1.0 / (excl + p + EPS)
+        sh = p * inv
+        sinv = 1.0 / (ssum[r0:r1, None] + EPS)
+        ds = ((do[r0:r1] @ vt[:, :r1] - dbar[r0:r1, None]) * sinv).masked_fill(~causal, 0.0)
+        g = ds * sh * inv                                          # ds p / (c + p + eps)^2
+        later = torch.flip(torch.cumsum(torch.flip(g, (0,)), dim=0), (0,)) - g
+        u = later + (0.0 if mutant == "no_suffix_carry" else suffix[:r1])
+        dp = (ds * (excl + EPS) * inv * inv - u).masked_fill(~causal, 0.0)
+        ghat[r0:r1] = (p * dp).sum(dim=1)
+        da = p * (dp - ghat[r0:r1, None])
+        dq[r0:r1] = (da @ k[:r1]) * sc
+        dk[:r1] += (da.T @ q[r0:r1]) * sc
+        dv[:r1] += (sh * sinv).T @ do[r0:r1]
+        suffix[:r1] += g.sum(dim=0)
+    inter = dict(out=out, lse=lse, ssum=ssum, ghat=ghat, totals=demand)
     return (dq, dk, dv), inter
 
 

@@ -126,3 +126,22 @@ def test_backward_grad_dtypes_follow_inputs():
     for x in xs:
         assert x.grad.dtype == torch.float16
         assert torch.isfinite(x.grad).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_backward_converted_operands_match_oracle(dtype, head_dim):
+    """fp32 or fp16 inputs with dot_precision="bf16": the backward converts q,
+    k, v (and dO) to bf16 operands in its preparation launch (the z = 3 job
+    picks V's copy).  Gradients against the closed-form oracle on the inputs
+    as given, within the bf16 bound; gradients come back in the input dtype."""
+    seq = 257
+    q, k, v, do = orc.make_inputs((1, 3, seq, head_dim), seed=31 + head_dim, qk_scale=0.5,
+                                  with_dout=True, dtype=dtype)
+    out, grads = _run(q, k, v, do, "bf16")
+    want, _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
+    assert max_abs(out, orc.attention_f64(q, k, v)) < 5e-2
+    for name, g, w in zip(("dq", "dk", "dv"), grads, want):
+        assert g.dtype == dtype, name
+        err = max_abs(g, torch.from_numpy(w))
+        assert err < 5e-2, f"{name} max abs err {err}"

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.dil_abi_version() == 1
+    assert lib.dil_abi_version() == 2
     assert lib.dil_status_string(0) == b"success"
     for code in (-1, -2, -3, -4, -5):
         assert lib.dil_status_string(code) != b"unknown status"
@@ -62,14 +62,51 @@ def test_workspace_queries(lib):
 
 def test_argument_errors_before_any_launch(lib):
     # invalid head_dim / dtype / precision / shapes are rejected on the host
-    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 48, 1, None, 0, None) == -1
-    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 64, 7, None, 0, None) == -2
-    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 9, 64, 1, None, 0, None) == -4
-    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 64, 1, None, 0, None) == -3
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 48, 1, 1, None, 0, None) == -1
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 64, 7, 1, None, 0, None) == -2
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 4, 64, 1, 5, None, 0, None) == -2
+    assert lib.dil_decode_step(None, None, None, None, None, 1, 8, 9, 64, 1, 1, None, 0, None) == -4
     assert lib.dil_forward(None, None, None, 1, 8, 64, 1, 9, None, None, None, None, None, None,
                            None, None, 0, None) == -5
     assert lib.dil_prefill_chunk(None, None, None, 1, 8, 4, 10, 64, 1, 2, None, None, None, None,
                                  None, None, None, 0, None) == -4
+
+
+def test_null_pointers_are_argument_errors(lib):
+    """A NULL where the header requires a buffer is a status (-4) returned
+    before any launch, never a device fault.  The stand-in addresses below are
+    never dereferenced: every call returns before launching."""
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(16)]
+    big = 1 << 40
+    # decode: each required pointer in turn
+    for hole in range(5):
+        ptrs = [None if i == hole else fake[i] for i in range(5)]
+        assert lib.dil_decode_step(*ptrs, 1, 8, 4, 64, 1, 1, fake[5], big, None) == -4, hole
+    assert lib.dil_decode_step(*fake[:5], 1, 8, 4, 64, 1, 1, None, big, None) == -4
+    # with every pointer set, the workspace size is the next check
+    assert lib.dil_decode_step(*fake[:5], 1, 8, 4, 64, 1, 1, fake[5], 0, None) == -3
+    # forward: pk may be NULL, nothing else may
+    fwd_ptrs = fake[:3]
+    outs = fake[3:9]                              # out, rmax, rden, ssum, carry, committed_total
+    for hole in range(6):
+        o = [None if i == hole else outs[i] for i in range(6)]
+        assert lib.dil_forward(*fwd_ptrs, 1, 8, 64, 1, 2, *o, None, fake[9], big, None) == -4, hole
+    assert lib.dil_forward(None, *fake[1:3], 1, 8, 64, 1, 2, *outs, None, fake[9], big, None) == -4
+    assert lib.dil_forward(*fwd_ptrs, 1, 8, 64, 1, 2, *outs, None, fake[9], 0, None) == -3
+    # backward: pk is required there
+    ins = fake[:10]                               # q k v dout out rmax rden ssum carry pk
+    for hole in range(10):
+        a = [None if i == hole else ins[i] for i in range(10)]
+        assert lib.dil_backward(*a, 1, 8, 64, 1, 1, 1, 2, *fake[10:13], fake[13], big, None) == -4, hole
+    for hole in range(3):
+        g = [None if i == hole else fake[10 + i] for i in range(3)]
+        assert lib.dil_backward(*ins, 1, 8, 64, 1, 1, 1, 2, *g, fake[13], big, None) == -4, hole
+    # prefill
+    pre = fake[:3]
+    rest = fake[3:9]                              # committed out rmax rden ssum carry
+    for hole in range(6):
+        r = [None if i == hole else rest[i] for i in range(6)]
+        assert lib.dil_prefill_chunk(*pre, 1, 8, 4, 16, 64, 1, 2, *r, fake[9], big, None) == -4, hole
 
 
 def test_python_layer_raises_without_gpu_tensors():

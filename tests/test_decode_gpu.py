@@ -89,3 +89,30 @@ def test_decode_argument_errors():
     with pytest.raises(ValueError):
         bad = torch.zeros(1, 1, 8, 48, device="cuda")
         kernels.dilution_decode_step(torch.zeros(1, 1, 1, 48, device="cuda"), bad, bad, com, 2)
+
+
+@pytest.mark.parametrize("qdt,cdt,tol", [(torch.float32, torch.bfloat16, 1e-4),
+                                         (torch.bfloat16, torch.float32, 2e-2),
+                                         (torch.float16, torch.bfloat16, 2e-3)])
+def test_decode_query_keeps_its_dtype(qdt, cdt, tol):
+    """q1 is read in its own dtype and the output stored in it, whatever the
+    caches hold (reference kernels.py:953, 1029).  An fp32 query over bf16
+    caches stays within the fp32 tolerance of the oracle on the same values:
+    nothing on the query side is rounded to bf16."""
+    from dilution import kernels
+
+    batch, heads, length, d = 2, 3, 3000, 64
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(batch, heads, 1, d, generator=g).to(qdt)
+    kc = torch.randn(batch, heads, length + 4, d, generator=g).to(cdt)
+    vc = torch.randn(batch, heads, length + 4, d, generator=g).to(cdt)
+    com = torch.rand(batch, heads, length + 4, generator=g) * 3.0
+    com[..., length - 1:] = 0.0
+    out_ref, com_ref = orc.decode_step(q, kc, vc, com, length)     # fp64 of the given values
+    comg = com.cuda()
+    out = kernels.dilution_decode_step(q.cuda(), kc.cuda(), vc.cuda(), comg, length)
+    assert out.dtype == qdt
+    err = max_abs(out, out_ref)
+    assert err < tol, err
+    assert max_abs(comg, com_ref) < 1e-5
+    assert comg[..., length:].abs().max().item() == 0

@@ -84,12 +84,95 @@ def test_checkpoints_totals_and_row_stats(seq):
     assert bm == 32
     carry = orc.carry_checkpoints(q, k, bm).reshape(2, -1, seq)
     assert aux["carry"].shape == carry.shape
-    assert max_abs(aux["carry"], carry) < 1e-5
+    for rb in range(carry.shape[1]):
+        # only the block's causal keys are written (test_kernels.py:143-149)
+        end = min((rb + 1) * bm, seq)
+        assert max_abs(aux["carry"][:, rb, :end], carry[:, rb, :end]) < 1e-5, rb
     rmax, rden = orc.row_stats(q, k)
     assert max_abs(aux["rmax"], rmax.reshape(2, seq)) < 1e-4
     lse_got = aux["rmax"].double().cpu() + torch.log2(aux["rden"].double().cpu())
     lse_want = (rmax + torch.log2(rden)).reshape(2, seq)
     assert (lse_got - lse_want).abs().max().item() < 1e-5
+
+
+def test_c1_exact_shape_fp32_forward():
+    """BASELINE config 1 as stated: B1 H4 T512 d64, q, k, v ~ N(0,1) fp32,
+    the reference's default ieee precision, scale 1/sqrt(d), eps 1e-9."""
+    from dilution import kernels
+
+    q, k, v = orc.make_inputs((1, 4, 512, 64), seed=1)
+    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda())
+    assert got.shape == (1, 4, 512, 64) and got.dtype == torch.float32
+    assert max_abs(got, orc.attention_f64(q, k, v)) < 1e-4
+    assert max_abs(got, orc.attention_fp32(q, k, v)) < 1e-4
+
+
+def _forward_into(q, k, v, carry, prec=2):
+    """dil_forward through the C ABI into a caller-owned carry buffer."""
+    from dilution import _hip
+
+    lib = _hip.lib()
+    n, t, d = q.shape
+    f32 = dict(device=q.device, dtype=torch.float32)
+    out = torch.empty(n, t, d, **f32)
+    stats = [torch.empty(n, t, **f32) for _ in range(4)]        # rmax rden ssum total
+    dt = {torch.float32: 0, torch.bfloat16: 1}[q.dtype]
+    ws = torch.empty(lib.dil_forward_workspace_bytes(n, t, d, dt, prec, 0), dtype=torch.uint8,
+                     device=q.device)
+    status = lib.dil_forward(q.data_ptr(), k.data_ptr(), v.data_ptr(), n, t, d, dt, prec,
+                             out.data_ptr(), stats[0].data_ptr(), stats[1].data_ptr(),
+                             stats[2].data_ptr(), carry.data_ptr(), stats[3].data_ptr(), None,
+                             ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    _hip.check(status, "dil_forward")
+    return out, stats
+
+
+@pytest.mark.parametrize("seq", [1, 65, 257, 1025])
+def test_carry_future_triangle_unwritten_and_unread(seq):
+    """The forward neither writes nor reads the carry checkpoints past each
+    block's causal keys (the reference's hygiene check, test_kernels.py:21-43,
+    143-149): a carry buffer poisoned with NaN gives bit-identical outputs,
+    the causal part is written, and the future triangle still holds NaN."""
+    q, k, v = (t.reshape(2, seq, 64).cuda() for t in
+               orc.make_inputs((1, 2, seq, 64), seed=seq, dtype=torch.bfloat16))
+    nb = (seq + 31) // 32
+    clean = torch.zeros(2, nb, seq, device="cuda")
+    poisoned = torch.full((2, nb, seq), float("nan"), device="cuda")
+    out_a, st_a = _forward_into(q, k, v, clean)
+    out_b, st_b = _forward_into(q, k, v, poisoned)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    for a, b in zip(st_a, st_b):
+        assert torch.equal(a, b)
+    rows = torch.arange(nb, device="cuda")[:, None]
+    keys = torch.arange(seq, device="cuda")[None, :]
+    future = (keys >= 32 * (rows + 1)).expand(2, nb, seq)
+    assert torch.equal(poisoned[~future], clean[~future])
+    assert torch.isnan(poisoned[future]).all()
+
+
+def test_backward_ignores_carry_future_triangle():
+    """The backward reads only the causal checkpoints: NaN written into the
+    future triangle of the saved carry leaves every gradient bit-identical."""
+    from dilution import kernels
+
+    seq = 300
+    q, k, v, do = orc.make_inputs((1, 2, seq, 64), seed=5, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    qg, kg, vg, dog = (t.cuda() for t in (q, k, v, do))
+    out, aux = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True,
+                                                  _save_pk=True)
+    saved = [qg, kg, vg, out, aux["rmax"], aux["rden"], aux["carry"], aux["ssum"], aux["pk"]]
+    clean = kernels._backward(saved, dog, "bf16", kernels._PRODUCTION)
+    nb = aux["carry"].shape[1]
+    rows = torch.arange(nb, device="cuda")[:, None]
+    keys = torch.arange(seq, device="cuda")[None, :]
+    poisoned = aux["carry"].clone()
+    poisoned[(keys >= 32 * (rows + 1)).expand_as(poisoned)] = float("nan")
+    saved[6] = poisoned
+    dirty = kernels._backward(saved, dog, "bf16", kernels._PRODUCTION)
+    for a, b in zip(clean, dirty):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("head_dim", [16, 32, 64, 128])

@@ -6,14 +6,25 @@ every slice.
 * C3, B1 H16 T16384 d64 bf16 (q, k ~ 0.5 N(0,1), v, dO ~ N(0,1)):
   - output rows of slices 0 and 15 against ``attention_blocked_f64`` on the
     bf16-rounded inputs (2e-2 max-abs, 1e-2 mean-rel: the bf16 bounds);
+  - dq, dk, dv of slices 0 and 15 against the row-blocked fp64 backward
+    ``grads_blocked_f64`` on the host (5e-2 max-abs), and of all 16 slices
+    against the same function evaluated in float64 on the device;
   - the first 4096 rows are bit-identical to the forward of the 4096-token
     prefix (causality, test_model.py:46-56);
   - rows of the attention matrix sum to one, so sum_j dv_j = sum_i dO_i.  The
     kernel rounds the share tile, dO / (S + eps) and dv to bf16 (relative
     error <= 2^-9 each), which bounds the gap by 2^-8 (sum |dv| + sum |dO|).
-* The same shape in fp32 operands: sum_j dk_j = 0 (adding a constant to every
-  key leaves each softmax row unchanged) within 1e-4 of sum_j |dk_j|, and the
-  dv identity within 1e-5.
+* The same shape in fp32 operands: outputs and dq, dk, dv of slices 0 and 15
+  against ``grads_blocked_f64`` on the host and of every slice on the device
+  (1e-4 max-abs); sum_j dk_j = 0 (adding a constant to every key leaves each
+  softmax row unchanged) within 1e-4 of sum_j |dk_j|, and the dv identity
+  within 1e-5.
+* C2, B8 H16 T2048 d64 bf16 (128 slices, 16 per XCD: the packed longest-first
+  dispatch): outputs and gradients of every slice against
+  ``grads_blocked_f64`` on the device, four slices on the host.
+* T = 131072, one slice, bf16: outputs and gradients of every row and key
+  against ``grads_blocked_f64`` in float64 on the device, with the middle
+  4096 rows and keys reported on their own; and the far end in closed form.
 * C4, B16 H16 d64 bf16: a 16384-token prompt prefilled in 8 chunks of 2048,
   then 256 decode steps to 16640.  Prefill rows, decode rows and the demand
   equal the one-call forward of all 16640 rows (2e-2 on bf16 outputs, 1e-5
@@ -44,6 +55,20 @@ def _blocked(q, k, v):
     return torch.from_numpy(out), torch.from_numpy(tot)
 
 
+def _grads_oracle(q, k, v, do, sl, device, block=1024):
+    """((dq, dk, dv), intermediates) of one slice sl = (b, h) from the
+    row-blocked fp64 backward on `device` (the host, or the GPU where the host
+    would take minutes); inputs are the bf16-rounded / fp32 values upcast."""
+    args = [t[sl].to(device=device, dtype=torch.float64) for t in (q, k, v, do)]
+    return orc.grads_blocked_f64(*args, block=block)
+
+
+def _check_grads(got, want, tol, where):
+    for name, g, w in zip(("dq", "dk", "dv"), got, want):
+        err = (g.double().cpu() - w.cpu()).abs().max().item()
+        assert err < tol, f"{where} {name} max abs err {err}"
+
+
 def test_c3_training_bf16_full_size():
     from dilution import kernels
 
@@ -68,18 +93,66 @@ def test_c3_training_bf16_full_size():
     bound = 2.0 ** -8 * (dv.abs().sum(2) + dod.abs().sum(2))
     assert (gap <= bound).all(), (gap / bound).max().item()
 
+    grads = [x.grad for x in xs]
+    for h in range(16):
+        want, inter = _grads_oracle(q, k, v, do, (0, h), "cuda")
+        _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (device oracle)")
+    for h in (0, 15):
+        want, _ = _grads_oracle(q, k, v, do, (0, h), "cpu")
+        _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (host oracle)")
 
-def test_c3_training_fp32_key_shift_invariance():
+
+def test_c3_training_fp32_full_size():
     from dilution import kernels
 
     q, k, v, do = orc.make_inputs((1, 16, 16384, 64), seed=3, qk_scale=0.5, with_dout=True)
     xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
-    kernels.dilution_attention(*xs, dot_precision="ieee").backward(do.cuda())
+    out = kernels.dilution_attention(*xs, dot_precision="ieee")
+    out.backward(do.cuda())
+    out = out.detach()
+    grads = [x.grad for x in xs]
+    for h in range(16):
+        want, inter = _grads_oracle(q, k, v, do, (0, h), "cuda")
+        assert max_abs(out[0, h], inter["out"]) < 1e-4, h
+        _check_grads([g[0, h] for g in grads], want, 1e-4, f"slice {h} (device oracle)")
+    for h in (0, 15):
+        want, inter = _grads_oracle(q, k, v, do, (0, h), "cpu")
+        assert max_abs(out[0, h], inter["out"]) < 1e-4, h
+        _check_grads([g[0, h] for g in grads], want, 1e-4, f"slice {h} (host oracle)")
     dk = xs[1].grad.double().cpu()
     assert (dk.sum(2).abs() <= 1e-4 * dk.abs().sum(2)).all()
     dv = xs[2].grad.double().cpu()
     gap = (dv.sum(2) - do.double().sum(2)).abs()
     assert (gap <= 1e-5 * (dv.abs().sum(2) + do.double().abs().sum(2))).all()
+
+
+def test_c2_training_bf16_every_slice():
+    """B8 H16 T2048 d64 bf16, q, k ~ 0.5 N(0,1), v, dO ~
+    N(0,1).  128 slices put 16 on each XCD, the shape that dispatches every
+    XCD's slices longest first (packed across slices)."""
+    from dilution import kernels
+
+    q, k, v, do = orc.make_inputs((8, 16, 2048, 64), seed=21, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="bf16")
+    out.backward(do.cuda())
+    out = out.detach()
+    grads = [x.grad for x in xs]
+    worst = 0.0
+    for b in range(8):
+        for h in range(16):
+            want, inter = _grads_oracle(q, k, v, do, (b, h), "cuda", block=512)
+            assert max_abs(out[b, h], inter["out"]) < 2e-2, (b, h)
+            assert mean_rel(out[b, h], inter["out"]) < 1e-2, (b, h)
+            _check_grads([g[b, h] for g in grads], want, 5e-2, f"slice {(b, h)}")
+            worst = max(worst, max((g[b, h].double().cpu() - w.cpu()).abs().max().item()
+                                   for g, w in zip(grads, want)))
+    for sl in ((0, 0), (3, 7), (5, 2), (7, 15)):
+        want, inter = _grads_oracle(q, k, v, do, sl, "cpu", block=512)
+        assert max_abs(out[sl], inter["out"]) < 2e-2, sl
+        _check_grads([g[sl] for g in grads], want, 5e-2, f"slice {sl} (host oracle)")
+    print(f"C2 worst gradient error {worst:.3e}")
 
 
 def test_c4_chunked_prefill_then_256_decode_steps():
@@ -153,6 +226,31 @@ def test_decode_at_128k_context():
         want64, want_com = orc.decode_step(q1[sl].cpu(), kc[sl].cpu(), vc[sl].cpu(), before[sl].cpu(), length)
         assert max_abs(out[sl], want64) < 2e-2
         assert max_abs(com[sl][..., :length], want_com[..., :length]) < 1e-5 * 4.0
+
+
+def test_sequence_of_131072_gradients_against_blocked_oracle():
+    """One slice at T = 131072 (bf16): every output row and every dq, dk, dv
+    row against the row-blocked fp64 oracle evaluated on the device (the host
+    would take hours), the middle 4096 rows / keys reported on their own --
+    the suffix checkpoints and the row pass at 4096 row tiles, far past the
+    benchmark's sizes."""
+    from dilution import kernels
+
+    seq, d = 131072, 64
+    q, k, v, do = orc.make_inputs((1, 1, seq, d), seed=8, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="bf16")
+    out.backward(do.cuda())
+    out = out.detach()
+    grads = [x.grad[0, 0] for x in xs]
+    torch.cuda.synchronize()
+    want, inter = _grads_oracle(q, k, v, do, (0, 0), "cuda", block=2048)
+    assert max_abs(out[0, 0], inter["out"]) < 2e-2
+    assert mean_rel(out[0, 0], inter["out"]) < 1e-2
+    mid = slice(seq // 2 - 2048, seq // 2 + 2048)
+    _check_grads([g[mid] for g in grads], [w[mid] for w in want], 5e-2, "middle rows / keys")
+    _check_grads(grads, want, 5e-2, "all rows / keys")
 
 
 def test_sequence_of_131072_far_end_closed_forms():

@@ -97,7 +97,11 @@ def test_gpu_forward_fixture(prec):
     if prec == "ieee":
         assert max_abs(out, t(g["out"])) < 1e-4
         assert max_abs(aux["committed_total"], t(g["committed_total"])) < 1e-5
-        assert max_abs(aux["carry"].reshape(g["carry"].shape), t(g["carry"])) < 1e-5
+        carry = aux["carry"].reshape(g["carry"].shape)
+        nb, seq = carry.shape[-2:]
+        for rb in range(nb):                 # the written (causal) keys of each block
+            end = min(32 * (rb + 1), seq)
+            assert max_abs(carry[..., rb, :end], t(g["carry"])[..., rb, :end]) < 1e-5, rb
         assert max_abs(aux["pk"].reshape(g["pk"].shape), t(g["pk"])) < 2e-5
     else:
         # bf16 operands on bf16-rounded inputs: compare with the oracle on the

@@ -237,3 +237,106 @@ def test_continuation_nll_matches_full_forward():
             logits, _ = model(seq[:, :-1], seq[:, 1:])
         want = torch.nn.functional.cross_entropy(logits[0, -len(c):].float(), seq[0, -len(c):])
         assert abs(got[r] - want.item()) < 1e-4, r
+
+
+# --- the production operator against its specification --------------------
+
+def _spec_forward(q, k, v, dot_precision="ieee", return_aux=False, **_):
+    """The operator as the fp32 oracle states it (kernels.py:40-68), with the
+    demand totals a prefill hands to the decode cache."""
+    from oracle import dilution_oracle as orc
+
+    out = orc.attention_fp32(q.cpu(), k.cpu(), v.cpu()).to(q.device)
+    if return_aux:
+        return out, {"committed_total": orc.bids(q.float().cpu(), k.float().cpu()).sum(-2)
+                     .float().to(q.device)}
+    return out
+
+
+def _spec_decode(q1, k_cache, v_cache, committed, length, **_):
+    """The eager cached step (model.py:242-257), advancing the demand in place."""
+    from oracle import dilution_oracle as orc
+
+    out, com = orc.decode_step(q1.cpu(), k_cache.cpu(), v_cache.cpu(), committed.cpu(), length,
+                               dtype=torch.float64)
+    committed.copy_(com.float())
+    return out.to(device=q1.device, dtype=q1.dtype)
+
+
+@pytest.mark.gpu
+@needs_gpu
+@pytest.mark.parametrize("kinds", [None, ["dilution", "softmax"]])
+def test_production_model_matches_specification(kinds, monkeypatch):
+    """The model on the HIP operator against the same model on the operator's
+    specification (reference test_kernels.py:79-95, whose bound is 2e-2 for
+    tf32 noise; fp32 operands here)."""
+    from dilution import lm
+
+    model = _small(kinds=kinds)
+    g = torch.Generator().manual_seed(11)
+    idx = torch.randint(0, 97, (2, 96), generator=g).cuda()
+    with torch.no_grad():
+        fused = model.lm_head(model.ln_f(_hidden(model, idx)))
+        monkeypatch.setattr(lm.kernels, "dilution_attention_forward", _spec_forward)
+        spec = model.lm_head(model.ln_f(_hidden(model, idx)))
+    assert torch.isfinite(fused).all()
+    err = (fused - spec).abs().max().item()
+    assert err < 1e-4, err
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_production_cached_decode_matches_specification(monkeypatch):
+    """Prefill + cached decode on the HIP kernels against the eager cached
+    decode of the specification and against the full forward (reference
+    test_kernels.py:245-273)."""
+    from dilution import cache as dcache
+    from dilution import lm
+
+    model = _small(chunk=None)
+    g = torch.Generator().manual_seed(12)
+    tokens = torch.randint(0, 97, (2, 40), generator=g).cuda()
+    prefix = 24
+
+    def run():
+        logits, caches = model.prefill(tokens[:, :prefix], capacity=tokens.shape[1])
+        outs = [logits[:, -1]]
+        for pos in range(prefix, tokens.shape[1]):
+            outs.append(model.decode_step(tokens[:, pos:pos + 1], caches)[:, -1])
+        return torch.stack(outs, dim=1)
+
+    with torch.no_grad():
+        fused = run()
+        full = model.lm_head(model.ln_f(_hidden(model, tokens)))
+        monkeypatch.setattr(dcache.kernels, "dilution_attention_forward", _spec_forward)
+        monkeypatch.setattr(dcache.kernels, "dilution_decode_step", _spec_decode)
+        eager = run()
+    assert torch.isfinite(fused).all()
+    assert (fused - eager).abs().max().item() < 1e-4
+    assert (fused - full[:, prefix - 1:]).abs().max().item() < 1e-4
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_c5_training_step_full_size():
+    """BASELINE config 5's training step: 12 layers, d_model 1024, 16 heads of
+    64, SwiGLU 4x, RMSNorm, vocab 50304, no position encoding, bf16 weights
+    N(0, 0.02), uniform token ids, B4 T16384: a finite loss near ln(vocab)
+    for a random init and finite gradients in every parameter."""
+    import math
+
+    from dilution.lm import DilutionLM, LMConfig
+
+    cfg = LMConfig()                                   # the C5 defaults
+    assert (cfg.n_layers, cfg.d_model, cfg.n_heads, cfg.vocab_size) == (12, 1024, 16, 50304)
+    torch.manual_seed(0)
+    model = DilutionLM(cfg).to(device="cuda", dtype=torch.bfloat16).train()
+    g = torch.Generator(device="cuda").manual_seed(13)
+    idx = torch.randint(0, cfg.vocab_size, (4, 16385), device="cuda", generator=g)
+    _, loss = model(idx[:, :-1], idx[:, 1:])
+    loss.backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(loss)
+    assert abs(loss.item() - math.log(cfg.vocab_size)) < 1.0, loss.item()
+    for name, p in model.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name

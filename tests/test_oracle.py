@@ -119,6 +119,43 @@ def test_closed_form_backward_matches_autograd(t):
     assert np.abs(inter["out"] - orc.attention_f64(q, k, v).numpy()).max() < 1e-12
 
 
+@pytest.mark.parametrize("t,block", [(1, 4), (33, 7), (100, 32), (257, 64), (130, 512)])
+def test_blocked_backward_matches_closed_form(t, block):
+    """The row-blocked backward (the full-length gradient checker) against the
+    dense decomposition, itself pinned to autograd above, at ragged lengths
+    and block sizes that do and do not divide T."""
+    q, k, v = _rand((1, 1, t, 16), seed=500 + t, scale=0.7)
+    do = torch.randn(t, 16, dtype=torch.float64, generator=torch.Generator().manual_seed(t))
+    want, inter_w = orc.grads_closed_form_f64(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), do.numpy())
+    got, inter = orc.grads_blocked_f64(q[0, 0], k[0, 0], v[0, 0], do, block=block)
+    for w, g in zip(want, got):
+        assert np.abs(g.numpy() - w).max() < 1e-10
+    assert np.abs(inter["ghat"].numpy() - inter_w["ghat"]).max() < 1e-10
+    assert np.abs(inter["out"].numpy() - inter_w["out"]).max() < 1e-12
+    assert np.abs(inter["totals"].numpy() - orc.demand_totals(q, k)[0, 0].numpy()).max() < 1e-10
+    # adding a constant to every key leaves the output unchanged: sum_j dk_j = 0
+    assert got[1].sum(0).abs().max() < 1e-10 * (1.0 + got[1].abs().sum())
+
+
+def test_blocked_backward_matches_autograd_directly():
+    q, k, v = _rand((1, 1, 50, 8), seed=77)
+    do = torch.randn(1, 1, 50, 8, dtype=torch.float64, generator=torch.Generator().manual_seed(78))
+    ref = orc.grads_autograd(q, k, v, do)
+    got, _ = orc.grads_blocked_f64(q[0, 0], k[0, 0], v[0, 0], do[0, 0], block=16)
+    for r, g in zip(ref, got):
+        assert (r[0, 0] - g).abs().max() < 1e-10
+
+
+@pytest.mark.parametrize("mutant", ["no_suffix_carry", "no_demand_carry"])
+def test_blocked_backward_planted_mistakes_fail(mutant):
+    q, k, v = _rand((1, 1, 90, 8), seed=79, scale=0.7)
+    do = torch.randn(90, 8, dtype=torch.float64, generator=torch.Generator().manual_seed(80))
+    want, _ = orc.grads_closed_form_f64(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), do.numpy())
+    got, _ = orc.grads_blocked_f64(q[0, 0], k[0, 0], v[0, 0], do, block=32, mutant=mutant)
+    err = max(np.abs(g.numpy() - w).max() for w, g in zip(want, got))
+    assert err > 1e-3, (mutant, err)
+
+
 def test_row_stats_and_pk_match_library_softmax():
     q, k, v = _rand((1, 2, 50, 16), seed=8)
     rmax, rden = orc.row_stats(q, k)
