@@ -47,6 +47,9 @@ const char* dil_status_string(int status) {
     case dil::kErrVariant:
       return "operator variant out of range (bid 0-7, share 0-2, shift > 0) or not built for this "
              "head_dim (the ablation variants are built for head_dim 64)";
+    case dil::kErrScratch:
+      return "the call needs more scratch than dil_decode_step_noalloc holds "
+             "(DIL_NOALLOC_SCRATCH_BYTES); use dil_decode_step with a workspace";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

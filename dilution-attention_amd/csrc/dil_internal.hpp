@@ -14,6 +14,7 @@ constexpr int kErrWorkspace = -3;
 constexpr int kErrShape = -4;
 constexpr int kErrPrecision = -5;
 constexpr int kErrVariant = -6;
+constexpr int kErrScratch = -7;
 
 // Operator variant (the reference's kernels_bid ablations): bid function
 // 0..7, share mode 0 (none) / 1 (dilution) / 2 (exclusive), and the SHIFT of

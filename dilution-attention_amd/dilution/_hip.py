@@ -46,6 +46,8 @@ SIGNATURES = {
     "dil_decode_workspace_bytes": (_c_int64, [_c_int64, _c_int64, _c_int]),
     "dil_decode_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _c_int,
                                  _c_int, _c_int, _vp, _c_int64, _vp]),
+    "dil_decode_step_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64,
+                                         _c_int, _c_int, _c_int, _vp]),
     "dil_timing_enable": (_c_int, [_c_int]),
     "dil_timing_reset": (_c_int, []),
     "dil_timing_count": (_c_int, []),

@@ -133,6 +133,25 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
                     void* stream);
 
 /*
+ * Allocation-free cached decode step.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Arguments and results as dil_decode_step, without the workspace: the
+ * kernels' scratch lives in a static device array of
+ * DIL_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until the
+ * process ends.  A call needing more than that, i.e.
+ * dil_decode_workspace_bytes(n, length, head_dim) > DIL_NOALLOC_SCRATCH_BYTES
+ * (about n * length <= 16.7M at head_dim 64), returns -7 before any launch.
+ * No allocation of any kind is made.  All calls on one GPU share its array:
+ * calls that overlap on one GPU (two streams, two host threads) race.
+ */
+#define DIL_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int dil_decode_step_noalloc(const void* q1, const void* k_cache, const void* v_cache,
+                            float* committed, void* out, int64_t n, int64_t capacity,
+                            int64_t length, int head_dim, int dtype, int q_dtype, void* stream);
+
+/*
  * Operator variants: the bid and share ablations.  Replace the entry points of
  * src/dilution/kernels_bid.py -- dilution_attention_forward (:424-489, its
  * _dilution_k1 :280-360 and _dilution_k2 :362-411), _DilutionAttentionFn.
