@@ -38,6 +38,7 @@
 #include "dil_tiles.hpp"
 #include "dil_variant.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace dil {
@@ -901,11 +902,391 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 }
 
 // ---------------------------------------------------------------------------
+// key-parallel reverse pass that also forms dq (bf16 operands, head_dim 64)
+//
+// bwd_key's walk, widened to 8 waves = 256 keys per workgroup, with the dq
+// product done in the same walk instead of a second (row-parallel) sweep of
+// the whole chain.  After each query tile every wave transposes its (p dp)
+// tile with an identity MFMA (rows in lanes) and stages it in LDS as bf16;
+// behind the step's barrier the 8 waves then form the tile's dq contribution
+// over the group's 256 keys, one 16 x 16 output block each
+// (v_mfma_f32_16x16x32_bf16, K parked in LDS), and store it as a bf16
+// partial per (key group, query tile), with the row sums of (p dp) (the
+// ghat partials) in fp32.  bwd_dq_reduce adds the partials of every key
+// group in a fixed order (deterministic, no atomics).
+//
+// Partials are stored compactly: key group g meets query tiles
+// [8 g, nq), tile (g, qt) sits at keyq_tile_base(g, nq) + qt - 8 g.
+
+constexpr int kKqWaves = 8;
+constexpr int kKqThreads = 64 * kKqWaves;
+constexpr int kKqKeys = kKqWaves * kTileK;        // 256 keys per workgroup
+constexpr int kKqTilesPerGroup = kKqKeys / kTileQ;  // query tiles spanned by a key group
+constexpr int kPdStride = kKqKeys + 8;            // bf16 per staged (p dp) row (+16 B: bank offset)
+
+__host__ __device__ inline int64_t keyq_tile_base(int64_t g, int64_t nq) {
+  return g * nq - static_cast<int64_t>(kKqTilesPerGroup) * g * (g - 1) / 2;
+}
+__host__ __device__ inline int64_t keyq_groups(int64_t T) { return (T + kKqKeys - 1) / kKqKeys; }
+__host__ __device__ inline int64_t keyq_tiles(int64_t T) {
+  const int64_t nq = (T + kTileQ - 1) / kTileQ;
+  return keyq_tile_base(keyq_groups(T), nq);
+}
+
+template <int D>
+__global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* __restrict__ dqp,
+                                                           float* __restrict__ ghp, int64_t ntiles) {
+  static_assert(D == 64, "the dq-forming key pass is built for head_dim 64");
+  using CT = __bf16;
+  using TL = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
+  __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
+  // lse, -dbs of the tile's rows, then padding: every thread of the stash writes a slot
+  __shared__ __attribute__((aligned(16))) float st_s[2][kKqThreads];
+  __shared__ float cs_s[2][kKqKeys];                                   // demand entering the tile
+  __shared__ __attribute__((aligned(16))) CT pd_s[2][kTileQ * kPdStride];   // (p dp), [row][key]
+  __shared__ float gh_s[2][kKqWaves][kTileQ];                          // row sums of (p dp) per wave
+  // B operand of the dq product: K of the group's keys, per d quarter and key
+  // step (32 keys), lane-minor (one conflict-free 16-byte read per fragment)
+  __shared__ __attribute__((aligned(16))) bf16x8 kpark[D / 16][kKqWaves][64];
+  __shared__ __attribute__((aligned(16))) bf16x8 id_park[2][64];       // transpose identity
+
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const float hf = static_cast<float>(h);
+  const int kg = item.idx;
+  const int kb0 = kg * kKqWaves;                 // first key tile of the group
+  const int kb = kb0 + wave;                     // key tile of this wave
+  const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
+  const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
+  const bool active = static_cast<int64_t>(kb) * kTileK < P.T;
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.T * D;
+  const CT* dos = static_cast<const CT*>(P.dout) + slice * P.T * D;
+  const CT* qts = static_cast<const CT*>(P.qt) + slice * D * P.t_pad;
+  const CT* dots = static_cast<const CT*>(P.dot) + slice * D * P.t_pad;
+  const float* lse = P.lse + slice * P.T;
+  const float* dbs = P.dbs + slice * P.T;
+
+  // this wave's keys as B operands (lane <-> key)
+  RowFrag<CT, D> kf, vf;
+  if (key < P.T) {
+    load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
+    load_row_frag<CT, D>(vf, static_cast<const CT*>(P.v) + (slice * P.T + key) * D + h * (D / 2));
+  } else {
+    zero_row_frag<CT, D>(kf);
+    zero_row_frag<CT, D>(vf);
+  }
+  // park K of the group's keys for the dq product: fragment (d quarter u, key
+  // step w, lane) holds K[32 (kb0 + w) + 8 (lane >> 4) + t][16 u + (lane & 15)],
+  // t = 0..7: 16 contiguous bytes of the tile-major K^T copy (zero past the
+  // slice's padded length, through the resource bound)
+  {
+    const CT* kts = static_cast<const CT*>(P.kt) + slice * D * P.t_pad;
+    const int64_t first = static_cast<int64_t>(kb0) * kTileK * D;           // element offset of tile kb0
+    const auto rs = make_rsrc(kts + first, (D * P.t_pad - first) * static_cast<int64_t>(sizeof(CT)));
+#pragma unroll
+    for (int u = 0; u < D / 16; ++u) {
+      const int d = 16 * u + (lane & 15);
+      const uint32_t off = static_cast<uint32_t>(((wave * D + d) * kTileK + 8 * (lane >> 4)) * sizeof(CT));
+      kpark[u][wave][lane] = buffer_load16<bf16x8>(rs, off, 0);
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
+    }
+  }
+
+  floatx16 dka[kDTiles<D>], dva[kDTiles<D>];
+#pragma unroll
+  for (int t = 0; t < kDTiles<D>; ++t) {
+    dka[t] = floatx16{};
+    dva[t] = floatx16{};
+  }
+  float sufk = 0.f;
+
+  // staging: waves 0-3 copy the Q row tile and its transpose, waves 4-7 dO'
+  // and its transpose (one 16-byte chunk of each per thread); threads 0-63
+  // the row statistics, threads 0-255 the demand checkpoints of the 256 keys
+  const bool second = threadIdx.x >= 256;       // wave-uniform
+  const int c256 = threadIdx.x & 255;
+  const CT* rsrc = second ? dos : qs;
+  const CT* tsrc = second ? dots : qts;
+  bf16x8 rr = {}, tr = {};
+  RowStatsLoader<2> sl;
+  const int64_t ck = static_cast<int64_t>(kb0) * kTileK + c256;
+  const bool ck_ok = ck < P.T && !second;
+  const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
+  float cr = 0.f;
+  auto fetch = [&](int qt) {
+    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
+    const int64_t rows = min(max(P.T - row0, int64_t{0}), int64_t{kTileQ});
+    rr = buffer_load16<bf16x8>(make_rsrc(rsrc + row0 * D, rows * D * static_cast<int64_t>(sizeof(CT))),
+                               static_cast<uint32_t>(c256 * 16), 0);
+    tr = buffer_load16<bf16x8>(make_rsrc(tsrc + row0 * D, kTileQ * D * static_cast<int64_t>(sizeof(CT))),
+                               static_cast<uint32_t>(c256 * 16), 0);
+    sl.load(lse, dbs, dbs, row0, P.T);
+    cr = ccol[static_cast<int64_t>(qt) * P.T];
+  };
+  auto stash = [&](int buf) {
+    {
+      const int row = c256 / (D / 8), c = (c256 % (D / 8)) * 8;
+      CT* dst = (second ? do_s[buf] : q_s[buf]) + qs_slot(row) * TL::kKStride + c;
+      *reinterpret_cast<bf16x8*>(dst) = rr;
+    }
+    {
+      const int d = c256 / (kTileQ / 8), c = (c256 % (kTileQ / 8)) * 8;
+      CT* dst = (second ? dot_s[buf] : qt_s[buf]) + d * TL::kTStride + c;
+      *reinterpret_cast<bf16x8*>(dst) = tr;
+    }
+    sl.store_all(st_s[buf]);
+    if (!second) cs_s[buf][c256] = ck_ok ? cr : 0.f;
+  };
+  constexpr int kSteps = kTileQ / Mma<CT>::kStep;
+
+  // (p dp) of this wave's keys for the tile, staged for the dq product:
+  // register i of half h of the transposed tile holds key acc_row(i, h), a run
+  // of 4 consecutive keys per 4 registers
+  auto stage_pd = [&](int buf, const float (&xv)[16]) {
+    CT* dst = pd_s[buf] + l32 * kPdStride + wave * kTileK + 4 * h;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const floatx2 a = {xv[4 * r], xv[4 * r + 1]}, b = {xv[4 * r + 2], xv[4 * r + 3]};
+      const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
+      const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
+      *reinterpret_cast<bf16x4*>(dst + 8 * r) = v;
+    }
+  };
+
+  auto step = [&](int buf, auto diag_tag, auto&& between) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    const float* st = st_s[buf];
+    const float cin = cs_s[buf][wave * kTileK + l32];   // demand entering the tile
+    RowFrag<CT, D> qf, dof;
+    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
+    lds_row_frag<CT, D>(dof, do_s[buf], l32, h);
+    float lz[16], ndb[16];
+    lds_read16(st + kTileQ + 16 * h, ndb);
+    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
+    // the previous tile's dq product queues on the MFMA unit behind the score
+    // products and runs under this tile's exp2 / scan chain
+    between();
+    lds_read16(st + 16 * h, lz);
+    float p[16], x[16], sh[16], w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
+    if constexpr (DIAG) {
+      const int dk = l32 - 16 * h;               // key - row(i) = dk - i on the diagonal tile
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dk > i) p[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = p[i];
+    scan_incl_qs(x, cin + kEps, hf);               // demand + p + eps
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = fast_rcp(x[i]);                       // inv
+      sh[i] = p[i] * x[i];
+    }
+    // dv^T += dO'^T sh  (keys in lanes; dO' carries the 1/(S+eps) of A)
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto bfr = acc_frag<CT>(sh, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      w[i] = dov[i];                               // ds
+      x[i] = w[i] * (sh[i] * x[i]);                // g = ds sh inv
+    }
+    sufk += scan_suffix_qs(x, sufk, hf);           // x = G
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = fmaf(w[i], sh[i], -p[i] * x[i]);   // p dp
+    // dk_main^T += Q^T (p dp), and the transposed (p dp) for dq
+    floatx16 xt = floatx16{};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const auto bfr = acc_frag<CT>(w, s);
+#pragma unroll
+      for (int t = 0; t < kDTiles<D>; ++t)
+        dka[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
+      xt = Mma<CT>::mma(bfr, id_park[s][lane], xt);
+    }
+    float xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = xt[i];
+    stage_pd(buf, xv);
+    // ghat partial of row l32: the transposed values are the bf16 operands dq multiplies
+    const HalfPair gp = halves(sum16(xv));
+    if (h == 0) gh_s[buf][wave][l32] = gp.lo + gp.hi;
+  };
+  // a wave whose keys all follow the tile's rows contributes nothing
+  auto stage_zero = [&](int buf) {
+    float z[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    stage_pd(buf, z);
+    if (h == 0) gh_s[buf][wave][l32] = 0.f;
+  };
+
+  // dq contribution of the group's 256 keys to query tile qt: wave w forms
+  // rows 16 (w & 1) + [0, 16) x head dims 16 (w >> 1) + [0, 16)
+  const int rh = wave & 1, dq4 = wave >> 1;
+  __bf16* dqp_s = dqp + slice * ntiles * (D * kTileQ);
+  float* ghp_s = ghp + slice * ntiles * kTileQ;
+  const int64_t gbase = keyq_tile_base(kg, nq) - static_cast<int64_t>(kKqTilesPerGroup) * kg;
+  auto dq_product = [&](int qt, int buf) {
+    if (qt < 0) return;
+    floatx4 acc = floatx4{};
+    const CT* arow = pd_s[buf] + (16 * rh + (lane & 15)) * kPdStride + 8 * (lane >> 4);
+#pragma unroll
+    for (int ks = 0; ks < kKqWaves; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + kTileK * ks);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kpark[dq4][ks][lane], acc, 0, 0, 0);
+    }
+    // output: lane <-> head dim 16 dq4 + (lane & 15), register j <-> row 16 rh + 4 (lane >> 4) + j;
+    // the partial tile is stored [d][32 rows]
+    const int64_t tile = gbase + qt;
+    const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
+    const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
+    const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
+    *reinterpret_cast<bf16x4*>(dqp_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ + 16 * rh +
+                               4 * (lane >> 4)) = v;
+    if (threadIdx.x < kTileQ) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < kKqWaves; ++w) s += gh_s[buf][w][threadIdx.x];
+      ghp_s[tile * kTileQ + threadIdx.x] = s;
+    }
+  };
+
+  fetch(nq - 1);
+  stash(0);
+  __syncthreads();
+  // the stash is unconditional (the last iteration stashes into the idle
+  // buffer), so the wait for the fetched data never waits on a store.  The
+  // dq product of tile qt + 1 (staged before the previous barrier, in the
+  // other buffer) runs inside step qt, before this step's barrier, which the
+  // stage of tile qt - 1 into that buffer follows.
+  auto iter = [&](int j, int buf) __attribute__((always_inline)) {
+    const int qt = nq - 1 - j;                   // query tiles in reverse
+    fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
+    const int prev = j > 0 ? qt + 1 : -1;
+    auto product = [&]() { dq_product(prev, buf ^ 1); };
+    if (active && qt >= kb) {
+      if (qt > kb) step(buf, std::false_type{}, product);
+      else step(buf, std::true_type{}, product);
+    } else {
+      product();
+      stage_zero(buf);
+    }
+    stash(buf ^ 1);
+    sync_lds();
+  };
+  double_buffered<false>(0, nq - kb0, iter);
+  dq_product(kb0, (nq - kb0 - 1) & 1);          // the last tile, staged before the final barrier
+
+  if (key < P.T) {
+    float* dkrow = P.dkm + (slice * P.T + key) * D;
+    const int64_t dvrow = (slice * P.T + key) * D;
+#pragma unroll
+    for (int t = 0; t < kDTiles<D>; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * t + acc_row(i, h);
+        if (d < D) {
+          dkrow[d] = dka[t][i];
+          store_as(P.dv, dvrow + d, P.gdt, dva[t][i]);
+        }
+      }
+  }
+}
+
+// dq = scale * (sum over key groups of the dq partials) - ghat pk, ghat = the
+// sum of the ghat partials, both in key-group order; and the (ghat * q)^T
+// tiles of the dk correction.  Grid: (query tiles, slices from slice0), the
+// tiles with the most key groups first.  Thread t sums elements [8 t, 8 t + 8)
+// of the [d][32 rows] partial tiles.
+template <int D>
+__global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restrict__ dqp,
+                                                          const float* __restrict__ ghp, int64_t ntiles,
+                                                          int64_t T, const float* __restrict__ pk,
+                                                          const __bf16* __restrict__ qt, int64_t t_pad,
+                                                          void* __restrict__ dq, int gdt, float scale,
+                                                          __bf16* __restrict__ qgt, int64_t slice0) {
+  static_assert(D * kTileQ == 8 * kThreads, "one 16-byte chunk of the partial tile per thread");
+  __shared__ float sum_s[D][kTileQ + 1];
+  __shared__ float g_s[kTileQ];
+  const int64_t slice = slice0 + blockIdx.y;
+  const int nq = static_cast<int>((T + kTileQ - 1) / kTileQ);
+  const int tq = nq - 1 - static_cast<int>(blockIdx.x);
+  const int ng = min(static_cast<int>(keyq_groups(T)) - 1, tq / kKqTilesPerGroup) + 1;
+  const int t = threadIdx.x;
+  const __bf16* base = dqp + slice * ntiles * (D * kTileQ) + 8 * t;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < ng; ++g) {
+    const int64_t tile = keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g;
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + tile * (D * kTileQ));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
+  }
+  const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
+  if (t < kTileQ) {
+    float s = 0.f;
+    for (int g = 0; g < ng; ++g)
+      s += ghp[(slice * ntiles + keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g) * kTileQ + t];
+    g_s[t] = s;
+  }
+  __syncthreads();
+  // (ghat * q)^T: the same [d][32 rows] chunk of the tile-major Q^T copy
+  {
+    const int64_t off = slice * D * t_pad + tmajor_index(static_cast<int64_t>(tq) * kTileQ + r8, d, D);
+    const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qt + off);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(qv[e]) * g_s[r8 + e];
+    store8<__bf16>(qgt + off, v);
+  }
+  // dq rows: thread t takes row t / 8, head dims 8 (t % 8) + [0, 8)
+  const int row = t / (D / 8), d8 = (t % (D / 8)) * 8;
+  const int64_t grow = static_cast<int64_t>(tq) * kTileQ + row;
+  if (grow < T) {
+    const float gr = g_s[row];
+    const int64_t o = (slice * T + grow) * D + d8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) store_as(dq, o + e, gdt, sum_s[d8 + e][row] * scale - gr * pk[o + e]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 struct BwdWorkspace {
   size_t lse, rb1, sinv, dbs, ghat, sufk, dkm, qt, kt, dot, qgt, qc, kc, vc, doc, total;
+  size_t dqp, ghp;            // key-pass dq partials (alias sufk; the paths use one or the other)
 };
+
+// The dq-forming key pass serves bf16 operands at head_dim 64 while its
+// partials (bf16 dq tiles + fp32 row sums: ~1 byte per causal score element)
+// fit this budget; the row-parallel dq pass serves everything else.
+constexpr int64_t kKeyqBudgetBytes = int64_t{24} << 30;
+
+inline int64_t keyq_partial_bytes(int64_t n, int64_t T, int D) {
+  return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
+}
+inline bool keyq_eligible(int64_t n, int64_t T, int D, int lowp) {
+  return lowp && D == 64 && keyq_partial_bytes(n, T, D) <= kKeyqBudgetBytes;
+}
 
 BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int lowp) {
   const size_t ct = lowp ? 2 : 4;
@@ -923,7 +1304,17 @@ BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, 
   w.dbs = w.sinv + rowf;
   w.ghat = w.dbs + rowf;
   w.sufk = w.ghat + rowf;
-  w.dkm = w.sufk + align_up(4 * n * nb * T);
+  // the suffix checkpoints (row-parallel dq pass) and the key pass's dq
+  // partials share one region
+  size_t region = align_up(4 * n * nb * T);
+  w.dqp = w.sufk;
+  w.ghp = w.sufk;
+  if (keyq_eligible(n, T, D, lowp)) {
+    const size_t dqb = align_up(static_cast<size_t>(n * keyq_tiles(T) * D * kTileQ * 2));
+    w.ghp = w.dqp + dqb;
+    region = std::max(region, dqb + align_up(static_cast<size_t>(n * keyq_tiles(T) * kTileQ * 4)));
+  }
+  w.dkm = w.sufk + region;
   w.qt = w.dkm + align_up(4 * n * T * D);
   w.kt = w.qt + tsz;
   w.dot = w.kt + tsz;
@@ -1009,6 +1400,28 @@ int launch_backward(const BackwardArgs& a) {
   });
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
+  if constexpr (sizeof(CT) == 2 && D == 64 && is_production<BID, SHARE>()) {
+    if (keyq_eligible(a.n, a.T, D, a.lowp)) {
+      // one key pass forms dv, dk_main and the dq partials; the reduction
+      // finishes dq and writes the (ghat q)^T tiles of the dk correction
+      __bf16* dqp = reinterpret_cast<__bf16*>(ws + w.dqp);
+      float* ghp = reinterpret_cast<float*>(ws + w.ghp);
+      const int64_t ntiles = keyq_tiles(a.T);
+      P.kgroups = static_cast<int>(keyq_groups(a.T));
+      const dim3 gkq(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
+      DIL_TIMED("bwd_keyq", st, (bwd_keyq<D><<<gkq, kKqThreads, 0, st>>>(P, dqp, ghp, ntiles)));
+      const unsigned nq = static_cast<unsigned>((a.T + kTileQ - 1) / kTileQ);
+      slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+        DIL_TIMED("bwd_dq_reduce", st,
+                  (bwd_dq_reduce<D><<<dim3(nq, ns), kThreads, 0, st>>>(dqp, ghp, ntiles, a.T, a.pk, qt, t_pad,
+                                                                      a.dq, a.grad_dtype, P.scale, qgt, s0)));
+      });
+      P.kgroups = (nkt + 3) / 4;
+      const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
+      DIL_TIMED("bwd_dkcorr", st, (bwd_dkcorr<CT, D, BID><<<gkey, kThreads, 0, st>>>(P)));
+      return static_cast<int>(hipGetLastError());
+    }
+  }
   P.kgroups = (nkt + 3) / 4;
   const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
