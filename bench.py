@@ -85,6 +85,9 @@ ALGO_PRODUCTS = {
     "fwd_out": 1,       # share @ V
     "bwd_key": 4,       # Q K^T recompute, dO V^T, A^T dO (dv), (p dp)^T Q (dk)
     "bwd_query": 1,     # (p dp) K (dq)
+    # bf16 operands at head_dim 64: one key pass forms dv, dk and the dq
+    # partials (Q K^T recompute, dO V^T, dv, dk, dq)
+    "bwd_keyq": 5,
 }
 
 # Algorithmic bytes per key of each decode kernel (d = head_dim, bf16 cache):

@@ -1008,6 +1008,8 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     dva[t] = floatx16{};
   }
   float sufk = 0.f;
+  const bf16x8 ones8 = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
+                        __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
   // staging: waves 0-3 copy the Q row tile and its transpose, waves 4-7 dO'
   // and its transpose (one 16-byte chunk of each per thread); threads 0-63
@@ -1048,17 +1050,17 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
   };
   constexpr int kSteps = kTileQ / Mma<CT>::kStep;
 
-  // (p dp) of this wave's keys for the tile, staged for the dq product:
-  // register i of half h of the transposed tile holds key acc_row(i, h), a run
-  // of 4 consecutive keys per 4 registers
-  auto stage_pd = [&](int buf, const float (&xv)[16]) {
+  // (p dp) of this wave's keys for the tile, staged for the dq product from
+  // the packed transposed tile: fragment s of half h holds keys acc_row(8 s +
+  // t, h), two runs of 4 consecutive keys (16 s + 4 h, 16 s + 8 + 4 h)
+  auto stage_pd = [&](int buf, const bf16x8 (&xf)[2]) {
     CT* dst = pd_s[buf] + l32 * kPdStride + wave * kTileK + 4 * h;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const floatx2 a = {xv[4 * r], xv[4 * r + 1]}, b = {xv[4 * r + 2], xv[4 * r + 3]};
-      const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
-      const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
-      *reinterpret_cast<bf16x4*>(dst + 8 * r) = v;
+    for (int s = 0; s < 2; ++s) {
+      const bf16x4 lo = {xf[s][0], xf[s][1], xf[s][2], xf[s][3]};
+      const bf16x4 hi = {xf[s][4], xf[s][5], xf[s][6], xf[s][7]};
+      *reinterpret_cast<bf16x4*>(dst + 16 * s) = lo;
+      *reinterpret_cast<bf16x4*>(dst + 16 * s + 8) = hi;
     }
   };
 
@@ -1123,16 +1125,19 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     float xv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) xv[i] = xt[i];
-    stage_pd(buf, xv);
-    // ghat partial of row l32: the transposed values are the bf16 operands dq multiplies
-    const HalfPair gp = halves(sum16(xv));
-    if (h == 0) gh_s[buf][wave][l32] = gp.lo + gp.hi;
+    const bf16x8 xf[2] = {acc_frag<CT>(xv, 0), acc_frag<CT>(xv, 1)};
+    stage_pd(buf, xf);
+    // ghat partial of row l32 (the row sums of the bf16 operands dq
+    // multiplies): all-ones A against the transposed tile, every register of
+    // the result holds its lane's row sum
+    floatx16 gs = floatx16{};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) gs = Mma<CT>::mma(ones8, xf[s], gs);
+    if (h == 0) gh_s[buf][wave][l32] = gs[0];
   };
   // a wave whose keys all follow the tile's rows contributes nothing
   auto stage_zero = [&](int buf) {
-    float z[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    const bf16x8 z[2] = {bf16x8{}, bf16x8{}};
     stage_pd(buf, z);
     if (h == 0) gh_s[buf][wave][l32] = 0.f;
   };
@@ -1231,10 +1236,22 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   const int ng = min(static_cast<int>(keyq_groups(T)) - 1, tq / kKqTilesPerGroup) + 1;
   const int t = threadIdx.x;
   const __bf16* base = dqp + slice * ntiles * (D * kTileQ) + 8 * t;
+  // groups in order, four loads in flight (the partial sums are added in
+  // group order: deterministic)
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int g = 0; g < ng; ++g) {
-    const int64_t tile = keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g;
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + tile * (D * kTileQ));
+  auto tile_of = [&](int g) { return keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g; };
+  int g = 0;
+  for (; g + 4 <= ng; g += 4) {
+    bf16x8 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const bf16x8*>(base + tile_of(g + u) * (D * kTileQ));
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
+  }
+  for (; g < ng; ++g) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + tile_of(g) * (D * kTileQ));
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
   }
@@ -1243,8 +1260,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
   if (t < kTileQ) {
     float s = 0.f;
-    for (int g = 0; g < ng; ++g)
-      s += ghp[(slice * ntiles + keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g) * kTileQ + t];
+    for (int gi = 0; gi < ng; ++gi) s += ghp[(slice * ntiles + tile_of(gi)) * kTileQ + t];
     g_s[t] = s;
   }
   __syncthreads();
