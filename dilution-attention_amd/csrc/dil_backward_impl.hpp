@@ -255,16 +255,6 @@ constexpr bool query_parks() {
   return sizeof(CT) == 2 && D <= 64;
 }
 
-// Sum of 16 values as a depth-4 tree.
-__device__ __forceinline__ float sum16(const float (&v)[16]) {
-  float a[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) a[k] = v[k] + v[k + 8];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) a[k] += a[k + 4];
-  return (a[0] + a[2]) + (a[1] + a[3]);
-}
-
 // ---------------------------------------------------------------------------
 // key-parallel reverse pass: dv, dk_main, suffix checkpoints
 

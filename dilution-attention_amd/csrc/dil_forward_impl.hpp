@@ -480,10 +480,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   floatx16 o[kDTiles<D>];
 #pragma unroll
   for (int t = 0; t < kDTiles<D>; ++t) o[t] = floatx16{};
-  // row sums of the shares ride on the share @ V products as a ones column:
-  // column 0 of this tile (lanes 0 and 32) accumulates them
-  floatx16 orow = floatx16{};
-  const auto ones = ones_col_frag<CT>(l32);
+  // row sums of the shares: each lane adds the transposed shares of its row
+  // (row l32, the keys of its half) on the VALU -- the values that multiply V
+  float rsum = 0.f;
 
   // The demand checkpoints of a stage (each wave's rows, the stage's 64 keys)
   // are staged through LDS with the tiles: thread t loads the one of wave
@@ -572,8 +571,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
 #pragma unroll
         for (int t = 0; t < kDTiles<D>; ++t)
           o[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(vttile[buf][slot0 + n], 32 * t + l32, h, s), o[t]);
-        orow = Mma<CT>::mma(af, ones, orow);
       }
+      rsum += sum16(xv);
     }
   };
 
@@ -620,11 +619,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   };
   double_buffered<(D <= 64)>(0, nst, iter);      // head_dim 128 has no registers to spare
 
-  // row sums: column 0 of orow, register i of half h <-> row acc_row(i, h)
-  if (l32 == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ssum_s[wave][acc_row(i, h)] = orow[i];
-  }
+  // row sums: the two halves of row l32
+  const HalfPair rp = halves(rsum);
+  if (h == 0) ssum_s[wave][l32] = rp.lo + rp.hi;
   __syncthreads();
   if (h == 0 && W.r0 + l32 < P.C) P.ssum[slice * P.C + W.r0 + l32] = ssum_s[wave][l32];
 #pragma unroll

@@ -341,6 +341,16 @@ __device__ __forceinline__ void sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Sum of 16 values as a depth-4 tree.
+__device__ __forceinline__ float sum16(const float (&v)[16]) {
+  float a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) a[k] = v[k] + v[k + 8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] += a[k + 4];
+  return (a[0] + a[2]) + (a[1] + a[3]);
+}
+
 // 16 per-register values as an accumulator (the initial value of a product).
 __device__ __forceinline__ floatx16 as_x16(const float (&v)[16]) {
   floatx16 r;
