@@ -397,12 +397,12 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     if constexpr (is_production<BID, SHARE>()) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        w[i] = dov[i];                           // ds
-        x[i] = w[i] * (sh[i] * x[i]);            // g = ds sh inv
+        w[i] = dov[i] * sh[i];                   // ds sh
+        x[i] = w[i] * x[i];                      // g = ds sh inv
       }
       sufk += scan_suffix_qs(x, sufk, hf);       // x = G
 #pragma unroll
-      for (int i = 0; i < 16; ++i) w[i] = fmaf(w[i], sh[i], -p[i] * x[i]);   // p dp
+      for (int i = 0; i < 16; ++i) w[i] = fmaf(-p[i], x[i], w[i]);   // p dp = ds sh - p G
     } else {
       // dp = ds inv - G (+ g for the exclusive share; ds with no share step);
       // the MFMA operand is jac dp (jac = p for the softmax bids)
@@ -640,12 +640,12 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        ds[i] = dov[i];
-        x[i] = ds[i] * (sh[i] * x[i]);           // g
+        ds[i] = dov[i] * sh[i];                  // ds sh
+        x[i] = ds[i] * x[i];                     // g
       }
       scan_suffix_qs(x, sin, hf);                // x = G
 #pragma unroll
-      for (int i = 0; i < 16; ++i) ds[i] = fmaf(ds[i], sh[i], -p[i] * x[i]);   // p dp
+      for (int i = 0; i < 16; ++i) ds[i] = fmaf(-p[i], x[i], ds[i]);   // p dp = ds sh - p G
     } else {
       // dp = ds inv - G (+ g for the exclusive share; ds with no share step)
       if constexpr (SHARE != SHARE_NONE) {
@@ -898,7 +898,7 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 // product done in the same walk instead of a second (row-parallel) sweep of
 // the whole chain.  After each query tile every wave transposes its (p dp)
 // tile with an identity MFMA (rows in lanes) and stages it in LDS as bf16;
-// behind the step's barrier the 8 waves then form the tile's dq contribution
+// after the next step's chain the 8 waves then form the tile's dq contribution
 // over the group's 256 keys, one 16 x 16 output block each
 // (v_mfma_f32_16x16x32_bf16, K parked in LDS), and store it as a bf16
 // partial per (key group, query tile), with the row sums of (p dp) (the
@@ -1054,7 +1054,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     }
   };
 
-  auto step = [&](int buf, auto diag_tag, auto&& between) {
+  auto step = [&](int buf, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     const float* st = st_s[buf];
     const float cin = cs_s[buf][wave * kTileK + l32];   // demand entering the tile
@@ -1065,9 +1065,6 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     lds_read16(st + kTileQ + 16 * h, ndb);
     const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
     const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
-    // the previous tile's dq product queues on the MFMA unit behind the score
-    // products and runs under this tile's exp2 / scan chain
-    between();
     lds_read16(st + 16 * h, lz);
     float p[16], x[16], sh[16], w[16];
 #pragma unroll
@@ -1096,12 +1093,12 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      w[i] = dov[i];                               // ds
-      x[i] = w[i] * (sh[i] * x[i]);                // g = ds sh inv
+      w[i] = dov[i] * sh[i];                       // ds sh
+      x[i] = w[i] * x[i];                          // g = ds sh inv
     }
     sufk += scan_suffix_qs(x, sufk, hf);           // x = G
 #pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = fmaf(w[i], sh[i], -p[i] * x[i]);   // p dp
+    for (int i = 0; i < 16; ++i) w[i] = fmaf(-p[i], x[i], w[i]);   // p dp = ds sh - p G
     // dk_main^T += Q^T (p dp), and the transposed (p dp) for dq
     floatx16 xt = floatx16{};
 #pragma unroll
@@ -1153,13 +1150,15 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
     const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
     const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
-    *reinterpret_cast<bf16x4*>(dqp_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ + 16 * rh +
-                               4 * (lane >> 4)) = v;
+    // streamed past the caches: the partials are read once, by bwd_dq_reduce
+    __builtin_nontemporal_store(__builtin_bit_cast(floatx2, v),
+                                reinterpret_cast<floatx2*>(dqp_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ +
+                                                           16 * rh + 4 * (lane >> 4)));
     if (threadIdx.x < kTileQ) {
       float s = 0.f;
 #pragma unroll
       for (int w = 0; w < kKqWaves; ++w) s += gh_s[buf][w][threadIdx.x];
-      ghp_s[tile * kTileQ + threadIdx.x] = s;
+      __builtin_nontemporal_store(s, ghp_s + tile * kTileQ + threadIdx.x);
     }
   };
 
@@ -1167,23 +1166,23 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
   stash(0);
   __syncthreads();
   // the stash is unconditional (the last iteration stashes into the idle
-  // buffer), so the wait for the fetched data never waits on a store.  The
-  // dq product of tile qt + 1 (staged before the previous barrier, in the
-  // other buffer) runs inside step qt, before this step's barrier, which the
-  // stage of tile qt - 1 into that buffer follows.
+  // buffer).  The dq product of tile qt + 1 (staged before the previous
+  // barrier, in the other buffer) runs after step qt's stash, before this
+  // step's barrier, which the stage of tile qt - 1 into that buffer follows.
+  // Issued after the stash, its partial store is not among the memory
+  // operations the stash waits for, so no step waits for its own store.
   auto iter = [&](int j, int buf) __attribute__((always_inline)) {
     const int qt = nq - 1 - j;                   // query tiles in reverse
     fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
     const int prev = j > 0 ? qt + 1 : -1;
-    auto product = [&]() { dq_product(prev, buf ^ 1); };
     if (active && qt >= kb) {
-      if (qt > kb) step(buf, std::false_type{}, product);
-      else step(buf, std::true_type{}, product);
+      if (qt > kb) step(buf, std::false_type{});
+      else step(buf, std::true_type{});
     } else {
-      product();
       stage_zero(buf);
     }
     stash(buf ^ 1);
+    dq_product(prev, buf ^ 1);
     sync_lds();
   };
   double_buffered<false>(0, nq - kb0, iter);
