@@ -75,6 +75,8 @@ WORKLOADS = {
     "train8k": (2, 16, 8192, 64),
     # the whole LM's attention call (B4 H16 at 16K)
     "lm16k": (4, 16, 16384, 64),
+    # head_dim 128 at the headline's FLOPs (half the heads)
+    "train16k_d128": (1, 8, 16384, 128),
 }
 
 # Algorithmic products (each B H T^2 d FLOPs causal) that each kernel of the

@@ -463,16 +463,19 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
   double_buffered<true>(0, nq - kb0, iter);
 
   if (key < P.T) {
+    // registers 4 j .. 4 j + 3 hold four consecutive head dims (acc_row)
     float* dkrow = P.dkm + (slice * P.T + key) * D;
     const int64_t dvrow = (slice * P.T + key) * D;
 #pragma unroll
     for (int t = 0; t < kDTiles<D>; ++t)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * t + acc_row(i, h);
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * t + acc_row(4 * j, h);
         if (d < D) {
-          dkrow[d] = dka[t][i];
-          store_as(P.dv, dvrow + d, P.gdt, dva[t][i]);
+          *reinterpret_cast<floatx4*>(dkrow + d) =
+              floatx4{dka[t][4 * j], dka[t][4 * j + 1], dka[t][4 * j + 2], dka[t][4 * j + 3]};
+          store4_as(P.dv, dvrow + d, P.gdt,
+                    floatx4{dva[t][4 * j], dva[t][4 * j + 1], dva[t][4 * j + 2], dva[t][4 * j + 3]});
         }
       }
   }
@@ -759,6 +762,18 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
   }
   __syncthreads();
   if (h == 0 && r0 + l32 < P.T) P.ghat[slice * P.T + r0 + l32] = g_s[wave][l32];
+  // the pk loads first (the dq stores could alias them for all the compiler knows)
+  float pkv[16][kDTiles<D>];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = acc_row(i, h);
+    const int64_t base = (slice * P.T + r0 + row) * D;
+#pragma unroll
+    for (int t = 0; t < kDTiles<D>; ++t) {
+      const int d = 32 * t + l32;
+      pkv[i][t] = (bid_normalized<BID>() && r0 + row < P.T && d < D) ? P.pk[base + d] : 0.f;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = acc_row(i, h);
@@ -769,7 +784,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
       for (int t = 0; t < kDTiles<D>; ++t) {
         const int d = 32 * t + l32;
         if (d < D) {
-          const float corr = bid_normalized<BID>() ? gr * P.pk[base + d] : 0.f;
+          const float corr = bid_normalized<BID>() ? gr * pkv[i][t] : 0.f;
           store_as(P.dq, base + d, P.gdt, dqa[t][i] * P.scale - corr);
         }
       }
@@ -880,13 +895,28 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   double_buffered<true>(kb0, q_end, iter);
 
   if (key < P.T) {
+    // every dk_main load first (the dk stores could alias them for all the
+    // compiler knows), four consecutive head dims per load and store
     const int64_t base = (slice * P.T + key) * D;
+    floatx4 dm[kDTiles<D>][4];
 #pragma unroll
     for (int t = 0; t < kDTiles<D>; ++t)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * t + acc_row(i, h);
-        if (d < D) store_as(P.dk, base + d, P.gdt, (P.dkm[base + d] - dkc[t][i]) * P.scale);
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * t + acc_row(4 * j, h);
+        dm[t][j] = d < D ? *reinterpret_cast<const floatx4*>(P.dkm + base + d) : floatx4{};
+      }
+#pragma unroll
+    for (int t = 0; t < kDTiles<D>; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * t + acc_row(4 * j, h);
+        if (d < D) {
+          floatx4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (dm[t][j][e] - dkc[t][4 * j + e]) * P.scale;
+          store4_as(P.dk, base + d, P.gdt, v);
+        }
       }
   }
 }
@@ -1189,16 +1219,19 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
   dq_product(kb0, (nq - kb0 - 1) & 1);          // the last tile, staged before the final barrier
 
   if (key < P.T) {
+    // registers 4 j .. 4 j + 3 hold four consecutive head dims (acc_row)
     float* dkrow = P.dkm + (slice * P.T + key) * D;
     const int64_t dvrow = (slice * P.T + key) * D;
 #pragma unroll
     for (int t = 0; t < kDTiles<D>; ++t)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * t + acc_row(i, h);
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * t + acc_row(4 * j, h);
         if (d < D) {
-          dkrow[d] = dka[t][i];
-          store_as(P.dv, dvrow + d, P.gdt, dva[t][i]);
+          *reinterpret_cast<floatx4*>(dkrow + d) =
+              floatx4{dka[t][4 * j], dka[t][4 * j + 1], dka[t][4 * j + 2], dka[t][4 * j + 3]};
+          store4_as(P.dv, dvrow + d, P.gdt,
+                    floatx4{dva[t][4 * j], dva[t][4 * j + 1], dva[t][4 * j + 2], dva[t][4 * j + 3]});
         }
       }
   }
@@ -1248,8 +1281,18 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
 #pragma unroll
   for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
   if (t < kTileQ) {
+    // eight loads in flight, added in group order
+    const float* gp = ghp + slice * ntiles * kTileQ + t;
     float s = 0.f;
-    for (int gi = 0; gi < ng; ++gi) s += ghp[(slice * ntiles + tile_of(gi)) * kTileQ + t];
+    int gi = 0;
+    for (; gi + 8 <= ng; gi += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = gp[tile_of(gi + u) * kTileQ];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; gi < ng; ++gi) s += gp[tile_of(gi) * kTileQ];
     g_s[t] = s;
   }
   __syncthreads();
@@ -1268,8 +1311,13 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   if (grow < T) {
     const float gr = g_s[row];
     const int64_t o = (slice * T + grow) * D + d8;
+    const floatx4* pk4 = reinterpret_cast<const floatx4*>(pk + o);
+    const floatx4 pa = pk4[0], pb = pk4[1];
+    const float pkv[8] = {pa[0], pa[1], pa[2], pa[3], pb[0], pb[1], pb[2], pb[3]};
+    float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) store_as(dq, o + e, gdt, sum_s[d8 + e][row] * scale - gr * pk[o + e]);
+    for (int e = 0; e < 8; ++e) v[e] = sum_s[d8 + e][row] * scale - gr * pkv[e];
+    store8_as(dq, o, gdt, v);
   }
 }
 

@@ -32,6 +32,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kEps = 1e-9f;                    // reference kernels.py:66-67
 constexpr float kLog2e = 1.4426950408889634f;
@@ -75,6 +76,35 @@ __device__ __forceinline__ void store_as(void* base, int64_t idx, int dt, float 
   if (dt == DT_F32) static_cast<float*>(base)[idx] = v;
   else if (dt == DT_BF16) static_cast<uint16_t*>(base)[idx] = f32_to_bf16_bits(v);
   else static_cast<uint16_t*>(base)[idx] = f32_to_f16_bits(v);
+}
+
+// Store 4 fp32 values as 4 consecutive elements of storage dtype `dt` (the
+// rounding of store_as) in one store: idx is a multiple of 4.
+__device__ __forceinline__ void store4_as(void* base, int64_t idx, int dt, const floatx4& v) {
+  if (dt == DT_F32) {
+    *reinterpret_cast<floatx4*>(static_cast<float*>(base) + idx) = v;
+  } else {
+    u16x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = (dt == DT_BF16) ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
+    *reinterpret_cast<u16x4*>(static_cast<uint16_t*>(base) + idx) = r;
+  }
+}
+
+// Store 8 fp32 values as 8 consecutive elements of storage dtype `dt` (the
+// rounding of store_as), in 16-byte stores: idx is a multiple of 8 and the
+// base 16-byte aligned.
+__device__ __forceinline__ void store8_as(void* base, int64_t idx, int dt, const float (&v)[8]) {
+  if (dt == DT_F32) {
+    floatx4* p = reinterpret_cast<floatx4*>(static_cast<float*>(base) + idx);
+    p[0] = floatx4{v[0], v[1], v[2], v[3]};
+    p[1] = floatx4{v[4], v[5], v[6], v[7]};
+  } else {
+    u16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (dt == DT_BF16) ? f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
+    *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(base) + idx) = r;
+  }
 }
 
 // ---------------------------------------------------------------------------
