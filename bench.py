@@ -40,6 +40,9 @@ The same line carries
   * ``fp32``: the "ieee" mode (fp32 operands, fp32 MFMA; the reference
     forward's default) at the headline shape, fwd+bwd and the forward alone
     (2 B H T^2 d), with the dominant kernel against the fp32 MFMA peak;
+  * ``tf32``: the same for the "tf32" mode (the reference model's precision
+    for fp32 activations), whose fp32 values run as split bf16 operands (three
+    bf16 products per product), priced against a third of the bf16 peak;
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
     formula) timed on this host's cores on one (batch, head) slice of the
     headline workload; ``decode.cpu_baseline``: the oracle's decode step in
@@ -283,10 +286,13 @@ def bench_sdpa(args, inputs):
             "value": round(tflops, 2), "unit": "TFLOP/s"}
 
 
-def bench_fp32(args, inputs):
-    """The "ieee" mode (fp32 operands and fp32 MFMA; the reference forward's
-    default precision, kernels.py:328-335) at the training shape: fwd+bwd and
-    the forward alone, priced against the fp32 MFMA peak."""
+def bench_fp32(args, inputs, prec="ieee"):
+    """An fp32-operand mode at the training shape: fwd+bwd and the forward
+    alone.  "ieee" (fp32 MFMA; the reference forward's default precision,
+    kernels.py:328-335) is priced against the fp32 MFMA peak; "tf32" (the
+    reference model's precision for fp32 activations, model.py:172, run as
+    split bf16 operands: three bf16 products per product) against a third of
+    the bf16 peak."""
     import torch
 
     from dilution import kernels
@@ -297,10 +303,10 @@ def bench_fp32(args, inputs):
     def train():
         for x in xs:
             x.grad = None
-        kernels.dilution_attention(*xs, dot_precision="ieee").backward(do)
+        kernels.dilution_attention(*xs, dot_precision=prec).backward(do)
 
     def forward():
-        kernels.dilution_attention_forward(q, k, v)
+        kernels.dilution_attention_forward(q, k, v, dot_precision=prec)
 
     steps = args.variant_steps
     for _ in range(2):
@@ -314,15 +320,16 @@ def bench_fp32(args, inputs):
     dom = max((nm for nm in per if nm in ALGO_PRODUCTS), key=lambda nm: per[nm][1])
     dom_ms = per[dom][1] / per[dom][0]
     achieved = ALGO_PRODUCTS[dom] * unit / (dom_ms * 1e-3) / 1e12
-    log(f"fp32 fwd+bwd: {ms_train:.3f} ms/step; forward {ms_fwd:.3f} ms")
+    log(f"{prec} fwd+bwd: {ms_train:.3f} ms/step; forward {ms_fwd:.3f} ms")
     del xs
-    return {"dot_precision": "ieee", "dtype": "f32", "train_ms": round(ms_train, 4),
+    peak = PEAK_FP32_TFLOPS if prec == "ieee" else PEAK_BF16_TFLOPS / 3.0
+    return {"dot_precision": prec, "dtype": "f32", "train_ms": round(ms_train, 4),
             "train_tflops": round(7.0 * unit / (ms_train * 1e-3) / 1e12, 2),
             "forward_ms": round(ms_fwd, 4),
             "forward_tflops": round(2.0 * unit / (ms_fwd * 1e-3) / 1e12, 2),
             "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
-                         "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "avg_launch_ms": round(dom_ms, 4)},
+                         "peak": round(peak, 1), "unit": "TFLOP/s",
+                         "frac": round(achieved / peak, 4), "avg_launch_ms": round(dom_ms, 4)},
             "kernels": {name: round(tot / max(n, 1), 4) for name, (n, tot) in per.items()}}
 
 
@@ -732,7 +739,8 @@ def main() -> int:
         line["variants"] = bench_variants(args, dev, tr["inputs"])
         torch.cuda.empty_cache()
     if not args.no_fp32:
-        line["fp32"] = bench_fp32(args, tr["inputs"])
+        line["fp32"] = bench_fp32(args, tr["inputs"], "ieee")
+        line["tf32"] = bench_fp32(args, tr["inputs"], "tf32")
         torch.cuda.empty_cache()
     del tr["inputs"]
     if not args.no_prefill:

@@ -104,7 +104,7 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
 
 int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
                                     int precision, int want_pk) {
-  return dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision == 2, want_pk);
+  return dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision, want_pk);
 }
 
 int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
@@ -122,7 +122,7 @@ int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, 
                static_cast<const void*>(workspace)))
     return dil::kErrShape;
   if (workspace_bytes <
-      dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision == 2, pk != nullptr))
+      dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision, pk != nullptr))
     return dil::kErrWorkspace;
   dil::ForwardArgs a{};
   a.q = q;
@@ -136,7 +136,7 @@ int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, 
   a.q0 = 0;
   a.head_dim = head_dim;
   a.dtype = dtype;
-  a.lowp = precision == 2;
+  a.prec = precision;
   a.out = out;
   a.o_sn = seq * head_dim;
   a.rmax = rmax;
@@ -166,7 +166,7 @@ int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t 
 
 int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
                                     int dtype, int precision) {
-  return dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision == 2, 0);
+  return dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0);
 }
 
 int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_cache, int64_t n,
@@ -184,7 +184,7 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
                static_cast<const void*>(carry), static_cast<const void*>(workspace)))
     return dil::kErrShape;
   if (workspace_bytes <
-      dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision == 2, 0))
+      dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0))
     return dil::kErrWorkspace;
   dil::ForwardArgs a{};
   a.q = q_chunk;
@@ -198,7 +198,7 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
   a.q0 = start;
   a.head_dim = head_dim;
   a.dtype = dtype;
-  a.lowp = precision == 2;
+  a.prec = precision;
   a.out = out;
   a.o_sn = chunk * head_dim;
   a.rmax = rmax;
@@ -218,7 +218,7 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
 
 int64_t dil_backward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
                                      int precision) {
-  return dil::backward_workspace_bytes(n, seq, head_dim, dtype, precision == 2);
+  return dil::backward_workspace_bytes(n, seq, head_dim, dtype, precision);
 }
 
 int dil_backward_variant(const void* q, const void* k, const void* v, const void* dout,
@@ -237,7 +237,7 @@ int dil_backward_variant(const void* q, const void* k, const void* v, const void
                static_cast<const void*>(carry), static_cast<const void*>(pk), dq, dk, dv,
                static_cast<const void*>(workspace)))
     return dil::kErrShape;
-  if (workspace_bytes < dil::backward_workspace_bytes(n, seq, head_dim, dtype, precision == 2))
+  if (workspace_bytes < dil::backward_workspace_bytes(n, seq, head_dim, dtype, precision))
     return dil::kErrWorkspace;
   dil::BackwardArgs a{};
   a.q = q;
@@ -259,7 +259,7 @@ int dil_backward_variant(const void* q, const void* k, const void* v, const void
   a.dtype = dtype;
   a.dout_dtype = dout_dtype;
   a.grad_dtype = grad_dtype;
-  a.lowp = precision == 2;
+  a.prec = precision;
   a.var = dil::Variant{bid, share, shift};
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;

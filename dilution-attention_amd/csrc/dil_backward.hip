@@ -9,15 +9,19 @@ namespace {
 
 template <int D>
 int dispatch_backward(const BackwardArgs& a) {
-  return a.lowp ? launch_backward<__bf16, D>(a) : launch_backward<float, D>(a);
+  switch (a.prec) {
+    case 2: return launch_backward<__bf16, D>(a);
+    case 1: return launch_backward<split32, D>(a);
+    default: return launch_backward<float, D>(a);
+  }
 }
 
 }  // namespace
 
-int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int lowp) {
+int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int prec) {
   // sized with dout needing conversion (the larger case)
   return static_cast<int64_t>(
-      bwd_layout(n, T, head_dim, dtype, lowp ? DT_F32 : DT_BF16, lowp).total);
+      bwd_layout(n, T, head_dim, dtype, prec == 2 ? DT_F32 : DT_BF16, prec).total);
 }
 
 int backward(const BackwardArgs& a) {

@@ -172,19 +172,7 @@ __global__ __launch_bounds__(kThreads) void prep_ghat_q(const CT* __restrict__ q
   __syncthreads();
   for (int e8 = threadIdx.x * 8; e8 < 32 * D; e8 += kThreads * 8) {
     float v[8];
-    if constexpr (sizeof(CT) == 2) {
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qt + base + e8);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = static_cast<float>(x[k]);
-    } else {
-      const floatx4* p = reinterpret_cast<const floatx4*>(qt + base + e8);
-      const floatx4 a = p[0], b = p[1];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[k] = a[k];
-        v[4 + k] = b[k];
-      }
-    }
+    load8<CT>(qt + base + e8, v);
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] *= g_s[(e8 & 31) + k];
     store8<CT>(dst + base + e8, v);
@@ -1337,13 +1325,13 @@ constexpr int64_t kKeyqBudgetBytes = int64_t{24} << 30;
 inline int64_t keyq_partial_bytes(int64_t n, int64_t T, int D) {
   return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
 }
-inline bool keyq_eligible(int64_t n, int64_t T, int D, int lowp) {
-  return lowp && D == 64 && keyq_partial_bytes(n, T, D) <= kKeyqBudgetBytes;
+inline bool keyq_eligible(int64_t n, int64_t T, int D, int prec) {
+  return prec == 2 && D == 64 && keyq_partial_bytes(n, T, D) <= kKeyqBudgetBytes;
 }
 
-BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int lowp) {
-  const size_t ct = lowp ? 2 : 4;
-  const int ctc = lowp ? DT_BF16 : DT_F32;
+BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int prec) {
+  const size_t ct = prec == 2 ? 2 : 4;
+  const int ctc = native_dtype(prec);
   const bool convert = dtype != ctc;
   const bool convert_do = dout_dtype != ctc;
   const int64_t nb = (T + kTileQ - 1) / kTileQ;
@@ -1362,7 +1350,7 @@ BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, 
   size_t region = align_up(4 * n * nb * T);
   w.dqp = w.sufk;
   w.ghp = w.sufk;
-  if (keyq_eligible(n, T, D, lowp)) {
+  if (keyq_eligible(n, T, D, prec)) {
     const size_t dqb = align_up(static_cast<size_t>(n * keyq_tiles(T) * D * kTileQ * 2));
     w.ghp = w.dqp + dqb;
     region = std::max(region, dqb + align_up(static_cast<size_t>(n * keyq_tiles(T) * kTileQ * 4)));
@@ -1385,8 +1373,8 @@ template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 int launch_backward(const BackwardArgs& a) {
   // the workspace is sized for the worst case (dout converted), so that the
   // size query need not know dout's dtype
-  const int ctc = sizeof(CT) == 2 ? DT_BF16 : DT_F32;
-  const BwdWorkspace w = bwd_layout(a.n, a.T, D, a.dtype, ctc == DT_BF16 ? DT_F32 : DT_BF16, a.lowp);
+  const int ctc = kNativeDtype<CT>;
+  const BwdWorkspace w = bwd_layout(a.n, a.T, D, a.dtype, ctc == DT_BF16 ? DT_F32 : DT_BF16, kOperandPrec<CT>);
   char* ws = static_cast<char*>(a.workspace);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const bool convert = a.dtype != ctc;
@@ -1453,8 +1441,8 @@ int launch_backward(const BackwardArgs& a) {
   });
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
-  if constexpr (sizeof(CT) == 2 && D == 64 && is_production<BID, SHARE>()) {
-    if (keyq_eligible(a.n, a.T, D, a.lowp)) {
+  if constexpr (std::is_same_v<CT, __bf16> && D == 64 && is_production<BID, SHARE>()) {
+    if (keyq_eligible(a.n, a.T, D, kOperandPrec<CT>)) {
       // one key pass forms dv, dk_main and the dq partials; the reduction
       // finishes dq and writes the (ghat q)^T tiles of the dk correction
       __bf16* dqp = reinterpret_cast<__bf16*>(ws + w.dqp);

@@ -5,8 +5,10 @@
 //     64-bit slice strides passed explicitly.  D is a template parameter in
 //     {16, 32, 64, 128}.
 //   * Matrix products use the 32x32 MFMA family: bf16 operands
-//     (v_mfma_f32_32x32x16_bf16) or fp32 operands (v_mfma_f32_32x32x2_f32);
-//     both accumulate in fp32 and share one accumulator layout:
+//     (v_mfma_f32_32x32x16_bf16), fp32 operands (v_mfma_f32_32x32x2_f32), or
+//     split operands (fp32 values as bf16 hi + lo pairs, three bf16 MFMAs per
+//     step: the "tf32" precision); all accumulate in fp32 and share one
+//     accumulator layout:
 //       lane l, register i  ->  column (l & 31), row 8*(i>>2) + 4*(l>>5) + (i&3).
 //   * An operand tile of 32 rows x K is held one row per lane (row = l & 31);
 //     the two lane halves (h = l >> 5) hold two disjoint halves of the K index
@@ -22,6 +24,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace dil {
 
@@ -108,7 +112,19 @@ __device__ __forceinline__ void store8_as(void* base, int64_t idx, int dt, const
 }
 
 // ---------------------------------------------------------------------------
-// MFMA traits: compute type CT is __bf16 or float.
+// MFMA traits: compute type CT is __bf16, float or split32.
+
+// Storage element of split operands: an fp32 value x held as hi = bf16(x)
+// and lo = bf16(x - hi), both rounded to nearest even, so hi + lo is x to
+// within 2^-17 |x|.  Eight consecutive elements are stored as their eight hi
+// halves, then their eight lo halves (32 bytes); every access of a split
+// tile touches whole groups of eight that start at a multiple of 8 elements.
+struct split32 {
+  uint32_t bits;
+};
+struct SplitFrag {
+  bf16x8 hi, lo;
+};
 
 template <typename CT> struct Mma;
 
@@ -119,6 +135,8 @@ template <> struct Mma<__bf16> {
   __device__ static __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  // b holds values exact in the operand type (identity, ones)
+  __device__ static __forceinline__ floatx16 mma_bexact(frag a, frag b, floatx16 c) { return mma(a, b, c); }
   // Pack 8 fp32 values into one operand fragment (round to nearest even).
   __device__ static __forceinline__ frag pack(const float* v) {
     floatx2 p0 = {v[0], v[1]}, p1 = {v[2], v[3]}, p2 = {v[4], v[5]}, p3 = {v[6], v[7]};
@@ -138,8 +156,60 @@ template <> struct Mma<float> {
   __device__ static __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
+  __device__ static __forceinline__ floatx16 mma_bexact(frag a, frag b, floatx16 c) { return mma(a, b, c); }
   __device__ static __forceinline__ frag pack(const float* v) { return v[0]; }
 };
+
+// a b ~ a.hi b.hi + a.hi b.lo + a.lo b.hi: the dropped a.lo b.lo and the
+// rounding of lo leave an error below 2^-15 |a||b| per product term, finer
+// than the 10-bit mantissa of tf32 operands.
+template <> struct Mma<split32> {
+  static constexpr int kPerLane = 8;
+  static constexpr int kStep = 16;
+  using frag = SplitFrag;
+  __device__ static __forceinline__ floatx16 mma(frag a, frag b, floatx16 c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.hi, b.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.hi, b.lo, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.lo, b.hi, c, 0, 0, 0);
+  }
+  // b exact in bf16 (its lo half is zero): two products
+  __device__ static __forceinline__ floatx16 mma_bexact(frag a, frag b, floatx16 c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.hi, b.hi, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.lo, b.hi, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ frag pack(const float* v) {
+    frag f;
+    f.hi = Mma<__bf16>::pack(v);
+    float r[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r[t] = v[t] - static_cast<float>(f.hi[t]);
+    f.lo = Mma<__bf16>::pack(r);
+    return f;
+  }
+};
+
+// Operand types whose fragments carry 8 K elements per lane (bf16 and split)
+template <typename CT> constexpr bool kWideFrag = Mma<CT>::kPerLane == 8;
+
+// The C ABI's precision code of an operand type (0 "ieee", 1 "tf32", 2
+// "bf16"), and the storage dtype that already is the operand type (-1: none,
+// split operands are always built)
+template <typename CT>
+constexpr int kOperandPrec = std::is_same_v<CT, __bf16> ? 2 : std::is_same_v<CT, split32> ? 1 : 0;
+template <typename CT>
+constexpr int kNativeDtype = std::is_same_v<CT, __bf16> ? DT_BF16 : std::is_same_v<CT, float> ? DT_F32 : -1;
+inline int native_dtype(int prec) { return prec == 2 ? DT_BF16 : prec == 0 ? DT_F32 : -1; }
+
+// The fragment of 8 consecutive K elements starting at p (a group start)
+template <typename CT>
+__device__ __forceinline__ typename Mma<CT>::frag frag8_at(const CT* p) {
+  if constexpr (std::is_same_v<CT, split32>) {
+    const bf16x8* q = reinterpret_cast<const bf16x8*>(p);
+    return SplitFrag{q[0], q[1]};
+  } else {
+    return *reinterpret_cast<const bf16x8*>(p);
+  }
+}
 
 // Row permutation within a 32-row tile: swap bits 2 and 3 (an involution).
 __device__ __forceinline__ int rho(int m) {
@@ -167,10 +237,9 @@ template <typename CT, int D> struct RowFrag {
 // from a buffer that already holds the compute type.
 template <typename CT, int D>
 __device__ __forceinline__ void load_row_frag(RowFrag<CT, D>& rf, const CT* src) {
-  if constexpr (sizeof(CT) == 2) {
-    const bf16x8* p = reinterpret_cast<const bf16x8*>(src);
+  if constexpr (kWideFrag<CT>) {
 #pragma unroll
-    for (int s = 0; s < RowFrag<CT, D>::kSteps; ++s) rf.f[s] = p[s];
+    for (int s = 0; s < RowFrag<CT, D>::kSteps; ++s) rf.f[s] = frag8_at<CT>(src + 8 * s);
   } else {
     const floatx4* p = reinterpret_cast<const floatx4*>(src);
 #pragma unroll

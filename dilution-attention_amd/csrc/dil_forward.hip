@@ -9,14 +9,18 @@ namespace {
 
 template <int D>
 int dispatch_forward(const ForwardArgs& a) {
-  return a.lowp ? launch_forward<__bf16, D>(a) : launch_forward<float, D>(a);
+  switch (a.prec) {
+    case 2: return launch_forward<__bf16, D>(a);
+    case 1: return launch_forward<split32, D>(a);
+    default: return launch_forward<float, D>(a);
+  }
 }
 
 }  // namespace
 
-int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int lowp,
+int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int prec,
                                 int want_pk) {
-  return static_cast<int64_t>(fwd_layout(n, C, Tk, head_dim, dtype, lowp, want_pk).total);
+  return static_cast<int64_t>(fwd_layout(n, C, Tk, head_dim, dtype, prec, want_pk).total);
 }
 
 int forward(const ForwardArgs& a) {

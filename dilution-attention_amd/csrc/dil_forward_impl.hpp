@@ -643,9 +643,9 @@ struct FwdWorkspace {
   size_t vt, kt, qc, kc, total;
 };
 
-FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int lowp, int want_pk) {
-  const size_t ct = lowp ? 2 : 4;
-  const bool convert = lowp ? dtype != DT_BF16 : dtype != DT_F32;
+FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int prec, int want_pk) {
+  const size_t ct = prec == 2 ? 2 : 4;
+  const bool convert = dtype != native_dtype(prec);
   FwdWorkspace w{};
   const size_t tsz = align_up(ct * n * D * pad64(Tk));
   w.vt = 0;
@@ -658,10 +658,10 @@ FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int 
 
 template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 int launch_forward(const ForwardArgs& a) {
-  const FwdWorkspace w = fwd_layout(a.n, a.C, a.Tk, D, a.dtype, a.lowp, a.pk != nullptr);
+  const FwdWorkspace w = fwd_layout(a.n, a.C, a.Tk, D, a.dtype, kOperandPrec<CT>, a.pk != nullptr);
   char* ws = static_cast<char*>(a.workspace);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
-  const bool convert = sizeof(CT) == 2 ? a.dtype != DT_BF16 : a.dtype != DT_F32;
+  const bool convert = a.dtype != kNativeDtype<CT>;
   const int64_t tk_pad = pad64(a.Tk);
 
   CT* vt = reinterpret_cast<CT*>(ws + w.vt);

@@ -94,7 +94,7 @@ struct ForwardArgs {
   const void* v;
   int64_t kv_sn;
   int64_t n, C, Tk, q0;
-  int head_dim, dtype, lowp;   // lowp: bf16 MFMA operands; else fp32 operands
+  int head_dim, dtype, prec;   // precision code: 0 fp32, 1 split (tf32), 2 bf16 MFMA operands
   float* out;            // (n, C, D) fp32, slice stride o_sn
   int64_t o_sn;
   float* rmax;           // (n, C) fp32 (log2-domain row max of the scaled affinities)
@@ -112,7 +112,7 @@ struct ForwardArgs {
   void* stream;
 };
 
-int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int lowp,
+int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int prec,
                                 int want_pk);
 int forward(const ForwardArgs& a);
 
@@ -132,13 +132,13 @@ struct BackwardArgs {
   void* dk;
   void* dv;
   int64_t n, T;
-  int head_dim, dtype, dout_dtype, grad_dtype, lowp;
+  int head_dim, dtype, dout_dtype, grad_dtype, prec;   // prec as in ForwardArgs
   void* workspace;
   int64_t workspace_bytes;
   void* stream;
 };
 
-int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int lowp);
+int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int prec);
 int backward(const BackwardArgs& a);
 
 // The ablation variants of one bid function (any share mode), head_dim 64;

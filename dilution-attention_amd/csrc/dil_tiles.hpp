@@ -29,15 +29,43 @@ __host__ __device__ inline int64_t tmajor_index(int64_t t, int d, int D) {
 }
 
 // Store 8 fp32 values as 8 consecutive CT elements (one 16-byte store for
-// bf16, rounded to nearest even; two for fp32).  dst is 16-byte aligned.
+// bf16, rounded to nearest even; two for fp32 and for a split group, hi then
+// lo).  dst is 16-byte aligned (a group start for split).
 template <typename CT>
 __device__ __forceinline__ void store8(CT* dst, const float (&v)[8]) {
-  if constexpr (sizeof(CT) == 2) {
+  if constexpr (std::is_same_v<CT, split32>) {
+    const SplitFrag f = Mma<split32>::pack(v);
+    reinterpret_cast<bf16x8*>(dst)[0] = f.hi;
+    reinterpret_cast<bf16x8*>(dst)[1] = f.lo;
+  } else if constexpr (sizeof(CT) == 2) {
     *reinterpret_cast<bf16x8*>(dst) = Mma<__bf16>::pack(v);
   } else {
     const floatx4 a = {v[0], v[1], v[2], v[3]}, b = {v[4], v[5], v[6], v[7]};
     reinterpret_cast<floatx4*>(dst)[0] = a;
     reinterpret_cast<floatx4*>(dst)[1] = b;
+  }
+}
+
+// Load 8 consecutive CT elements (the layout store8 writes) as fp32.
+template <typename CT>
+__device__ __forceinline__ void load8(const CT* src, float (&v)[8]) {
+  if constexpr (std::is_same_v<CT, split32>) {
+    const bf16x8* q = reinterpret_cast<const bf16x8*>(src);
+    const bf16x8 hi = q[0], lo = q[1];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = static_cast<float>(hi[k]) + static_cast<float>(lo[k]);
+  } else if constexpr (sizeof(CT) == 2) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(src);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = static_cast<float>(x[k]);
+  } else {
+    const floatx4* p = reinterpret_cast<const floatx4*>(src);
+    const floatx4 a = p[0], b = p[1];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[k] = a[k];
+      v[4 + k] = b[k];
+    }
   }
 }
 
@@ -301,8 +329,8 @@ template <typename CT, int D>
 __device__ __forceinline__ typename Mma<CT>::frag lds_t_frag(const CT* lds, int r, int h, int s) {
   if (D < 32 && r >= D) return typename Mma<CT>::frag{};
   const CT* row = lds + r * Tiles<CT, D>::kTStride;
-  if constexpr (sizeof(CT) == 2) {
-    return *reinterpret_cast<const bf16x8*>(row + 16 * s + 8 * h);
+  if constexpr (kWideFrag<CT>) {
+    return frag8_at<CT>(row + 16 * s + 8 * h);
   } else {
     return row[perm_row(s, h)];
   }
@@ -320,7 +348,7 @@ __device__ __forceinline__ typename Mma<CT>::frag acc_frag(const float* v, int s
 // instruction s in half h) equals n = lane & 31.
 template <typename CT>
 __device__ __forceinline__ typename Mma<CT>::frag ident_frag(int l32, int h, int s) {
-  if constexpr (sizeof(CT) == 2) {
+  if constexpr (kWideFrag<CT>) {
     float v[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) v[t] = (16 * s + 8 * h + t == l32) ? 1.f : 0.f;
@@ -449,8 +477,8 @@ template <typename CT, int D>
 __device__ __forceinline__ typename Mma<CT>::frag lds_tq_frag(const CT* lds, int r, int h, int s) {
   if (D < 32 && r >= D) return typename Mma<CT>::frag{};
   const CT* row = lds + r * Tiles<CT, D>::kTStride;
-  if constexpr (sizeof(CT) == 2) {
-    return *reinterpret_cast<const bf16x8*>(row + 16 * h + 8 * s);
+  if constexpr (kWideFrag<CT>) {
+    return frag8_at<CT>(row + 16 * h + 8 * s);
   } else {
     return row[16 * h + s];
   }
@@ -460,7 +488,7 @@ __device__ __forceinline__ typename Mma<CT>::frag lds_tq_frag(const CT* lds, int
 // query held in k slot k equals n = lane & 31.
 template <typename CT>
 __device__ __forceinline__ typename Mma<CT>::frag ident_qs(int l32, int h, int s) {
-  if constexpr (sizeof(CT) == 2) {
+  if constexpr (kWideFrag<CT>) {
     float v[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) v[t] = (16 * h + 8 * s + t == l32) ? 1.f : 0.f;
@@ -474,7 +502,7 @@ __device__ __forceinline__ typename Mma<CT>::frag ident_qs(int l32, int h, int s
 // of the 32-wide output tile receives the sum of the A operand's row over k.
 template <typename CT>
 __device__ __forceinline__ typename Mma<CT>::frag ones_col_frag(int l32) {
-  if constexpr (sizeof(CT) == 2) {
+  if constexpr (kWideFrag<CT>) {
     const float v = l32 == 0 ? 1.f : 0.f;
     const float w[8] = {v, v, v, v, v, v, v, v};
     return Mma<CT>::pack(w);

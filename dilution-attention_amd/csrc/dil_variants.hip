@@ -23,7 +23,8 @@ int forward_share(const ForwardArgs& a) {
   if constexpr (is_production<kB, SHARE>()) {
     return kErrVariant;                      // the production operator is built in dil_forward.hip
   } else {
-    return a.lowp ? launch_forward<__bf16, kD, kB, SHARE>(a) : launch_forward<float, kD, kB, SHARE>(a);
+    // the ablation variants run "tf32" on fp32 operands
+    return a.prec == 2 ? launch_forward<__bf16, kD, kB, SHARE>(a) : launch_forward<float, kD, kB, SHARE>(a);
   }
 }
 
@@ -32,7 +33,7 @@ int backward_share(const BackwardArgs& a) {
   if constexpr (is_production<kB, SHARE>()) {
     return kErrVariant;
   } else {
-    return a.lowp ? launch_backward<__bf16, kD, kB, SHARE>(a) : launch_backward<float, kD, kB, SHARE>(a);
+    return a.prec == 2 ? launch_backward<__bf16, kD, kB, SHARE>(a) : launch_backward<float, kD, kB, SHARE>(a);
   }
 }
 

@@ -72,8 +72,10 @@ def dilution_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
 
 
 def _precision_code(dot_precision: str) -> int:
-    """"ieee" / "tf32": fp32 MFMA operands; "bf16": bf16 MFMA operands
-    (kernels.py:318-325).  gfx950 has no tf32 MFMA, so tf32 runs as ieee."""
+    """The C ABI's precision code (kernels.py:318-325): "ieee" fp32 MFMA
+    operands; "tf32" fp32 values split into bf16 hi + lo operands, three bf16
+    products per product (gfx950 has no tf32 MFMA; the split keeps about 16
+    bits of each operand, more than tf32's 10); "bf16" bf16 MFMA operands."""
     if dot_precision not in _PRECISIONS:
         raise ValueError("dot_precision must be one of ieee, tf32, bf16")
     return _PRECISIONS[dot_precision]
@@ -306,7 +308,8 @@ def dilution_attention(
 
     dot_precision "bf16" (default) uses bf16 MFMA operands for the score and
     value products with fp32 accumulation and fp32 demand/share math;
-    "tf32"/"ieee" keep fp32 operands.
+    "ieee" keeps fp32 operands; "tf32" runs fp32 values as split bf16
+    operands (three bf16 products per product).
     """
     return _DilutionAttentionFn.apply(
         q, k, v, dot_precision, block_m, block_n,

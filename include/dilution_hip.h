@@ -13,9 +13,12 @@
  *     head_dim elements each.
  *   - dtype:     0 = float32, 1 = bfloat16, 2 = float16 (storage type of
  *                q / k / v / dout / outputs where stated).
- *   - precision: 0 = "ieee", 1 = "tf32" (both fp32 MFMA operands on gfx950,
- *                which has no tf32 MFMA), 2 = "bf16" (bf16 MFMA operands).
- *                fp32 accumulation and fp32 demand/share math in every mode.
+ *   - precision: 0 = "ieee" (fp32 MFMA operands), 1 = "tf32" (gfx950 has no
+ *                tf32 MFMA: fp32 values split into bf16 hi + lo operands,
+ *                hi*hi + hi*lo + lo*hi on bf16 MFMA, about 16 bits kept per
+ *                operand; the *_variant entry points run it as "ieee"),
+ *                2 = "bf16" (bf16 MFMA operands).  fp32 accumulation and
+ *                fp32 demand/share math in every mode.
  *   - head_dim in {16, 32, 64, 128}.
  *   - Every launch is asynchronous on `stream` (a hipStream_t); no entry point
  *     synchronises, allocates device memory or keeps state between calls.

@@ -27,9 +27,12 @@ def _run(q, k, v, do, prec):
 
 
 @pytest.mark.parametrize("seq", [1, 8, 64, 257, 1024, 2049])
-def test_backward_fp32_matches_oracle(seq):
+@pytest.mark.parametrize("prec", ["ieee", "tf32"])
+def test_backward_fp32_matches_oracle(seq, prec):
+    """fp32 operands ("ieee") and split bf16 operands ("tf32") both within the
+    fp32-mode bound."""
     q, k, v, do = orc.make_inputs((2, 4, seq, 64), seed=seq, with_dout=True)
-    out, grads = _run(q, k, v, do, "ieee")
+    out, grads = _run(q, k, v, do, prec)
     (dq, dk, dv), _ = orc.grads_closed_form_f64(q.numpy(), k.numpy(), v.numpy(), do.numpy())
     assert max_abs(out, orc.attention_f64(q, k, v)) < 1e-4
     for name, g, want in zip(("dq", "dk", "dv"), grads, (dq, dk, dv)):
@@ -40,9 +43,10 @@ def test_backward_fp32_matches_oracle(seq):
 
 
 @pytest.mark.parametrize("head_dim", [16, 32, 128])
-def test_backward_fp32_head_dims(head_dim):
+@pytest.mark.parametrize("prec", ["ieee", "tf32"])
+def test_backward_fp32_head_dims(head_dim, prec):
     q, k, v, do = orc.make_inputs((1, 2, 200, head_dim), seed=head_dim, with_dout=True)
-    _, grads = _run(q, k, v, do, "ieee")
+    _, grads = _run(q, k, v, do, prec)
     want, _ = orc.grads_closed_form_f64(q.numpy(), k.numpy(), v.numpy(), do.numpy())
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert max_abs(g, torch.from_numpy(w)) < 1e-4, name

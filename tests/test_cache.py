@@ -48,6 +48,11 @@ def test_alloc_and_append_follow_the_reference_protocol():
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
 @pytest.mark.parametrize("chunk", [None, 96, 256])
 def test_chunked_prefill_then_decode_matches_full_rows(dtype, tol, chunk):
+    """The cache prefills with the model's precision rule (model.py:203):
+    bf16 operands for bf16 activations, "tf32" otherwise.  Split bf16
+    operands ("tf32") leave p about 2^-17 relative off, so the fp32 demand
+    totals (up to ~8 here) are held to 1e-5 of their magnitude; the bf16
+    operands of bf16 inputs give exact products and keep 1e-5 absolute."""
     from dilution import cache as dc
 
     batch, heads, d, prompt, steps = 2, 4, 64, 600, 12
@@ -61,12 +66,13 @@ def test_chunked_prefill_then_decode_matches_full_rows(dtype, tol, chunk):
     assert y.dtype == dtype and cache["len"] == prompt
     assert max_abs(y, full[:, :, :prompt]) < tol
     want = orc.demand_totals(q[:, :, :prompt], k[:, :, :prompt])
-    assert max_abs(cache["committed"][:, :, :prompt], want) < 1e-5
+    dtol = 1e-5 * (1.0 if dtype == torch.bfloat16 else max(1.0, float(want.abs().max())))
+    assert max_abs(cache["committed"][:, :, :prompt], want) < dtol
     for t in range(prompt, total):
         out = dc.step_cache(qg[:, :, t:t + 1], kg[:, :, t:t + 1], vg[:, :, t:t + 1], cache)
         assert out.dtype == dtype
         assert max_abs(out[:, :, 0], full[:, :, t]) < tol, t
-    assert max_abs(cache["committed"][:, :, :total], orc.demand_totals(q, k)) < 1e-5
+    assert max_abs(cache["committed"][:, :, :total], orc.demand_totals(q, k)) < dtol
     assert cache["committed"][:, :, total:].abs().max().item() == 0
     assert cache["len"] == total
 

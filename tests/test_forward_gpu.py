@@ -20,13 +20,14 @@ pytestmark = [pytest.mark.gpu, needs_gpu]
 
 @pytest.mark.parametrize("seq", [1, 8, 33, 64, 128, 257, 1025])
 @pytest.mark.parametrize("shape", [(1, 1), (2, 4)])
-def test_forward_fp32_matches_oracle(seq, shape):
+@pytest.mark.parametrize("prec", ["ieee", "tf32"])
+def test_forward_fp32_matches_oracle(seq, shape, prec):
     from dilution import kernels
 
     batch, heads = shape
     q, k, v = orc.make_inputs((batch, heads, seq, 64), seed=seq)
     want = orc.attention_f64(q, k, v)
-    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda())
+    got = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision=prec)
     assert got.dtype == torch.float32 and got.shape == q.shape
     assert torch.isfinite(got).all()
     assert max_abs(got, want) < 1e-4

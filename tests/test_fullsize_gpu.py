@@ -126,6 +126,26 @@ def test_c3_training_fp32_full_size():
     assert (gap <= 1e-5 * (dv.abs().sum(2) + do.double().abs().sum(2))).all()
 
 
+def test_c3_training_tf32_full_size():
+    """The "tf32" precision (fp32 values as split bf16 operands, three bf16
+    products per product) at C3 shape within the fp32-mode bound."""
+    from dilution import kernels
+
+    q, k, v, do = orc.make_inputs((1, 16, 16384, 64), seed=4, qk_scale=0.5, with_dout=True)
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="tf32")
+    out.backward(do.cuda())
+    out = out.detach()
+    grads = [x.grad for x in xs]
+    for h in (0, 5, 10, 15):
+        want, inter = _grads_oracle(q, k, v, do, (0, h), "cuda")
+        assert max_abs(out[0, h], inter["out"]) < 1e-4, h
+        _check_grads([g[0, h] for g in grads], want, 1e-4, f"slice {h} (device oracle)")
+    want, inter = _grads_oracle(q, k, v, do, (0, 15), "cpu")
+    assert max_abs(out[0, 15], inter["out"]) < 1e-4
+    _check_grads([g[0, 15] for g in grads], want, 1e-4, "slice 15 (host oracle)")
+
+
 def test_c2_training_bf16_every_slice():
     """B8 H16 T2048 d64 bf16, q, k ~ 0.5 N(0,1), v, dO ~
     N(0,1).  128 slices put 16 on each XCD, the shape that dispatches every
