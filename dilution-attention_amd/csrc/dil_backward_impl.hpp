@@ -673,7 +673,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
     // transpose the dq operand (jac dp): queries in lanes, keys (natural order) in registers
     floatx16 xt = floatx16{};
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(ds, s), ident_at(s), xt);
+    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma_bexact(acc_frag<CT>(ds, s), ident_at(s), xt);
     float xv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) xv[i] = xt[i];
@@ -683,7 +683,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
 #pragma unroll
       for (int t = 0; t < kDTiles<D>; ++t)
         dqa[t] = Mma<CT>::mma(af, lds_t_frag<CT, D>(kt_s[buf], 32 * t + l32, h, s), dqa[t]);
-      if constexpr (!kPark && bid_log2<BID>()) gacc = Mma<CT>::mma(af, ones, gacc);
+      if constexpr (!kPark && bid_log2<BID>()) gacc = Mma<CT>::mma_bexact(af, ones, gacc);
     }
     // the transposed values are exact copies of the dq operand (bf16 operands
     // in bf16 mode), so these are the row sums of what dq multiplies
@@ -692,7 +692,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
       // ghat needs the row sums of p dp, a different operand from jac dp here
       floatx16 yt = floatx16{};
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s) yt = Mma<CT>::mma(acc_frag<CT>(x, s), ident_at(s), yt);
+      for (int s = 0; s < kSteps; ++s) yt = Mma<CT>::mma_bexact(acc_frag<CT>(x, s), ident_at(s), yt);
       float yv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) yv[i] = yt[i];
@@ -700,7 +700,7 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
         gsum += sum16(yv);
       } else {
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) gacc = Mma<CT>::mma(acc_frag<CT>(yv, s), ones, gacc);
+        for (int s = 0; s < kSteps; ++s) gacc = Mma<CT>::mma_bexact(acc_frag<CT>(yv, s), ones, gacc);
       }
     }
   };

@@ -558,7 +558,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
     for (int n = 0; n < N; ++n) {
       xt[n] = floatx16{};
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s) xt[n] = Mma<CT>::mma(acc_frag<CT>(p[n], s), ident[s], xt[n]);
+      for (int s = 0; s < kSteps; ++s) xt[n] = Mma<CT>::mma_bexact(acc_frag<CT>(p[n], s), ident[s], xt[n]);
     }
 #pragma unroll
     for (int n = 0; n < N; ++n) {
