@@ -517,7 +517,8 @@ def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
     model.prefill(prompt[:, :2048], capacity=2048)         # warm the kernels and allocator
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    logits, caches = model.prefill(prompt, capacity=pt + decode_tokens)
+    graph = kind == "dilution"
+    logits, caches = model.prefill(prompt, capacity=pt + decode_tokens * (2 if graph else 1))
     torch.cuda.synchronize()
     ms_prefill = (time.perf_counter() - t0) * 1e3
     tok = logits[:, -1].float().argmax(-1, keepdim=True)
@@ -532,6 +533,15 @@ def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
     attn_decode = sum(tot for _, tot in kernel_pass(decode_one, 1).values())
     log(f"lm[{kind}] prefill B{pb} T{pt}: {ms_prefill:.1f} ms; decode {ms_decode:.3f} "
         f"ms/token-step (dilution kernels {attn_decode:.3f} ms)")
+    if graph:
+        # the same greedy steps from here on, each one HIP graph replay
+        from dilution.lm import GraphDecoder
+
+        dec = GraphDecoder(model, caches, tok)
+        dec.step()                                          # warm-up and capture
+        ctx0 = caches[0]["len"]
+        ms_graph = timed(dec.step, decode_tokens - 2)
+        log(f"lm[{kind}] graph decode {ms_graph:.3f} ms/token-step")
     out = {"train": {"tokens_per_s": round(tb * tt / (ms_train * 1e-3), 1),
                      "ms_per_step": round(ms_train, 2), "steps": args.lm_train_steps,
                      "first_loss": round(loss0, 4), "batch": tb, "seq_len": tt,
@@ -546,12 +556,19 @@ def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
         out["train"]["attention_kernels_ms_per_step"] = round(attn_train, 2)
         out["prefill"]["chunk"] = cfg.prefill_chunk
         out["decode"]["attention_kernels_ms_per_step"] = round(attn_decode, 4)
+        out["decode"]["graph"] = {"tokens_per_s": round(pb / (ms_graph * 1e-3), 1),
+                                  "ms_per_token_step": round(ms_graph, 4),
+                                  "timed_steps": decode_tokens - 2,
+                                  "context": f"{ctx0 + 1}..{ctx0 + decode_tokens - 2}",
+                                  "how": "GraphDecoder: each step one HIP graph replay, length on the device"}
     out["config"] = {"workload": "C5 whole-LM", "attention": kind, "layers": cfg.n_layers,
                      "d_model": cfg.d_model, "heads": cfg.n_heads,
                      "head_dim": cfg.d_model // cfg.n_heads, "mlp": "SwiGLU 4x",
                      "norm": "RMSNorm", "vocab": cfg.vocab_size,
                      "params": sum(p.numel() for p in model.parameters()), "dtype": "bf16",
                      "data": "synthetic uniform token ids"}
+    if graph:
+        del dec
     del model, caches, logits
     torch.cuda.empty_cache()
     return out

@@ -34,7 +34,7 @@ int check_variant(const Variant& v, int head_dim) {
 
 extern "C" {
 
-int dil_abi_version(void) { return 2; }
+int dil_abi_version(void) { return 3; }
 
 const char* dil_status_string(int status) {
   switch (status) {
@@ -100,6 +100,40 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
   return dil_decode_step_variant(q1, k_cache, v_cache, committed, out, n, capacity, length,
                                  head_dim, dtype, q_dtype, 0, 1, 1.f, workspace, workspace_bytes,
                                  stream);
+}
+
+int dil_decode_step_dlen(const void* q1, const void* k_cache, const void* v_cache, float* committed,
+                         void* out, int64_t n, int64_t capacity, const int64_t* length,
+                         int64_t max_length, int head_dim, int dtype, int q_dtype, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+  if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
+  if (!valid_dtype(dtype) || !valid_dtype(q_dtype)) return dil::kErrDtype;
+  if (n < 1 || max_length < 1 || max_length > capacity) return dil::kErrShape;
+  if (!all_set(q1, k_cache, v_cache, static_cast<const void*>(committed), static_cast<const void*>(out),
+               static_cast<const void*>(length), static_cast<const void*>(workspace)))
+    return dil::kErrShape;
+  if (workspace_bytes < dil::decode_workspace_bytes(n, max_length, head_dim)) return dil::kErrWorkspace;
+  dil::DecodeArgs a{};
+  a.q1 = q1;
+  a.q_sn = head_dim;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.kv_sn = capacity * head_dim;
+  a.committed = committed;
+  a.c_sn = capacity;
+  a.out = out;
+  a.o_sn = head_dim;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.n = n;
+  a.length = max_length;
+  a.dlen = length;
+  a.head_dim = head_dim;
+  a.dtype = dtype;
+  a.q_dtype = q_dtype;
+  a.var = dil::Variant{0, 1, 1.f};
+  a.stream = stream;
+  return dil::decode_step(a);
 }
 
 int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,

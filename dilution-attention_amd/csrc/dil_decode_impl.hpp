@@ -83,6 +83,15 @@ __device__ __forceinline__ void load8_stream(const void* base, int64_t idx, floa
   }
 }
 
+// The live length: `length`, or the device-resident value clamped to
+// [0, length] (the scratch and the grid are sized for `length`).
+__device__ __forceinline__ int64_t live_length(const int64_t* dlen, int64_t length) {
+  return dlen == nullptr ? length : max(int64_t{0}, min(*dlen, length));
+}
+__device__ __forceinline__ int live_chunks(int64_t live, int64_t chunk) {
+  return static_cast<int>((live + chunk - 1) / chunk);
+}
+
 // Chunk statistics: softmax bids (max, sum 2^(a - max)) in log2 units; ratio
 // bids (0 or the minimum of a for minshift, sum of the numerators) in natural
 // units; none for the elementwise bids.
@@ -90,14 +99,16 @@ template <int D, int DT, int BID = BID_SOFTMAX>
 __global__ __launch_bounds__(kDecThreads) void dec_stats(
     const void* __restrict__ q1, int qdt, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
     float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
-    float qscale, int64_t slice0) {
+    float qscale, int64_t slice0, const int64_t* __restrict__ dlen) {
   using L = DecLayout<D>;
   const int64_t slice = slice0 + blockIdx.y;
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
+  const int64_t live = live_length(dlen, length);
+  if (c >= live_chunks(live, chunk)) return;             // past the live length: no statistics
   const int64_t j0 = c * chunk;
-  const int64_t j1 = min(j0 + chunk, length);
+  const int64_t j1 = min(j0 + chunk, live);
 
   float q[8];
   load8_f32(q1, slice * q_sn + sub * 8, qdt, q);        // q1 in its own dtype, as fp32
@@ -189,16 +200,22 @@ template <int D, int DT, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 __global__ __launch_bounds__(kDecThreads) void dec_apply(
     const void* __restrict__ vc, int64_t kv_sn, float* __restrict__ committed, int64_t c_sn,
     const float* __restrict__ aff, const float2* __restrict__ part, float* __restrict__ part_out,
-    int64_t length, int64_t chunk, int nchunk, float shift, int64_t slice0) {
+    int64_t length, int64_t chunk, int nchunk, float shift, int64_t slice0,
+    const int64_t* __restrict__ dlen) {
   using L = DecLayout<D>;
   const int64_t slice = slice0 + blockIdx.y;
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
+  // the scratch strides keep `length` and `nchunk` (the maxima); the walk
+  // covers the live length only
+  const int64_t live = live_length(dlen, length);
+  const int nlive = live_chunks(live, chunk);
+  if (c >= nlive) return;
 
   // Combine the chunk statistics of this slice (every wave redundantly).
   float m = -INFINITY, s = 0.f;
-  for (int i = lane; i < nchunk; i += 64) {
+  for (int i = lane; i < nlive; i += 64) {
     const float2 ps = part[slice * nchunk + i];
     const float mn = fmaxf(m, ps.x);
     if (mn > -INFINITY) {
@@ -214,20 +231,20 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
   const float lshift = __log2f(shift);
   if constexpr (BID != BID_SOFTMAX) {
     float mn = INFINITY, sm = 0.f;
-    for (int i = lane; i < nchunk; i += 64) {
+    for (int i = lane; i < nlive; i += 64) {
       const float2 ps = part[slice * nchunk + i];
       mn = fminf(mn, ps.x);
       sm += ps.y;
     }
     mn = -wave_max(-mn);
     sm = wave_sum(sm);
-    const float rden = BID == BID_MINSHIFT ? fmaxf(sm - static_cast<float>(length) * mn, 0.f)
+    const float rden = BID == BID_MINSHIFT ? fmaxf(sm - static_cast<float>(live) * mn, 0.f)
                                            : (BID == BID_EXPSHIFT ? shift : sm);
-    bid_row_params<BID>(BID == BID_MINSHIFT ? mn : 0.f, rden, static_cast<float>(length), true, r0, r1);
+    bid_row_params<BID>(BID == BID_MINSHIFT ? mn : 0.f, rden, static_cast<float>(live), true, r0, r1);
   }
 
   const int64_t j0 = c * chunk;
-  const int64_t j1 = min(j0 + chunk, length);
+  const int64_t j1 = min(j0 + chunk, live);
   const float* arow = aff + slice * length;
   float* crow = committed + slice * c_sn;
   const int64_t vbase = slice * kv_sn + sub * 8;
@@ -289,9 +306,12 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
 // the chunk partials, thread D the share totals, four chunks at a time.
 template <int D>
 __global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part_out, int nchunk,
-                                                  void* __restrict__ out, int64_t o_sn, int dt) {
+                                                  void* __restrict__ out, int64_t o_sn, int dt,
+                                                  int64_t length, int64_t chunk,
+                                                  const int64_t* __restrict__ dlen) {
   const int64_t slice = blockIdx.x;
-  const float* base = part_out + slice * nchunk * (D + 1);
+  const float* base = part_out + slice * nchunk * (D + 1);      // slice stride: the maximum
+  nchunk = live_chunks(live_length(dlen, length), chunk);
   __shared__ float tot_s;
   if (threadIdx.x == D) {
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -345,17 +365,18 @@ int launch_decode(const DecodeArgs& a) {
     DIL_TIMED("dec_stats", st,
               (dec_stats<D, DT, BID><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
                   a.q1, a.q_dtype, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length, chunk, nchunk,
-                  qscale, s0)));
+                  qscale, s0, a.dlen)));
   });
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("dec_apply", st,
               (dec_apply<D, DT, BID, SHARE><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
                   a.v_cache, a.kv_sn, a.committed, a.c_sn, aff, part, part_out, a.length, chunk, nchunk,
-                  a.var.shift, s0)));
+                  a.var.shift, s0, a.dlen)));
   });
   DIL_TIMED("dec_finish", st,
             dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
-                                                                             a.o_sn, a.q_dtype));
+                                                                             a.o_sn, a.q_dtype, a.length,
+                                                                             chunk, a.dlen));
   return static_cast<int>(hipGetLastError());
 }
 

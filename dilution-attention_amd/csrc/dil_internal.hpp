@@ -75,7 +75,8 @@ struct DecodeArgs {
   int64_t o_sn;
   void* workspace;
   int64_t workspace_bytes;
-  int64_t n, length;
+  int64_t n, length;     // with dlen: the maximum length (grid and scratch sized for it)
+  const int64_t* dlen;   // null, or the live length in device memory (clamped to [0, length])
   int head_dim, dtype;   // dtype: the caches'
   int q_dtype;           // q1's and the output's
   Variant var;

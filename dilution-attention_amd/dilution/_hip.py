@@ -48,6 +48,8 @@ SIGNATURES = {
                                  _c_int, _c_int, _vp, _c_int64, _vp]),
     "dil_decode_step_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64,
                                          _c_int, _c_int, _c_int, _vp]),
+    "dil_decode_step_dlen": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _vp, _c_int64,
+                                      _c_int, _c_int, _c_int, _vp, _c_int64, _vp]),
     "dil_timing_enable": (_c_int, [_c_int]),
     "dil_timing_reset": (_c_int, []),
     "dil_timing_count": (_c_int, []),
@@ -55,7 +57,7 @@ SIGNATURES = {
                                  ctypes.POINTER(_c_int64)]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _load_error: str | None = None

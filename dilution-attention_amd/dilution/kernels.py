@@ -440,3 +440,59 @@ def dilution_decode_step(
     if out.dtype != q1.dtype:
         out = out.to(q1.dtype)
     return out.view(batch, heads, 1, head_dim)
+
+
+def decode_step_device_length(q1: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              committed: torch.Tensor, length: torch.Tensor, max_length: int,
+                              out: torch.Tensor | None = None,
+                              workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``dilution_decode_step`` with the length in device memory: ``length``
+    is an int64 tensor of one element on the caches' device, read by the
+    kernels when they run, so one captured HIP graph serves every decode step
+    (no reference counterpart; the reference passes a Python int).
+    ``max_length`` (<= capacity) sizes the grid and the workspace; a live
+    length outside [0, max_length] is clamped.  ``out`` ((B, H, D) in q1's
+    dtype) and ``workspace`` (``decode_workspace(...)``) may be given so that
+    the call allocates nothing.  Results equal ``dilution_decode_step`` at the
+    live length, bitwise."""
+    batch, heads, one, head_dim = q1.shape
+    if one != 1:
+        raise ValueError("decode step takes exactly one query row per (batch, head)")
+    capacity = _check_cache(q1, k_cache, v_cache, committed)
+    if not 1 <= max_length <= capacity:
+        raise ValueError(f"max_length {max_length} outside cache capacity {capacity}")
+    if length.dtype != torch.int64 or length.numel() != 1 or length.device != k_cache.device:
+        raise ValueError("length must be one int64 element on the caches' device")
+    _check_head_dim(head_dim)
+    _check_device(q1, k_cache, v_cache, committed)
+    lib = _hip.lib()
+    n = batch * heads
+    dt = k_cache.dtype
+    if dt not in _DTYPES or v_cache.dtype != dt:
+        raise ValueError("k_cache and v_cache must share a float dtype")
+    if q1.dtype not in _DTYPES:
+        raise ValueError("q1 must be float32, bfloat16 or float16")
+    qf = q1.reshape(n, head_dim)
+    if not qf.is_contiguous():
+        qf = qf.contiguous()
+    if out is None:
+        out = torch.empty(n, head_dim, device=q1.device, dtype=q1.dtype)
+    elif out.dtype != q1.dtype or out.numel() != n * head_dim or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (B, H, D) tensor in q1's dtype")
+    need = lib.dil_decode_workspace_bytes(n, max_length, head_dim)
+    if workspace is None:
+        workspace = _workspace(need, q1.device)
+    elif workspace.numel() < need:
+        raise ValueError(f"workspace of {workspace.numel()} bytes, {need} needed")
+    status = lib.dil_decode_step_dlen(
+        qf.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), committed.data_ptr(), out.data_ptr(),
+        n, capacity, length.data_ptr(), max_length, head_dim, _DTYPES[dt], _DTYPES[q1.dtype],
+        workspace.data_ptr(), workspace.numel(), _stream(q1.device))
+    _hip.check(status, "dil_decode_step_dlen")
+    return out.view(batch, heads, 1, head_dim)
+
+
+def decode_workspace(batch: int, heads: int, max_length: int, head_dim: int, device) -> torch.Tensor:
+    """A workspace for ``decode_step_device_length`` up to ``max_length``."""
+    lib = _hip.lib()
+    return _workspace(lib.dil_decode_workspace_bytes(batch * heads, max_length, head_dim), device)

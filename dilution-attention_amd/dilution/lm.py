@@ -279,19 +279,38 @@ class DilutionLM(nn.Module):
             x = block.step_cache(x, cache)
         return self.lm_head(self.ln_f(x))
 
+    def graph_decode_eligible(self) -> bool:
+        """Every layer runs the production dilution operator (the decode step
+        GraphDecoder captures)."""
+        return all(isinstance(b.attn, DilutionAttention) and b.attn.production for b in self.h)
+
     @torch.no_grad()
     def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 0.0,
                  top_k: int | None = None, top_p: float | None = None,
-                 generator: torch.Generator | None = None, vocab_limit: int | None = None) -> torch.Tensor:
+                 generator: torch.Generator | None = None, vocab_limit: int | None = None,
+                 graph: bool = False) -> torch.Tensor:
         """Cached generation with caches sized prompt + max_new_tokens
         (model.py:473-509): temperature 0 is greedy, otherwise a sample of
         softmax(logits / temperature) after top-k / nucleus truncation;
         ``generator`` makes sampling reproducible, ``vocab_limit`` keeps the
-        new tokens below that id."""
+        new tokens below that id.  ``graph=True`` runs greedy decoding of an
+        all-dilution production stack through ``GraphDecoder`` (the same
+        tokens, one HIP graph replay per step)."""
         if vocab_limit is not None and not 0 < vocab_limit <= self.cfg.vocab_size:
             raise ValueError(f"vocab_limit must be in (0, {self.cfg.vocab_size}]")
         logits, caches = self.prefill(idx, capacity=idx.shape[1] + max_new_tokens)
         tokens = idx
+        if graph and not (temperature and temperature > 0.0) and self.graph_decode_eligible():
+            last = logits[:, -1, :].float()
+            if vocab_limit is not None:
+                last[:, vocab_limit:] = float("-inf")
+            nxt = last.argmax(dim=-1, keepdim=True)
+            out = [nxt]
+            if max_new_tokens > 1:
+                dec = GraphDecoder(self, caches, nxt, vocab_limit=vocab_limit)
+                for _ in range(max_new_tokens - 1):
+                    out.append(dec.step().clone())
+            return torch.cat([tokens, *out], dim=1)
         for step in range(max_new_tokens):
             last = logits[:, -1, :].float()
             if vocab_limit is not None:
@@ -305,6 +324,94 @@ class DilutionLM(nn.Module):
             if step + 1 < max_new_tokens:
                 logits = self.decode_step(nxt, caches)
         return tokens
+
+
+class GraphDecoder:
+    """Greedy decoding of an all-dilution, production-operator LM with each
+    token's step captured once as a HIP graph and replayed.
+
+    One step is: the embedding of the last token; per layer the norm, the q/k/v
+    projection, the cache append at a device-resident position
+    (``index_copy_``), the decode step with its length in device memory
+    (``kernels.decode_step_device_length``), the output projection and the
+    MLP; then the head, the argmax that becomes the next step's token, and the
+    position and length advanced by one on the device.  With nothing on the
+    host changing from step to step, one capture serves every step up to the
+    caches' capacity, and each step is a single graph launch.
+
+    ``caches`` come from ``DilutionLM.prefill`` (sized for the whole
+    generation); ``token`` (B, 1) is the token the first step consumes.  The
+    first ``step()`` runs eagerly (the capture's warm-up, on a side stream) and
+    then captures; later calls replay.  ``step()`` returns the (B, 1) token
+    buffer the step wrote (overwritten by the next step: clone to keep it);
+    ``logits`` holds that step's (B, 1, vocab) logits.  The caches' ``len``
+    follows the steps taken.
+    """
+
+    def __init__(self, model: "DilutionLM", caches: list, token: torch.Tensor,
+                 vocab_limit: int | None = None):
+        if not model.graph_decode_eligible():
+            raise ValueError("GraphDecoder needs every layer on the production dilution operator")
+        self.model, self.caches = model, caches
+        k0 = caches[0]["k"]
+        self.batch, self.heads, self.capacity, self.head_dim = k0.shape
+        self.len = caches[0]["len"]
+        if any(c["len"] != self.len or c["k"].shape != k0.shape for c in caches):
+            raise ValueError("every layer's cache must hold the same length and shape")
+        dev = k0.device
+        self.tok = token.detach().clone().to(device=dev, dtype=torch.long).view(self.batch, 1)
+        self.pos = torch.full((1,), self.len, dtype=torch.long, device=dev)      # next write position
+        self.live = torch.full((1,), self.len + 1, dtype=torch.long, device=dev)  # length after it
+        qdt = model.lm_head.weight.dtype
+        self.outs = [torch.empty(self.batch, self.heads, self.head_dim, device=dev, dtype=qdt)
+                     for _ in caches]
+        self.ws = kernels.decode_workspace(self.batch, self.heads, self.capacity, self.head_dim, dev)
+        self.logits = torch.empty(self.batch, 1, model.cfg.vocab_size, device=dev, dtype=qdt)
+        self.mask = None
+        if vocab_limit is not None:
+            self.mask = torch.zeros(model.cfg.vocab_size, device=dev)
+            self.mask[vocab_limit:] = float("-inf")
+        self.graph = None
+
+    def _body(self) -> None:
+        m = self.model
+        x = m.wte(self.tok)
+        for block, cache, out in zip(m.h, self.caches, self.outs):
+            q1, k1, v1 = block.attn._split_heads(block.ln_1(x))
+            cache["k"].index_copy_(2, self.pos, k1)
+            cache["v"].index_copy_(2, self.pos, v1)
+            y = kernels.decode_step_device_length(q1, cache["k"], cache["v"], cache["committed"],
+                                                  self.live, self.capacity, out=out, workspace=self.ws)
+            x = x + block.attn._merge_heads(y.to(x.dtype), self.batch, 1)
+            x = x + block.mlp(block.ln_2(x))
+        logits = m.lm_head(m.ln_f(x))
+        self.logits.copy_(logits)
+        last = logits[:, -1, :].float()
+        if self.mask is not None:
+            last = last + self.mask
+        self.tok.copy_(last.argmax(dim=-1, keepdim=True))
+        self.pos.add_(1)
+        self.live.add_(1)
+
+    @torch.no_grad()
+    def step(self) -> torch.Tensor:
+        if self.len >= self.capacity:
+            raise ValueError("decode step past the cache capacity (context_length)")
+        if self.graph is None:
+            side = torch.cuda.Stream(device=self.tok.device)
+            side.wait_stream(torch.cuda.current_stream(self.tok.device))
+            with torch.cuda.stream(side):
+                self._body()                       # a real step: warms up the libraries
+            torch.cuda.current_stream(self.tok.device).wait_stream(side)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self._body()                       # recorded, not run
+        else:
+            self.graph.replay()
+        self.len += 1
+        for c in self.caches:
+            c["len"] = self.len
+        return self.tok
 
 
 def filter_logits(logits: torch.Tensor, top_k: int | None = None, top_p: float | None = None) -> torch.Tensor:

@@ -136,6 +136,25 @@ int dil_decode_step(const void* q1, const void* k_cache, const void* v_cache, fl
                     void* stream);
 
 /*
+ * Cached decode step with the length in device memory.  No counterpart in
+ * the reference: it is for callers that replay one captured HIP graph for
+ * every decode step (the length changes each step; a kernel argument would
+ * be frozen into the graph).
+ *
+ * Arguments as dil_decode_step, except `length`: a device pointer to the
+ * live length (int64), read by the kernels when they run, and `max_length`
+ * (<= capacity), which sizes the grid and the workspace
+ * (dil_decode_workspace_bytes(n, max_length, head_dim)).  A live length
+ * outside [0, max_length] is clamped to it.  The results are those of
+ * dil_decode_step with the live length (bitwise: the same key chunks, summed
+ * in the same order).
+ */
+int dil_decode_step_dlen(const void* q1, const void* k_cache, const void* v_cache, float* committed,
+                         void* out, int64_t n, int64_t capacity, const int64_t* length,
+                         int64_t max_length, int head_dim, int dtype, int q_dtype, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/*
  * Allocation-free cached decode step.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.dil_abi_version() == 2
+    assert lib.dil_abi_version() == 3
     assert lib.dil_status_string(0) == b"success"
     for code in (-1, -2, -3, -4, -5):
         assert lib.dil_status_string(code) != b"unknown status"
@@ -85,6 +85,13 @@ def test_null_pointers_are_argument_errors(lib):
     assert lib.dil_decode_step(*fake[:5], 1, 8, 4, 64, 1, 1, None, big, None) == -4
     # with every pointer set, the workspace size is the next check
     assert lib.dil_decode_step(*fake[:5], 1, 8, 4, 64, 1, 1, fake[5], 0, None) == -3
+    # device-length decode: the five buffers and the length pointer
+    for hole in range(6):
+        ptrs = [None if i == hole else fake[i] for i in range(6)]
+        assert lib.dil_decode_step_dlen(*ptrs[:5], 1, 8, ptrs[5], 4, 64, 1, 1, fake[6], big,
+                                        None) == -4, hole
+    assert lib.dil_decode_step_dlen(*fake[:5], 1, 8, fake[5], 9, 64, 1, 1, fake[6], big, None) == -4
+    assert lib.dil_decode_step_dlen(*fake[:5], 1, 8, fake[5], 8, 64, 1, 1, fake[6], 0, None) == -3
     # forward: pk may be NULL, nothing else may
     fwd_ptrs = fake[:3]
     outs = fake[3:9]                              # out, rmax, rden, ssum, carry, committed_total

@@ -203,6 +203,53 @@ def test_filter_logits():
 
 @pytest.mark.gpu
 @needs_gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_graph_decode_replays_match_eager_decode(dtype):
+    """Every replay of the captured decode step against the eager step from
+    the same state: bitwise equal logits, tokens and caches (the device-length
+    decode walks the same key chunks in the same order).  Eager work and a
+    synchronisation separate the replays."""
+    from dilution.lm import GraphDecoder
+
+    model = _small(dtype=dtype)
+    g = torch.Generator().manual_seed(5)
+    idx = torch.randint(0, 97, (2, 37), generator=g).cuda()
+    cap = 37 + 11
+    logits_e, caches_e = model.prefill(idx, capacity=cap)
+    logits_g, caches_g = model.prefill(idx, capacity=cap)
+    assert torch.equal(logits_e, logits_g)
+    tok = logits_e[:, -1, :].float().argmax(dim=-1, keepdim=True)
+    dec = GraphDecoder(model, caches_g, tok)
+    for step in range(11):
+        le = model.decode_step(tok, caches_e)
+        tg = dec.step()
+        torch.cuda.synchronize()
+        assert torch.equal(dec.logits, le), step
+        tok = le[:, -1, :].float().argmax(dim=-1, keepdim=True)
+        assert torch.equal(tg, tok), step
+    for ce, cg in zip(caches_e, caches_g):
+        assert cg["len"] == ce["len"] == 37 + 11
+        for key in ("k", "v", "committed"):
+            assert torch.equal(cg[key], ce[key]), key
+    with pytest.raises(ValueError):
+        dec.step()                                # the cache is full
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_generate_graph_matches_eager():
+    model = _small()
+    idx = torch.zeros(2, 5, dtype=torch.long, device="cuda")
+    assert torch.equal(model.generate(idx, 9, graph=True), model.generate(idx, 9))
+    assert torch.equal(model.generate(idx, 9, graph=True, vocab_limit=10),
+                       model.generate(idx, 9, vocab_limit=10))
+    mixed = _small(kinds=["softmax", "dilution"])   # not eligible: the eager steps run
+    assert not mixed.graph_decode_eligible()
+    assert torch.equal(mixed.generate(idx, 6, graph=True), mixed.generate(idx, 6))
+
+
+@pytest.mark.gpu
+@needs_gpu
 def test_generate_sampling():
     model = _small()
     idx = torch.zeros(2, 5, dtype=torch.long, device="cuda")
