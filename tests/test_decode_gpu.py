@@ -116,3 +116,57 @@ def test_decode_query_keeps_its_dtype(qdt, cdt, tol):
     assert err < tol, err
     assert max_abs(comg, com_ref) < 1e-5
     assert comg[..., length:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize("dtype,head_dim", [(torch.bfloat16, 64), (torch.float32, 128)])
+def test_device_length_decode_is_the_decode_step(dtype, head_dim):
+    """decode_step_device_length (the length read from device memory, grid
+    and workspace sized for max_length) against dilution_decode_step at the
+    same live length: bitwise equal outputs and demand, around the 2048-key
+    chunk boundaries; one workspace serves every length."""
+    from dilution import kernels
+
+    batch, heads, cap = 2, 3, 5000
+    g = torch.Generator().manual_seed(11)
+    kc = torch.randn(batch, heads, cap, head_dim, generator=g).to(dtype).cuda()
+    vc = torch.randn(batch, heads, cap, head_dim, generator=g).to(dtype).cuda()
+    base = torch.rand(batch, heads, cap, generator=g).cuda() * 3
+    ws = kernels.decode_workspace(batch, heads, cap, head_dim, "cuda")
+    out = torch.empty(batch, heads, head_dim, device="cuda", dtype=dtype)
+    for length in (1, 2047, 2048, 2049, 4096, 4999, 5000):
+        q1 = torch.randn(batch, heads, 1, head_dim, generator=g).to(dtype).cuda()
+        c_ref = base.clone()
+        c_ref[..., length - 1] = 0
+        c_dev = c_ref.clone()
+        want = kernels.dilution_decode_step(q1, kc, vc, c_ref, length)
+        got = kernels.decode_step_device_length(q1, kc, vc, c_dev,
+                                                torch.tensor([length], device="cuda"), cap,
+                                                out=out, workspace=ws)
+        assert torch.equal(got, want), length
+        assert torch.equal(c_dev, c_ref), length
+
+
+def test_device_length_decode_clamps_the_live_length():
+    """A live length past max_length runs as max_length; 0 leaves the demand
+    untouched and outputs zeros.  Nothing past max_length is read or written."""
+    from dilution import kernels
+
+    batch, heads, cap, d = 1, 2, 3000, 64
+    g = torch.Generator().manual_seed(12)
+    kc = torch.randn(batch, heads, cap, d, generator=g).bfloat16().cuda()
+    vc = torch.randn(batch, heads, cap, d, generator=g).bfloat16().cuda()
+    q1 = torch.randn(batch, heads, 1, d, generator=g).bfloat16().cuda()
+    c0 = torch.rand(batch, heads, cap, generator=g).cuda()
+    c0[..., 2499] = 0
+    c_ref, c_dev = c0.clone(), c0.clone()
+    want = kernels.dilution_decode_step(q1, kc, vc, c_ref, 2500)
+    got = kernels.decode_step_device_length(q1, kc, vc, c_dev, torch.tensor([2600], device="cuda"), 2500)
+    assert torch.equal(got, want) and torch.equal(c_dev, c_ref)
+    c_zero = c0.clone()
+    got0 = kernels.decode_step_device_length(q1, kc, vc, c_zero, torch.tensor([0], device="cuda"), 2500)
+    assert torch.equal(c_zero, c0)
+    assert (got0 == 0).all()
+    with pytest.raises(ValueError):
+        kernels.decode_step_device_length(q1, kc, vc, c_zero, torch.tensor([5], device="cuda"), cap + 1)
+    with pytest.raises(ValueError):
+        kernels.decode_step_device_length(q1, kc, vc, c_zero, torch.tensor([5.0], device="cuda"), 10)
