@@ -93,6 +93,9 @@ ALGO_PRODUCTS = {
     # bf16 operands at head_dim 64: one key pass forms dv, dk and the dq
     # partials (Q K^T recompute, dO V^T, dv, dk, dq)
     "bwd_keyq": 5,
+    # bf16 operands at head_dim 64: one key pass forms the share V partials
+    # (in place of fwd_demand + fwd_out)
+    "fwd_keyout": 1,
 }
 
 # Algorithmic bytes per key of each decode kernel (d = head_dim, bf16 cache):

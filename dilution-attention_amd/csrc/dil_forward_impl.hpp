@@ -33,6 +33,7 @@
 #include "dil_tiles.hpp"
 #include "dil_variant.hpp"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace dil {
@@ -637,10 +638,327 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   }
 }
 // ---------------------------------------------------------------------------
+// key-parallel output pass (bf16 operands, head_dim 64, a chunk that starts
+// at row 0: the training forward and a first prefill chunk)
+//
+// fwd_demand's walk, widened to 8 waves = 256 keys per workgroup and forming
+// the output in the same walk, so the scores, exp2 and demand scan run once
+// after the statistics instead of twice.  Per 32-row tile every wave (32
+// keys, lane <-> key, rows in the query-split layout):
+//   * p = 2^(a c - lse), masked on the diagonal tile;
+//   * the demand entering the tile is the wave's running fp64 column sum
+//     (stored as the tile's checkpoint for the backward); an in-register scan
+//     gives demand + p + eps, the share p / (demand + p + eps), and the
+//     running sum advances by the tile's column total;
+//   * the share tile is transposed with an identity MFMA (rows in lanes) and
+//     staged in LDS as bf16; its row sums (the normaliser's partial, over the
+//     same bf16 values that multiply V) come from an all-ones operand.
+// After the next tile's stash the 8 waves form the tile's share V over the
+// group's 256 keys, one 16 x 16 output block each (v_mfma_f32_16x16x32_bf16,
+// V parked in LDS), stored as one bf16 [d][32 rows] partial per (key group,
+// tile) with the fp32 row sums beside it, compactly (keyq_tile_base).
+// fwd_out_reduce sums the partials of every key group in a fixed order and
+// normalises.
+
+template <int D>
+__global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16* __restrict__ op,
+                                                             float* __restrict__ rp, int64_t ntiles) {
+  static_assert(D == 64, "the key-parallel output pass is built for head_dim 64");
+  using CT = __bf16;
+  using TL = Tiles<CT, D>;
+  __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
+  __shared__ __attribute__((aligned(16))) float st_s[2][kTileQ];          // lse of the tile's rows
+  __shared__ __attribute__((aligned(16))) CT sh_s[2][kTileQ * kPdStride];  // shares, [row][key]
+  __shared__ float rs_s[2][kKqWaves][kTileQ];                              // row sums per wave
+  // B operand of the share V product: V of the group's keys, per d quarter
+  // and key step (32 keys), lane-minor
+  __shared__ __attribute__((aligned(16))) bf16x8 vpark[D / 16][kKqWaves][64];
+  __shared__ __attribute__((aligned(16))) bf16x8 id_park[2][64];          // transpose identity
+
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
+  if (!item.valid) return;
+  const int64_t slice = item.slice;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const float hf = static_cast<float>(h);
+  const int kg = item.idx;
+  const int kb0 = kg * kKqWaves;                 // first key tile (and first row tile) of the group
+  const int kb = kb0 + wave;                     // key tile of this wave
+  const int64_t T = P.Tk;                        // rows = keys: the chunk starts at row 0
+  const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
+  const bool key_ok = key < T;
+  const int nq = static_cast<int>((T + kTileQ - 1) / kTileQ);
+  const bool active = static_cast<int64_t>(kb) * kTileK < T;
+
+  const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
+  RowFrag<CT, D> kf;
+  if (key_ok) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + slice * P.k_sn + key * D + h * (D / 2));
+  else zero_row_frag<CT, D>(kf);
+  // park V: fragment (d quarter u, key step w, lane) holds
+  // V[32 (kb0 + w) + 8 (lane >> 4) + t][16 u + (lane & 15)], t = 0..7: 16
+  // contiguous bytes of the tile-major V^T copy (zero past its padded rows)
+  {
+    const CT* vts = static_cast<const CT*>(P.vt) + slice * P.t_sn;
+    const int64_t first = static_cast<int64_t>(kb0) * kTileK * D;
+    const auto rs = make_rsrc(vts + first, (P.t_sn - first) * static_cast<int64_t>(sizeof(CT)));
+#pragma unroll
+    for (int u = 0; u < D / 16; ++u) {
+      const int d = 16 * u + (lane & 15);
+      const uint32_t off = static_cast<uint32_t>(((wave * D + d) * kTileK + 8 * (lane >> 4)) * sizeof(CT));
+      vpark[u][wave][lane] = buffer_load16<bf16x8>(rs, off, 0);
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
+    }
+  }
+  const bf16x8 ones8 = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
+                        __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
+  double run = 0.0;                              // demand entering the current tile (this lane's key)
+  float* ccol = P.carry + slice * P.nb * T + min(key, T - 1);
+
+  // staging: threads 0-255 one 16-byte chunk of the Q row tile; threads 0-31
+  // the lse of its rows (+inf past the end: p = 0)
+  const bool stager = threadIdx.x < 256;        // wave-uniform
+  const int c256 = threadIdx.x & 255;
+  bf16x8 rr = {};
+  float lz = 0.f;
+  const float* rmax = P.rmax + slice * P.C;
+  const float* rden = P.rden + slice * P.C;
+  auto fetch = [&](int qt) {
+    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
+    const int64_t rows = min(max(T - row0, int64_t{0}), int64_t{kTileQ});
+    if (stager)
+      rr = buffer_load16<bf16x8>(make_rsrc(qs + row0 * D, rows * D * static_cast<int64_t>(sizeof(CT))),
+                                 static_cast<uint32_t>(c256 * 16), 0);
+    if (threadIdx.x < kTileQ) {
+      const int64_t r = row0 + threadIdx.x;
+      lz = r < T ? rmax[r] + __log2f(rden[r]) : INFINITY;
+    }
+  };
+  auto stash = [&](int buf) {
+    if (stager) {
+      const int row = c256 / (D / 8), c = (c256 % (D / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(q_s[buf] + qs_slot(row) * TL::kKStride + c) = rr;
+    }
+    if (threadIdx.x < kTileQ) st_s[buf][threadIdx.x] = lz;
+  };
+  constexpr int kSteps = kTileQ / Mma<CT>::kStep;
+
+  // the share tile of this wave's keys, staged for the product from the packed
+  // transposed tile: fragment s of half h holds keys acc_row(8 s + t, h), two
+  // runs of 4 consecutive keys (16 s + 4 h, 16 s + 8 + 4 h)
+  auto stage_sh = [&](int buf, const bf16x8 (&xf)[2]) {
+    CT* dst = sh_s[buf] + l32 * kPdStride + wave * kTileK + 4 * h;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const bf16x4 lo = {xf[s][0], xf[s][1], xf[s][2], xf[s][3]};
+      const bf16x4 hi = {xf[s][4], xf[s][5], xf[s][6], xf[s][7]};
+      *reinterpret_cast<bf16x4*>(dst + 16 * s) = lo;
+      *reinterpret_cast<bf16x4*>(dst + 16 * s + 8) = hi;
+    }
+  };
+  auto step = [&](int buf, int qt, auto diag_tag) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    RowFrag<CT, D> qf;
+    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
+    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    float lzr[16];
+    lds_read16(st_s[buf] + 16 * h, lzr);
+    float p[16], x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lzr[i]));
+    if constexpr (DIAG) {
+      const int dk = l32 - 16 * h;                 // key - row(i) = dk - i on the diagonal tile
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (dk > i) p[i] = 0.f;
+    }
+    const float cin = static_cast<float>(run);
+    if (h == 0 && key_ok) ccol[static_cast<int64_t>(qt) * T] = cin;   // the demand entering the tile
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = p[i];
+    run += static_cast<double>(scan_incl_qs(x, cin + kEps, hf));      // demand + p + eps
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] *= fast_rcp(x[i]);               // share
+    floatx16 xt = floatx16{};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) xt = Mma<CT>::mma(acc_frag<CT>(p, s), id_park[s][lane], xt);
+    float xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = xt[i];
+    const bf16x8 xf[2] = {acc_frag<CT>(xv, 0), acc_frag<CT>(xv, 1)};
+    stage_sh(buf, xf);
+    // row sums of the staged (bf16) shares: all-ones A against the transposed
+    // tile, every register of the result holds its lane's row sum
+    floatx16 gs = floatx16{};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) gs = Mma<CT>::mma(ones8, xf[s], gs);
+    if (h == 0) rs_s[buf][wave][l32] = gs[0];
+  };
+  auto stage_zero = [&](int buf) {
+    const bf16x8 z[2] = {bf16x8{}, bf16x8{}};
+    stage_sh(buf, z);
+    if (h == 0) rs_s[buf][wave][l32] = 0.f;
+  };
+
+  // share V of the group's 256 keys for tile qt: wave w forms rows
+  // 16 (w & 1) + [0, 16) x head dims 16 (w >> 1) + [0, 16)
+  const int rh = wave & 1, dq4 = wave >> 1;
+  __bf16* op_s = op + slice * ntiles * (D * kTileQ);
+  float* rp_s = rp + slice * ntiles * kTileQ;
+  const int64_t gbase = keyq_tile_base(kg, nq) - static_cast<int64_t>(kKqTilesPerGroup) * kg;
+  auto product = [&](int qt, int buf) {
+    if (qt < 0) return;
+    floatx4 acc = floatx4{};
+    const CT* arow = sh_s[buf] + (16 * rh + (lane & 15)) * kPdStride + 8 * (lane >> 4);
+#pragma unroll
+    for (int ks = 0; ks < kKqWaves; ++ks) {
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(arow + kTileK * ks);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, vpark[dq4][ks][lane], acc, 0, 0, 0);
+    }
+    // output: lane <-> head dim 16 dq4 + (lane & 15), register j <-> row 16 rh + 4 (lane >> 4) + j;
+    // the partial tile is stored [d][32 rows], streamed past the caches
+    const int64_t tile = gbase + qt;
+    const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
+    const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
+    const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
+    __builtin_nontemporal_store(__builtin_bit_cast(floatx2, v),
+                                reinterpret_cast<floatx2*>(op_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ +
+                                                           16 * rh + 4 * (lane >> 4)));
+    if (threadIdx.x < kTileQ) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < kKqWaves; ++w) s += rs_s[buf][w][threadIdx.x];
+      __builtin_nontemporal_store(s, rp_s + tile * kTileQ + threadIdx.x);
+    }
+  };
+
+  fetch(kb0);
+  stash(0);
+  __syncthreads();
+  // the product of tile qt - 1 (staged before the previous barrier, in the
+  // other buffer) runs after step qt's stash, before this step's barrier,
+  // which the stage of tile qt + 1 into that buffer follows
+  auto iter = [&](int j, int buf) __attribute__((always_inline)) {
+    const int qt = kb0 + j;                      // query tiles in causal order
+    fetch(min(qt + 1, nq - 1));                  // the last step reloads its own tile, unused
+    if (active && qt >= kb) {
+      if (qt > kb) step(buf, qt, std::false_type{});
+      else step(buf, qt, std::true_type{});
+    } else {
+      stage_zero(buf);
+    }
+    stash(buf ^ 1);
+    product(j > 0 ? qt - 1 : -1, buf ^ 1);
+    sync_lds();
+  };
+  double_buffered<false>(0, nq - kb0, iter);
+  product(nq - 1, (nq - kb0 - 1) & 1);          // the last tile, staged before the final barrier
+  if (h == 0 && key_ok) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
+}
+
+// out = (sum over key groups of the share V partials) / (S + eps), S = the sum
+// of the row-sum partials, both in key-group order; S is also the forward's
+// ssum.  Grid: (query tiles, slices from slice0), the tiles with the most key
+// groups first.  Thread t sums elements [8 t, 8 t + 8) of the [d][32 rows]
+// partial tiles.
+template <int D>
+__global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restrict__ op,
+                                                           const float* __restrict__ rp, int64_t ntiles,
+                                                           int64_t T, float* __restrict__ out, int64_t o_sn,
+                                                           float* __restrict__ ssum, int64_t slice0) {
+  static_assert(D * kTileQ == 8 * kThreads, "one 16-byte chunk of the partial tile per thread");
+  __shared__ float sum_s[D][kTileQ + 1];
+  __shared__ float s_s[kTileQ];
+  const int64_t slice = slice0 + blockIdx.y;
+  const int nq = static_cast<int>((T + kTileQ - 1) / kTileQ);
+  const int tq = nq - 1 - static_cast<int>(blockIdx.x);
+  const int ng = min(static_cast<int>(keyq_groups(T)) - 1, tq / kKqTilesPerGroup) + 1;
+  const int t = threadIdx.x;
+  const __bf16* base = op + slice * ntiles * (D * kTileQ) + 8 * t;
+  auto tile_of = [&](int g) { return keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g; };
+  // groups in order, four loads in flight
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int g = 0;
+  for (; g + 4 <= ng; g += 4) {
+    bf16x8 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const bf16x8*>(base + tile_of(g + u) * (D * kTileQ));
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
+  }
+  for (; g < ng; ++g) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + tile_of(g) * (D * kTileQ));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
+  }
+  const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
+  if (t < kTileQ) {
+    // eight loads in flight, added in group order
+    const float* gp = rp + slice * ntiles * kTileQ + t;
+    float s = 0.f;
+    int gi = 0;
+    for (; gi + 8 <= ng; gi += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = gp[tile_of(gi + u) * kTileQ];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; gi < ng; ++gi) s += gp[tile_of(gi) * kTileQ];
+    s_s[t] = s;
+    const int64_t row = static_cast<int64_t>(tq) * kTileQ + t;
+    if (row < T) ssum[slice * T + row] = s;
+  }
+  __syncthreads();
+  // output rows: thread t takes row t / 8, head dims 8 (t % 8) + [0, 8)
+  const int row = t / (D / 8), d8 = (t % (D / 8)) * 8;
+  const int64_t grow = static_cast<int64_t>(tq) * kTileQ + row;
+  if (grow < T) {
+    const float inv = 1.f / (s_s[row] + kEps);
+    floatx4 a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] = sum_s[d8 + e][row] * inv;
+      b[e] = sum_s[d8 + 4 + e][row] * inv;
+    }
+    floatx4* o = reinterpret_cast<floatx4*>(out + slice * o_sn + grow * D + d8);
+    o[0] = a;
+    o[1] = b;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
+// The key-parallel output pass can replace fwd_demand + fwd_out where it
+// serves (bf16, head_dim 64, production operator, a chunk starting at row 0,
+// its partials -- ~1 byte per causal score element -- within the budget).
+// Measured at C3 it is not faster: fwd_keyout 1.18 ms + fwd_out_reduce 0.26 ms
+// against fwd_demand 0.45 ms + fwd_out 0.95 ms (the reduction's read of the
+// 1.1 GB of partials outweighs the exp2 sweep it saves), so it runs only when
+// the environment sets DILUTION_FORWARD_KEY_PASS=1 (read at every call, by
+// the size query as well).
+constexpr int64_t kKeyoutBudgetBytes = int64_t{24} << 30;
+
+inline bool forward_key_pass_requested() {
+  const char* e = std::getenv("DILUTION_FORWARD_KEY_PASS");
+  return e != nullptr && e[0] == '1' && e[1] == '\0';
+}
+inline int64_t keyout_partial_bytes(int64_t n, int64_t T, int D) {
+  return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
+}
+inline bool keyout_eligible(int64_t n, int64_t C, int64_t Tk, int64_t q0, int D, int prec) {
+  return prec == 2 && D == 64 && q0 == 0 && C == Tk && keyout_partial_bytes(n, Tk, D) <= kKeyoutBudgetBytes &&
+         forward_key_pass_requested();
+}
+
 struct FwdWorkspace {
-  size_t vt, kt, qc, kc, total;
+  size_t vt, kt, qc, kc, op, rp, total;
 };
 
 FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int prec, int want_pk) {
@@ -652,7 +970,15 @@ FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int 
   w.kt = w.vt + tsz;
   w.qc = w.kt + (want_pk ? tsz : 0);
   w.kc = w.qc + (convert ? align_up(ct * n * C * D) : 0);
-  w.total = w.kc + (convert ? align_up(ct * n * Tk * D) : 0);
+  w.op = w.kc + (convert ? align_up(ct * n * Tk * D) : 0);
+  w.rp = w.op;
+  w.total = w.op;
+  // the key pass's partials, when a chunk of this shape can take it (the
+  // size query does not know the chunk's start: sized whenever C == Tk)
+  if (keyout_eligible(n, C, Tk, 0, D, prec)) {
+    w.rp = w.op + align_up(static_cast<size_t>(n * keyq_tiles(Tk) * D * kTileQ * 2));
+    w.total = w.rp + align_up(static_cast<size_t>(n * keyq_tiles(Tk) * kTileQ * 4));
+  }
   return w;
 }
 
@@ -723,6 +1049,25 @@ int launch_forward(const ForwardArgs& a) {
   const dim3 grid(static_cast<unsigned>(xcd_grid(P.groups * a.n)));
   if (a.pk) DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, true, BID><<<grid, kThreads, 0, st>>>(P)));
   else DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, false, BID><<<grid, kThreads, 0, st>>>(P)));
+  if constexpr (std::is_same_v<CT, __bf16> && D == 64 && BID == BID_SOFTMAX && SHARE == SHARE_INCL) {
+    if (keyout_eligible(a.n, a.C, a.Tk, a.q0, D, kOperandPrec<CT>)) {
+      // one key pass forms the checkpoints, the totals and the share V
+      // partials; the reduction finishes out and ssum
+      __bf16* op = reinterpret_cast<__bf16*>(ws + w.op);
+      float* rp = reinterpret_cast<float*>(ws + w.rp);
+      const int64_t ntiles = keyq_tiles(a.Tk);
+      P.kgroups = static_cast<int>(keyq_groups(a.Tk));
+      const dim3 gko(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
+      DIL_TIMED("fwd_keyout", st, (fwd_keyout<D><<<gko, kKqThreads, 0, st>>>(P, op, rp, ntiles)));
+      const unsigned nq = static_cast<unsigned>((a.Tk + kTileQ - 1) / kTileQ);
+      slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+        DIL_TIMED("fwd_out_reduce", st,
+                  (fwd_out_reduce<D><<<dim3(nq, ns), kThreads, 0, st>>>(op, rp, ntiles, a.Tk, a.out, a.o_sn,
+                                                                       a.ssum, s0)));
+      });
+      return static_cast<int>(hipGetLastError());
+    }
+  }
   P.kgroups = static_cast<int>((a.Tk + 4 * kTileK - 1) / (4 * kTileK));
   DIL_TIMED("fwd_demand", st,
             (fwd_demand<CT, D, BID><<<dim3(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n))),

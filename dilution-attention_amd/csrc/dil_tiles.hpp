@@ -147,6 +147,41 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepJobs jobs, int dt, i
 }
 
 // ---------------------------------------------------------------------------
+// Key groups of the key-parallel passes that form a row-side product (the
+// backward's dq, the forward's share V): 8 waves of 32 keys = 256 keys per
+// workgroup.  A group's per-(group, 32-row tile) partials are stored
+// compactly: key group g meets query tiles [8 g, nq), and tile (g, qt) sits
+// at keyq_tile_base(g, nq) + qt - 8 g.
+
+constexpr int kKqWaves = 8;
+constexpr int kKqThreads = 64 * kKqWaves;
+constexpr int kKqKeys = kKqWaves * kTileK;        // 256 keys per workgroup
+constexpr int kKqTilesPerGroup = kKqKeys / kTileQ;  // query tiles spanned by a key group
+constexpr int kPdStride = kKqKeys + 8;            // bf16 per staged row (+16 B: bank offset)
+
+__host__ __device__ inline int64_t keyq_tile_base(int64_t g, int64_t nq) {
+  return g * nq - static_cast<int64_t>(kKqTilesPerGroup) * g * (g - 1) / 2;
+}
+__host__ __device__ inline int64_t keyq_groups(int64_t T) { return (T + kKqKeys - 1) / kKqKeys; }
+__host__ __device__ inline int64_t keyq_tiles(int64_t T) {
+  const int64_t nq = (T + kTileQ - 1) / kTileQ;
+  return keyq_tile_base(keyq_groups(T), nq);
+}
+
+// 16 consecutive floats of LDS into registers (four 16-byte reads).
+__device__ __forceinline__ void lds_read16(const float* src, float (&v)[16]) {
+  const floatx4* p = reinterpret_cast<const floatx4*>(src);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const floatx4 x = p[u];
+    v[4 * u] = x[0];
+    v[4 * u + 1] = x[1];
+    v[4 * u + 2] = x[2];
+    v[4 * u + 3] = x[3];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // LDS staging of 32-row tiles
 
 template <typename CT, int D>

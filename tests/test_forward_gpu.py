@@ -262,3 +262,41 @@ def test_precision_argument_errors():
     with pytest.raises(ValueError):
         x = torch.zeros(1, 1, 4, 48, device="cuda")
         kernels.dilution_attention_forward(x, x, x)
+
+
+@pytest.mark.parametrize("seq", [1, 33, 257, 1000, 2048])
+def test_forward_key_pass_matches_three_pass(seq, monkeypatch):
+    """The key-parallel output pass (fwd_keyout + fwd_out_reduce, selected by
+    DILUTION_FORWARD_KEY_PASS=1) against the default three-pass forward and
+    the oracle: bf16 outputs at the bf16 bounds, the demand checkpoints
+    (causal part), totals and row sums of shares within fp32 summation-order
+    differences; gradients through it within the bf16 gradient bound."""
+    from dilution import kernels
+
+    q, k, v, do = orc.make_inputs((2, 4, seq, 64), seed=300 + seq, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    qg, kg, vg = (x.cuda() for x in (q, k, v))
+    out0, aux0 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True,
+                                                    _save_pk=True)
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
+    out1, aux1 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True,
+                                                    _save_pk=True)
+    want = orc.attention_fp32(q, k, v)
+    assert max_abs(out1, want) < 2e-2 and mean_rel(out1, want) < 1e-2
+    assert max_abs(out1, out0) < 1e-2
+    assert max_abs(aux1["committed_total"], aux0["committed_total"]) < 1e-5
+    # the two passes add each key's demand in a different fp32 order, so a
+    # share on a bf16 rounding boundary may round to the other neighbour: the
+    # row sums of the bf16 shares then differ by a few bf16 steps of a share
+    assert max_abs(aux1["ssum"], aux0["ssum"]) < 2e-2
+    carry0 = aux0["carry"].reshape(2, 4, -1, seq)
+    carry1 = aux1["carry"].reshape(2, 4, -1, seq)
+    for rb in range(carry0.shape[2]):
+        end = min(32 * (rb + 1), seq)
+        assert max_abs(carry1[:, :, rb, :end], carry0[:, :, rb, :end]) < 1e-5, rb
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="bf16")
+    out.backward(do.cuda())
+    (dq, dk, dv), _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
+    for name, g, w in zip(("dq", "dk", "dv"), (x.grad for x in xs), (dq, dk, dv)):
+        assert max_abs(g, torch.from_numpy(w)) < 5e-2, name
