@@ -1155,19 +1155,24 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     }
   };
 
+  const int late_dq = (threadIdx.x >> 8) ^ 1;     // wave-uniform: 1 for waves 0-3
   fetch(nq - 1);
   stash(0);
   __syncthreads();
   // the stash is unconditional (the last iteration stashes into the idle
   // buffer).  The dq product of tile qt + 1 (staged before the previous
-  // barrier, in the other buffer) runs after step qt's stash, before this
-  // step's barrier, which the stage of tile qt - 1 into that buffer follows.
-  // Issued after the stash, its partial store is not among the memory
-  // operations the stash waits for, so no step waits for its own store.
+  // barrier, in the other buffer) runs anywhere before this step's barrier,
+  // which the stage of tile qt - 1 into that buffer follows.  Waves w and
+  // w + 4 share a SIMD, and the barrier starts both in the same phase: waves
+  // 4-7 run the dq product before their step, waves 0-3 after their stash,
+  // so one wave's MFMA work issues under the other's VALU chain (-3% on this
+  // kernel).  Both issue the partial store after the tile fetch, so the
+  // stash, which waits for the fetch only, never waits for a store.
   auto iter = [&](int j, int buf) __attribute__((always_inline)) {
     const int qt = nq - 1 - j;                   // query tiles in reverse
     fetch(max(qt - 1, kb0));                     // the last step reloads its own tile, unused
     const int prev = j > 0 ? qt + 1 : -1;
+    if (late_dq == 0) dq_product(prev, buf ^ 1);
     if (active && qt >= kb) {
       if (qt > kb) step(buf, std::false_type{});
       else step(buf, std::true_type{});
@@ -1175,7 +1180,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
       stage_zero(buf);
     }
     stash(buf ^ 1);
-    dq_product(prev, buf ^ 1);
+    if (late_dq != 0) dq_product(prev, buf ^ 1);
     sync_lds();
   };
   double_buffered<false>(0, nq - kb0, iter);
