@@ -1234,14 +1234,14 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   for (; g + 4 <= ng; g += 4) {
     bf16x8 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const bf16x8*>(base + tile_of(g + u) * (D * kTileQ));
+    for (int u = 0; u < 4; ++u) v[u] = load_once(base + tile_of(g + u) * (D * kTileQ));
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
   }
   for (; g < ng; ++g) {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + tile_of(g) * (D * kTileQ));
+    const bf16x8 v = load_once(base + tile_of(g) * (D * kTileQ));
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
   }
@@ -1256,11 +1256,11 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
     for (; gi + 8 <= ng; gi += 8) {
       float v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = gp[tile_of(gi + u) * kTileQ];
+      for (int u = 0; u < 8; ++u) v[u] = load_once(gp + tile_of(gi + u) * kTileQ);
 #pragma unroll
       for (int u = 0; u < 8; ++u) s += v[u];
     }
-    for (; gi < ng; ++gi) s += gp[tile_of(gi) * kTileQ];
+    for (; gi < ng; ++gi) s += load_once(gp + tile_of(gi) * kTileQ);
     g_s[t] = s;
   }
   __syncthreads();

