@@ -157,7 +157,10 @@ constexpr int kKqWaves = 8;
 constexpr int kKqThreads = 64 * kKqWaves;
 constexpr int kKqKeys = kKqWaves * kTileK;        // 256 keys per workgroup
 constexpr int kKqTilesPerGroup = kKqKeys / kTileQ;  // query tiles spanned by a key group
-constexpr int kPdStride = kKqKeys + 8;            // bf16 per staged row (+16 B: bank offset)
+// bf16 per staged row: the 16-byte pad leaves the 8-byte stage writes and the
+// product's 16-byte reads 2-way bank-conflicted (512-byte rows would be
+// 16-way); a fully conflict-free layout measured no faster
+constexpr int kPdStride = kKqKeys + 8;
 
 __host__ __device__ inline int64_t keyq_tile_base(int64_t g, int64_t nq) {
   return g * nq - static_cast<int64_t>(kKqTilesPerGroup) * g * (g - 1) / 2;
