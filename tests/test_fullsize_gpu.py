@@ -14,6 +14,11 @@ every slice.
   - rows of the attention matrix sum to one, so sum_j dv_j = sum_i dO_i.  The
     kernel rounds the share tile, dO / (S + eps) and dv to bf16 (relative
     error <= 2^-9 each), which bounds the gap by 2^-8 (sum |dv| + sum |dO|).
+* The same shape through the key-parallel output pass
+  (DILUTION_FORWARD_KEY_PASS=1): outputs of slices 0 and 15 against the
+  blocked oracle, every output against the default forward (1e-2), demand
+  totals and checkpoints within fp32 summation-order differences (1e-5
+  relative), and dq, dk, dv of slices 0 and 15 against the device oracle.
 * The same shape in fp32 operands: outputs and dq, dk, dv of slices 0 and 15
   against ``grads_blocked_f64`` on the host and of every slice on the device
   (1e-4 max-abs); sum_j dk_j = 0 (adding a constant to every key leaves each
@@ -100,6 +105,42 @@ def test_c3_training_bf16_full_size():
     for h in (0, 15):
         want, _ = _grads_oracle(q, k, v, do, (0, h), "cpu")
         _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (host oracle)")
+
+
+def test_c3_key_pass_full_size(monkeypatch):
+    from dilution import kernels
+
+    q, k, v, do = orc.make_inputs((1, 16, 16384, 64), seed=4, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    qg, kg, vg = (t.cuda() for t in (q, k, v))
+    out0, aux0 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True)
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
+    out1, aux1 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True)
+    torch.cuda.synchronize()
+    for h in (0, 15):
+        want, tot = _blocked(q[0, h], k[0, h], v[0, h])
+        assert max_abs(out1[0, h], want) < 2e-2, h
+        assert mean_rel(out1[0, h], want) < 1e-2, h
+        rel = (aux1["committed_total"][0, h].double().cpu() - tot).abs() / tot.abs().clamp(min=1.0)
+        assert rel.max().item() < 1e-5, h
+    assert max_abs(out1, out0) < 1e-2
+    t0, t1 = aux0["committed_total"].double(), aux1["committed_total"].double()
+    assert ((t1 - t0).abs() / t0.abs().clamp(min=1.0)).max().item() < 1e-5
+    # checkpoints: the causal part of every 32-row block (keys before the block's end)
+    c0 = aux0["carry"].reshape(1, 16, -1, 16384).double()
+    c1 = aux1["carry"].reshape(1, 16, -1, 16384).double()
+    keys = torch.arange(16384, device=c0.device)
+    ends = 32 * (torch.arange(c0.shape[2], device=c0.device) + 1)
+    causal = keys[None, :] < ends[:, None]
+    diff = ((c1 - c0).abs() / c0.abs().clamp(min=1.0))[..., causal]
+    assert diff.max().item() < 1e-5
+    xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
+    out = kernels.dilution_attention(*xs, dot_precision="bf16")
+    out.backward(do.cuda())
+    grads = [x.grad for x in xs]
+    for h in (0, 15):
+        want, _ = _grads_oracle(q, k, v, do, (0, h), "cuda")
+        _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (device oracle, key pass)")
 
 
 def test_c3_training_fp32_full_size():
