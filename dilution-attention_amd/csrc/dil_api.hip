@@ -138,7 +138,8 @@ int dil_decode_step_dlen(const void* q1, const void* k_cache, const void* v_cach
 
 int64_t dil_forward_workspace_bytes(int64_t n, int64_t seq, int head_dim, int dtype,
                                     int precision, int want_pk) {
-  return dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision, want_pk);
+  return dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision, want_pk,
+                                      dil::forward_key_pass_requested());
 }
 
 int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, int64_t seq,
@@ -155,10 +156,12 @@ int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, 
                static_cast<const void*>(carry), static_cast<const void*>(committed_total),
                static_cast<const void*>(workspace)))
     return dil::kErrShape;
+  const bool key_pass = dil::forward_key_pass_requested();
   if (workspace_bytes <
-      dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision, pk != nullptr))
+      dil::forward_workspace_bytes(n, seq, seq, head_dim, dtype, precision, pk != nullptr, key_pass))
     return dil::kErrWorkspace;
   dil::ForwardArgs a{};
+  a.key_pass = key_pass;
   a.q = q;
   a.q_sn = seq * head_dim;
   a.k = k;
@@ -200,7 +203,8 @@ int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t 
 
 int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
                                     int dtype, int precision) {
-  return dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0);
+  return dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0,
+                                      dil::forward_key_pass_requested());
 }
 
 int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_cache, int64_t n,
@@ -217,10 +221,12 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
                static_cast<const void*>(rden), static_cast<const void*>(ssum),
                static_cast<const void*>(carry), static_cast<const void*>(workspace)))
     return dil::kErrShape;
+  const bool key_pass = dil::forward_key_pass_requested();
   if (workspace_bytes <
-      dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0))
+      dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0, key_pass))
     return dil::kErrWorkspace;
   dil::ForwardArgs a{};
+  a.key_pass = key_pass;
   a.q = q_chunk;
   a.q_sn = chunk * head_dim;
   a.k = k_cache;

@@ -19,8 +19,8 @@ int dispatch_forward(const ForwardArgs& a) {
 }  // namespace
 
 int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int prec,
-                                int want_pk) {
-  return static_cast<int64_t>(fwd_layout(n, C, Tk, head_dim, dtype, prec, want_pk).total);
+                                int want_pk, bool key_pass) {
+  return static_cast<int64_t>(fwd_layout(n, C, Tk, head_dim, dtype, prec, want_pk, key_pass).total);
 }
 
 int forward(const ForwardArgs& a) {

@@ -33,7 +33,6 @@
 #include "dil_tiles.hpp"
 #include "dil_variant.hpp"
 
-#include <cstdlib>
 #include <type_traits>
 
 namespace dil {
@@ -944,27 +943,24 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
 // Measured at C3 it is not faster: fwd_keyout 1.18 ms + fwd_out_reduce 0.26 ms
 // against fwd_demand 0.45 ms + fwd_out 0.95 ms (the reduction's read of the
 // 1.1 GB of partials outweighs the exp2 sweep it saves), so it runs only when
-// the environment sets DILUTION_FORWARD_KEY_PASS=1 (read at every call, by
-// the size query as well).
+// the environment sets DILUTION_FORWARD_KEY_PASS=1 (read once by each call
+// and by each size query: ForwardArgs::key_pass).
 constexpr int64_t kKeyoutBudgetBytes = int64_t{24} << 30;
 
-inline bool forward_key_pass_requested() {
-  const char* e = std::getenv("DILUTION_FORWARD_KEY_PASS");
-  return e != nullptr && e[0] == '1' && e[1] == '\0';
-}
 inline int64_t keyout_partial_bytes(int64_t n, int64_t T, int D) {
   return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
 }
-inline bool keyout_eligible(int64_t n, int64_t C, int64_t Tk, int64_t q0, int D, int prec) {
-  return prec == 2 && D == 64 && q0 == 0 && C == Tk && keyout_partial_bytes(n, Tk, D) <= kKeyoutBudgetBytes &&
-         forward_key_pass_requested();
+inline bool keyout_eligible(int64_t n, int64_t C, int64_t Tk, int64_t q0, int D, int prec, bool requested) {
+  return requested && prec == 2 && D == 64 && q0 == 0 && C == Tk &&
+         keyout_partial_bytes(n, Tk, D) <= kKeyoutBudgetBytes;
 }
 
 struct FwdWorkspace {
   size_t vt, kt, qc, kc, op, rp, total;
 };
 
-FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int prec, int want_pk) {
+FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int prec, int want_pk,
+                        bool key_pass) {
   const size_t ct = prec == 2 ? 2 : 4;
   const bool convert = dtype != native_dtype(prec);
   FwdWorkspace w{};
@@ -978,7 +974,7 @@ FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int 
   w.total = w.op;
   // the key pass's partials, when a chunk of this shape can take it (the
   // size query does not know the chunk's start: sized whenever C == Tk)
-  if (keyout_eligible(n, C, Tk, 0, D, prec)) {
+  if (keyout_eligible(n, C, Tk, 0, D, prec, key_pass)) {
     w.rp = w.op + align_up(static_cast<size_t>(n * keyq_tiles(Tk) * D * kTileQ * 2));
     w.total = w.rp + align_up(static_cast<size_t>(n * keyq_tiles(Tk) * kTileQ * 4));
   }
@@ -987,7 +983,7 @@ FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int 
 
 template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 int launch_forward(const ForwardArgs& a) {
-  const FwdWorkspace w = fwd_layout(a.n, a.C, a.Tk, D, a.dtype, kOperandPrec<CT>, a.pk != nullptr);
+  const FwdWorkspace w = fwd_layout(a.n, a.C, a.Tk, D, a.dtype, kOperandPrec<CT>, a.pk != nullptr, a.key_pass);
   char* ws = static_cast<char*>(a.workspace);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const bool convert = a.dtype != kNativeDtype<CT>;
@@ -1053,7 +1049,7 @@ int launch_forward(const ForwardArgs& a) {
   if (a.pk) DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, true, BID><<<grid, kThreads, 0, st>>>(P)));
   else DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, false, BID><<<grid, kThreads, 0, st>>>(P)));
   if constexpr (std::is_same_v<CT, __bf16> && D == 64 && BID == BID_SOFTMAX && SHARE == SHARE_INCL) {
-    if (keyout_eligible(a.n, a.C, a.Tk, a.q0, D, kOperandPrec<CT>)) {
+    if (keyout_eligible(a.n, a.C, a.Tk, a.q0, D, kOperandPrec<CT>, a.key_pass)) {
       // one key pass forms the checkpoints, the totals and the share V
       // partials; the reduction finishes out and ssum
       __bf16* op = reinterpret_cast<__bf16*>(ws + w.op);

@@ -3,6 +3,7 @@
 
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace dil {
 
@@ -108,13 +109,23 @@ struct ForwardArgs {
   int64_t tot_sn;
   float* pk;             // (n, C, D) fp32 scale * jac @ k (jac = p for softmax bids), or null
   Variant var;
+  bool key_pass;         // the key-parallel output pass is requested (read once per call)
   void* workspace;
   int64_t workspace_bytes;
   void* stream;
 };
 
+// DILUTION_FORWARD_KEY_PASS=1 requests the key-parallel output pass for the
+// calls that can take it.  Each entry point reads it once and hands the
+// answer to both its workspace check and its launch, so a change of the
+// variable between the two cannot make them disagree.
+inline bool forward_key_pass_requested() {
+  const char* e = getenv("DILUTION_FORWARD_KEY_PASS");
+  return e != nullptr && e[0] == '1' && e[1] == '\0';
+}
+
 int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int prec,
-                                int want_pk);
+                                int want_pk, bool key_pass);
 int forward(const ForwardArgs& a);
 
 struct BackwardArgs {
