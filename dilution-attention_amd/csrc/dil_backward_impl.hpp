@@ -1007,13 +1007,16 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
   const bool ck_ok = ck < P.T && !second;
   const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
   float cr = 0.f;
+  // whole-slice resources, built once: the tile offset advances a 32-bit
+  // per-lane offset (rows past T read as zeros through the resource bound)
+  const auto rres = make_rsrc(rsrc, P.T * D * static_cast<int64_t>(sizeof(CT)));
+  const auto tres = make_rsrc(tsrc, D * P.t_pad * static_cast<int64_t>(sizeof(CT)));
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-    const int64_t rows = min(max(P.T - row0, int64_t{0}), int64_t{kTileQ});
-    rr = buffer_load16<bf16x8>(make_rsrc(rsrc + row0 * D, rows * D * static_cast<int64_t>(sizeof(CT))),
-                               static_cast<uint32_t>(c256 * 16), 0);
-    tr = buffer_load16<bf16x8>(make_rsrc(tsrc + row0 * D, kTileQ * D * static_cast<int64_t>(sizeof(CT))),
-                               static_cast<uint32_t>(c256 * 16), 0);
+    const uint32_t off = static_cast<uint32_t>(qt) * static_cast<uint32_t>(kTileQ * D * sizeof(CT)) +
+                         static_cast<uint32_t>(c256 * 16);
+    rr = buffer_load16<bf16x8>(rres, off, 0);
+    tr = buffer_load16<bf16x8>(tres, off, 0);
     sl.load(lse, dbs, dbs, row0, P.T);
     cr = ccol[static_cast<int64_t>(qt) * P.T];
   };
@@ -1306,7 +1309,11 @@ inline int64_t keyq_partial_bytes(int64_t n, int64_t T, int D) {
   return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
 }
 inline bool keyq_eligible(int64_t n, int64_t T, int D, int prec) {
-  return prec == 2 && D == 64 && keyq_partial_bytes(n, T, D) <= kKeyqBudgetBytes;
+  // bwd_keyq reads the Q, dO' rows and their transposed copies through one
+  // buffer resource per slice, which covers at most 2^31 - 1 bytes (the
+  // budget already keeps T far below that: T^2 / 16 partials per slice)
+  const int64_t slice_bytes = static_cast<int64_t>(D) * pad64(T) * 2;
+  return prec == 2 && D == 64 && keyq_partial_bytes(n, T, D) <= kKeyqBudgetBytes && slice_bytes < (int64_t{1} << 31);
 }
 
 BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, int prec) {
