@@ -31,6 +31,11 @@
 //               keeps dO' and the identity in LDS: three workgroups per CU.
 //   prep_ghat_q (ghat * Q)^T tiles for the correction.
 //   bwd_dkcorr  one wave per key tile: dk = s dk_main - s sum_i p_ij (ghat_i q_i).
+//   bwd_keyq    (bf16 operands, head_dim 64) bwd_key and bwd_query's dq in one
+//               walk of 256 keys per workgroup: dq partials per key group,
+//               summed in order by bwd_dq_reduce, which also writes the
+//               (ghat * Q)^T tiles; it replaces bwd_key, bwd_query and
+//               prep_ghat_q for every bid / share pair.
 #pragma once
 
 #include "dil_common.hpp"
@@ -915,18 +920,24 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 // [8 g, nq), tile (g, qt) sits at keyq_tile_base(g, nq) + qt - 8 g (the
 // key-group constants and this indexing live with the tile helpers: the
 // forward's key pass uses them too).
+//
+// The bid / share variants run the same walk with bwd_key's variant chain:
+// the per-row parameter r1 is staged with the statistics, the dk and dq
+// operand is jac dp, the ratio bids' ghat partials are the row sums of p dp
+// (a second transposed tile), and the elementwise bids have none.
 
-template <int D>
+template <int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* __restrict__ dqp,
                                                            float* __restrict__ ghp, int64_t ntiles) {
   static_assert(D == 64, "the dq-forming key pass is built for head_dim 64");
   using CT = __bf16;
   using TL = Tiles<CT, D>;
+  constexpr int kNS = BID == BID_SOFTMAX ? 2 : 3;                // per-row statistics staged
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
   __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
-  // lse, -dbs of the tile's rows, then padding: every thread of the stash writes a slot
+  // lse (r0), -dbs, r1 of the tile's rows, then padding: every thread of the stash writes a slot
   __shared__ __attribute__((aligned(16))) float st_s[2][kKqThreads];
   __shared__ float cs_s[2][kKqKeys];                                   // demand entering the tile
   __shared__ __attribute__((aligned(16))) CT pd_s[2][kTileQ * kPdStride];   // (p dp), [row][key]
@@ -1002,7 +1013,8 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
   const CT* rsrc = second ? dos : qs;
   const CT* tsrc = second ? dots : qts;
   bf16x8 rr = {}, tr = {};
-  RowStatsLoader<2> sl;
+  RowStatsLoader<kNS> sl;
+  if constexpr (!bid_log2<BID>()) sl.pad0 = 0.f;
   const int64_t ck = static_cast<int64_t>(kb0) * kTileK + c256;
   const bool ck_ok = ck < P.T && !second;
   const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
@@ -1017,7 +1029,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
                          static_cast<uint32_t>(c256 * 16);
     rr = buffer_load16<bf16x8>(rres, off, 0);
     tr = buffer_load16<bf16x8>(tres, off, 0);
-    sl.load(lse, dbs, dbs, row0, P.T);
+    sl.load(lse, dbs, BID == BID_SOFTMAX ? dbs : P.rb1 + slice * P.T, row0, P.T);
     cr = ccol[static_cast<int64_t>(qt) * P.T];
   };
   auto stash = [&](int buf) {
@@ -1063,21 +1075,41 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
     lds_read16(st + 16 * h, lz);
     float p[16], x[16], sh[16], w[16];
+    [[maybe_unused]] float jac[16];
+    if constexpr (BID == BID_SOFTMAX) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
+      for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[i], P.c, -lz[i]));
+    } else {
+      float r1[16];
+      lds_read16(st + 2 * kTileQ + 16 * h, r1);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        p[i] = bid_p<BID>(sacc[i], P.c, P.scale, lz[i], r1[i], P.lshift);
+        jac[i] = bid_jac<BID>(p[i], sacc[i], P.scale, lz[i]);
+      }
+    }
     if constexpr (DIAG) {
       const int dk = l32 - 16 * h;               // key - row(i) = dk - i on the diagonal tile
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        if (dk > i) p[i] = 0.f;
+        if (dk > i) {
+          p[i] = 0.f;
+          if constexpr (BID != BID_SOFTMAX) jac[i] = 0.f;
+        }
     }
+    if constexpr (SHARE != SHARE_NONE) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = p[i];
-    scan_incl_qs(x, cin + kEps, hf);               // demand + p + eps
+      for (int i = 0; i < 16; ++i) x[i] = p[i];
+      if constexpr (SHARE == SHARE_EXCL) scan_excl_qs(x, cin + kEps, hf);   // demand + eps
+      else scan_incl_qs(x, cin + kEps, hf);                                // demand + p + eps
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x[i] = fast_rcp(x[i]);                       // inv
-      sh[i] = p[i] * x[i];
+      for (int i = 0; i < 16; ++i) {
+        x[i] = fast_rcp(x[i]);                     // inv
+        sh[i] = p[i] * x[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sh[i] = p[i];
     }
     // dv^T += dO'^T sh  (keys in lanes; dO' carries the 1/(S+eps) of A)
 #pragma unroll
@@ -1087,15 +1119,45 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
       for (int t = 0; t < kDTiles<D>; ++t)
         dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
     }
+    if constexpr (is_production<BID, SHARE>()) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      w[i] = dov[i] * sh[i];                       // ds sh
-      x[i] = w[i] * x[i];                          // g = ds sh inv
+      for (int i = 0; i < 16; ++i) {
+        w[i] = dov[i] * sh[i];                     // ds sh
+        x[i] = w[i] * x[i];                        // g = ds sh inv
+      }
+      sufk += scan_suffix_qs(x, sufk, hf);         // x = G
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i] = fmaf(-p[i], x[i], w[i]);   // p dp = ds sh - p G
+    } else {
+      // dp = ds inv - G (+ g for the exclusive share; ds with no share step);
+      // the MFMA operand is jac dp (jac = p for the log2 bids)
+      if constexpr (SHARE != SHARE_NONE) {
+        float g[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          w[i] = dov[i] * x[i];                    // ds inv
+          g[i] = w[i] * sh[i];                     // ds sh inv
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = g[i];
+        sufk += scan_suffix_qs(x, sufk, hf);       // x = G
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          w[i] -= x[i];
+          if constexpr (SHARE == SHARE_EXCL) w[i] += g[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = dov[i];
+      }
+      if constexpr (bid_ratio<BID>()) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = p[i] * w[i];   // p dp, the ghat operand
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i] *= bid_log2<BID>() ? p[i] : jac[i];
     }
-    sufk += scan_suffix_qs(x, sufk, hf);           // x = G
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = fmaf(-p[i], x[i], w[i]);   // p dp = ds sh - p G
-    // dk_main^T += Q^T (p dp), and the transposed (p dp) for dq
+    // dk_main^T += Q^T (jac dp), and the transposed (jac dp) for dq
     floatx16 xt = floatx16{};
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
@@ -1114,8 +1176,21 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     // multiplies): all-ones A against the transposed tile, every register of
     // the result holds its lane's row sum
     floatx16 gs = floatx16{};
+    if constexpr (bid_log2<BID>() && bid_normalized<BID>()) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) gs = Mma<CT>::mma(ones8, xf[s], gs);
+      for (int s = 0; s < 2; ++s) gs = Mma<CT>::mma(ones8, xf[s], gs);
+    } else if constexpr (bid_normalized<BID>()) {
+      // ghat needs the row sums of p dp, a different tile from the dq operand
+      floatx16 yt = floatx16{};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) yt = Mma<CT>::mma(acc_frag<CT>(x, s), id_park[s][lane], yt);
+      float yv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) yv[i] = yt[i];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) gs = Mma<CT>::mma(ones8, acc_frag<CT>(yv, s), gs);
+    }
+    // (the elementwise bids have no row normalisation: their ghat is zero)
     if (h == 0) gh_s[buf][wave][l32] = gs[0];
   };
   // a wave whose keys all follow the tile's rows contributes nothing
@@ -1213,7 +1288,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
 // tiles of the dk correction.  Grid: (query tiles, slices from slice0), the
 // tiles with the most key groups first.  Thread t sums elements [8 t, 8 t + 8)
 // of the [d][32 rows] partial tiles.
-template <int D>
+template <int D, bool GHAT = true>
 __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restrict__ dqp,
                                                           const float* __restrict__ ghp, int64_t ntiles,
                                                           int64_t T, const float* __restrict__ pk,
@@ -1251,7 +1326,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
 #pragma unroll
   for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
-  if (t < kTileQ) {
+  if (GHAT && t < kTileQ) {
     // eight loads in flight, added in group order
     const float* gp = ghp + slice * ntiles * kTileQ + t;
     float s = 0.f;
@@ -1267,8 +1342,9 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
     g_s[t] = s;
   }
   __syncthreads();
-  // (ghat * q)^T: the same [d][32 rows] chunk of the tile-major Q^T copy
-  {
+  // (ghat * q)^T: the same [d][32 rows] chunk of the tile-major Q^T copy (the
+  // elementwise bids have no ghat and no dk correction)
+  if constexpr (GHAT) {
     const int64_t off = slice * D * t_pad + tmajor_index(static_cast<int64_t>(tq) * kTileQ + r8, d, D);
     const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qt + off);
     float v[8];
@@ -1280,14 +1356,19 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   const int row = t / (D / 8), d8 = (t % (D / 8)) * 8;
   const int64_t grow = static_cast<int64_t>(tq) * kTileQ + row;
   if (grow < T) {
-    const float gr = g_s[row];
     const int64_t o = (slice * T + grow) * D + d8;
-    const floatx4* pk4 = reinterpret_cast<const floatx4*>(pk + o);
-    const floatx4 pa = pk4[0], pb = pk4[1];
-    const float pkv[8] = {pa[0], pa[1], pa[2], pa[3], pb[0], pb[1], pb[2], pb[3]};
     float v[8];
+    if constexpr (GHAT) {
+      const float gr = g_s[row];
+      const floatx4* pk4 = reinterpret_cast<const floatx4*>(pk + o);
+      const floatx4 pa = pk4[0], pb = pk4[1];
+      const float pkv[8] = {pa[0], pa[1], pa[2], pa[3], pb[0], pb[1], pb[2], pb[3]};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = sum_s[d8 + e][row] * scale - gr * pkv[e];
+      for (int e = 0; e < 8; ++e) v[e] = sum_s[d8 + e][row] * scale - gr * pkv[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = sum_s[d8 + e][row] * scale;
+    }
     store8_as(dq, o, gdt, v);
   }
 }
@@ -1428,7 +1509,7 @@ int launch_backward(const BackwardArgs& a) {
   });
   const int nkt = static_cast<int>((a.T + kTileK - 1) / kTileK);
   P.n = a.n;
-  if constexpr (std::is_same_v<CT, __bf16> && D == 64 && is_production<BID, SHARE>()) {
+  if constexpr (std::is_same_v<CT, __bf16> && D == 64) {
     if (keyq_eligible(a.n, a.T, D, kOperandPrec<CT>)) {
       // one key pass forms dv, dk_main and the dq partials; the reduction
       // finishes dq and writes the (ghat q)^T tiles of the dk correction
@@ -1437,12 +1518,13 @@ int launch_backward(const BackwardArgs& a) {
       const int64_t ntiles = keyq_tiles(a.T);
       P.kgroups = static_cast<int>(keyq_groups(a.T));
       const dim3 gkq(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
-      DIL_TIMED("bwd_keyq", st, (bwd_keyq<D><<<gkq, kKqThreads, 0, st>>>(P, dqp, ghp, ntiles)));
+      DIL_TIMED("bwd_keyq", st, (bwd_keyq<D, BID, SHARE><<<gkq, kKqThreads, 0, st>>>(P, dqp, ghp, ntiles)));
       const unsigned nq = static_cast<unsigned>((a.T + kTileQ - 1) / kTileQ);
       slice_batches(a.n, [&](int64_t s0, unsigned ns) {
+        constexpr bool kGhat = bid_normalized<BID>();   // the elementwise bids have no ghat
         DIL_TIMED("bwd_dq_reduce", st,
-                  (bwd_dq_reduce<D><<<dim3(nq, ns), kThreads, 0, st>>>(dqp, ghp, ntiles, a.T, a.pk, qt, t_pad,
-                                                                      a.dq, a.grad_dtype, P.scale, qgt, s0)));
+                  (bwd_dq_reduce<D, kGhat><<<dim3(nq, ns), kThreads, 0, st>>>(dqp, ghp, ntiles, a.T, a.pk, qt, t_pad,
+                                                                             a.dq, a.grad_dtype, P.scale, qgt, s0)));
       });
       P.kgroups = (nkt + 3) / 4;
       const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));

@@ -87,6 +87,31 @@ def test_variant_backward_bf16(bid):
         assert rel < bound, f"{bid} {name} relative error {rel}"
 
 
+@pytest.mark.parametrize("bid", orc.BIDS)
+@pytest.mark.parametrize("share", [False, "exclusive"], ids=str)
+def test_variant_backward_bf16_other_shares(bid, share):
+    """bf16 operands at head_dim 64 (the one-pass backward) with no share step
+    (dq, dk, dv) and with the exclusive share (dv only: its dq / dk cancel
+    1e9-scale terms, see below), against the fp64 autograd oracle on the
+    bf16-rounded inputs, relative to the largest gradient: 1e-2, relu2 2.5e-2."""
+    from dilution import kernels_bid as kb
+
+    q, k, v, do = (x.to(torch.bfloat16) for x in orc.make_inputs((1, 4, 200, 64), seed=43, qk_scale=0.5,
+                                                                  with_dout=True))
+    ref = [x.double().requires_grad_(True) for x in (q, k, v)]
+    orc.variant_attention_f64(*ref, bid, share, SHIFT).backward(do.double())
+    xs = [x.cuda().requires_grad_(True) for x in (q, k, v)]
+    kb.dilution_attention(*xs, dot_precision="bf16", bid=bid, share_cumsum=share,
+                          shift=SHIFT).backward(do.cuda())
+    bound = 2.5e-2 if bid == "relu2" else 1e-2
+    checked = ("dq", "dk", "dv") if share is False else ("dv",)
+    for name, r, x in zip(("dq", "dk", "dv"), ref, xs):
+        if name not in checked:
+            continue
+        rel = max_abs(x.grad, r.grad) / (r.grad.abs().max().item() + 1e-6)
+        assert rel < bound, f"{bid} {share} {name} relative error {rel}"
+
+
 @pytest.mark.parametrize("bid", ["softmax", "relu", "sigmoid"])
 def test_variant_exclusive_backward_dv(bid):
     """The exclusive share's dq/dk are fp32 noise on cancelling 1e9-scale terms
