@@ -26,7 +26,7 @@ namespace dil {
 int check_variant(const Variant& v, int head_dim) {
   if (v.bid < 0 || v.bid >= kNumBids || v.share < SHARE_NONE || v.share > SHARE_EXCL || !(v.shift > 0.f))
     return kErrVariant;
-  if ((v.bid != BID_SOFTMAX || v.share != SHARE_INCL) && head_dim != kVariantHeadDim) return kErrVariant;
+  (void)head_dim;                            // every variant is built for every valid head_dim
   return 0;
 }
 
@@ -45,8 +45,7 @@ const char* dil_status_string(int status) {
     case dil::kErrShape: return "invalid shape or length";
     case dil::kErrPrecision: return "dot_precision must be one of ieee, tf32, bf16";
     case dil::kErrVariant:
-      return "operator variant out of range (bid 0-7, share 0-2, shift > 0) or not built for this "
-             "head_dim (the ablation variants are built for head_dim 64)";
+      return "operator variant out of range (bid 0-7, share 0-2, shift > 0)";
     case dil::kErrScratch:
       return "the call needs more scratch than dil_decode_step_noalloc holds "
              "(DIL_NOALLOC_SCRATCH_BYTES); use dil_decode_step with a workspace";

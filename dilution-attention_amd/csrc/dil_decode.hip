@@ -1,6 +1,6 @@
 // Entry points of the cached decode step: the production operator for every
 // head_dim and dtype; the ablation variants are built in dil_variants.hip
-// (head_dim 64) and reached through decode_bid<BID>.
+// (every head_dim) and reached through decode_bid<BID>.
 #include "dil_decode_impl.hpp"
 
 namespace dil {

@@ -19,14 +19,13 @@ constexpr int kErrScratch = -7;
 
 // Operator variant (the reference's kernels_bid ablations): bid function
 // 0..7, share mode 0 (none) / 1 (dilution) / 2 (exclusive), and the SHIFT of
-// the expshift / sigshift bids.  The production operator is {0, 1, 1}; the
-// other variants are built for head_dim 64.
+// the expshift / sigshift bids.  The production operator is {0, 1, 1}; every
+// variant is built for the head dims of the production operator.
 struct Variant {
   int bid = 0;
   int share = 1;
   float shift = 1.f;
 };
-constexpr int kVariantHeadDim = 64;
 int check_variant(const Variant& v, int head_dim);
 
 inline size_t align_up(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
@@ -153,8 +152,8 @@ struct BackwardArgs {
 int64_t backward_workspace_bytes(int64_t n, int64_t T, int head_dim, int dtype, int prec);
 int backward(const BackwardArgs& a);
 
-// The ablation variants of one bid function (any share mode), head_dim 64;
-// each is built in its own object from dil_variants.hip.
+// The ablation variants of one bid function (any share mode and head_dim);
+// each bid is built in its own object from dil_variants.hip.
 template <int BID> int forward_bid(const ForwardArgs& a);
 template <int BID> int backward_bid(const BackwardArgs& a);
 template <int BID> int decode_bid(const DecodeArgs& a);

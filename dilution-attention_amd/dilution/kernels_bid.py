@@ -5,7 +5,7 @@ Drop-in for the reference module ``dilution.kernels_bid``
 and share ablations (configs/bid_8192/*).  Same public names and signatures;
 every launch goes to the HIP kernels of ``libdilution_hip.so``, compiled per
 (bid, share) as template variants of the production kernels
-(``dil_variants.hip``, head_dim 64, the width the ablation configs use).
+(``dil_variants.hip``, head_dim 16, 32, 64 or 128, as the production operator).
 
 Bids, with a = q.k / sqrt(d) on the causal window (kernels_bid.py:4-42):
 
@@ -33,8 +33,8 @@ HAS_HIP = _k.HAS_HIP
 
 BID_TYPES = ("softmax", "relu", "relu2", "softplus", "minshift", "sigmoid", "expshift", "sigshift")
 
-VARIANT_HEAD_DIM = 64
-"""head_dim of the built ablation variants (the production operator takes 16-128)."""
+VARIANT_HEAD_DIMS = (16, 32, 64, 128)
+"""head dims the ablation variants are built for (those of the production operator)."""
 
 
 def _bid_code(bid: str) -> int:
@@ -55,9 +55,8 @@ def _variant(bid: str, share_cumsum, shift: float, head_dim: int) -> tuple:
     code = (_bid_code(bid), _share_code(share_cumsum), float(shift))
     if not shift > 0:
         raise ValueError("shift must be positive")
-    if code[:2] != _k._PRODUCTION[:2] and head_dim != VARIANT_HEAD_DIM:
-        raise ValueError(f"the ablation variants are built for head_dim {VARIANT_HEAD_DIM}, "
-                         f"got {head_dim}")
+    if head_dim not in VARIANT_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {VARIANT_HEAD_DIMS}, got {head_dim}")
     return code
 
 

@@ -76,8 +76,8 @@ class LMConfig:
             raise ValueError('share_cumsum must be a boolean or "exclusive"')
         if self.bid not in kernels_bid.BID_TYPES:
             raise ValueError(f"bid must be one of {kernels_bid.BID_TYPES}; got {self.bid!r}")
-        if not self.production_operator() and self.d_model // self.n_heads != kernels_bid.VARIANT_HEAD_DIM:
-            raise ValueError(f"the bid / share ablations need head_dim {kernels_bid.VARIANT_HEAD_DIM}")
+        if not self.production_operator() and self.d_model // self.n_heads not in kernels_bid.VARIANT_HEAD_DIMS:
+            raise ValueError(f"the bid / share ablations need head_dim in {kernels_bid.VARIANT_HEAD_DIMS}")
 
     def production_operator(self) -> bool:
         """softmax bids with the dilution share: the operator of ``kernels``."""

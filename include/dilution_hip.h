@@ -186,8 +186,8 @@ int dil_decode_step_noalloc(const void* q1, const void* k_cache, const void* v_c
  *   share:  1 dilution p/(committed+p+eps), 2 exclusive p/(committed+eps),
  *           0 none (kernels_bid.py:123-127);
  *   shift:  SHIFT of expshift / sigshift (> 0).
- * (bid, share) = (0, 1) is the production operator (any head_dim); the other
- * variants are built for head_dim 64.  rmax / rden follow kernels_bid: the
+ * (bid, share) = (0, 1) is the production operator; every variant takes the
+ * head dims of the base entry points.  rmax / rden follow kernels_bid: the
  * row minimum (minshift) or 0 and the row sum of the bid numerators for the
  * ratio bids (1-4); 0 and 1 (SHIFT for expshift) for the elementwise bids;
  * pk holds scale * jac @ k, jac = dp/da (p for the softmax bids).  The

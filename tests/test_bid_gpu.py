@@ -189,12 +189,60 @@ def test_variant_decode_matches_full_rows(bid, share):
     assert max_abs(committed, totals) < 1e-5 * max(1.0, totals.abs().max().item())
 
 
+_OTHER_DIM_CASES = [("relu", True), ("relu2", False), ("minshift", True), ("softplus", "exclusive"),
+                    ("sigmoid", True), ("expshift", False), ("sigshift", "exclusive"), ("softmax", "exclusive")]
+
+
+@pytest.mark.parametrize("head_dim", [16, 32, 128])
+@pytest.mark.parametrize("bid,share", _OTHER_DIM_CASES, ids=lambda x: str(x))
+def test_variant_other_head_dims(bid, share, head_dim):
+    """Every variant is built for the production head dims: at 16, 32 and 128
+    (ragged T = 97), the fp32 forward against the fp64 oracle (1e-4, relu2
+    1e-3) with its demand totals (1e-5 relative), the gradients against fp64
+    autograd (2e-3 of the largest, relu2 5e-3; only dv under the exclusive
+    share, whose dq / dk cancel 1e9-scale terms), the bf16 forward (2e-2) and
+    a decode step of the last row (1e-4)."""
+    from dilution import kernels_bid as kb
+
+    t = 97
+    q, k, v, do = orc.make_inputs((1, 3, t, head_dim), seed=500 + head_dim, with_dout=True)
+    kw = dict(bid=bid, share_cumsum=share, shift=SHIFT)
+    want = orc.variant_attention_f64(q, k, v, bid, share, SHIFT)
+    got, aux = kb.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), return_aux=True, **kw)
+    bound = 1e-3 if bid == "relu2" else 1e-4
+    assert max_abs(got, want) < bound
+    totals = orc.variant_demand_totals(q, k, bid, SHIFT)
+    assert max_abs(aux["committed_total"], totals) < 1e-5 * max(1.0, totals.abs().max().item())
+
+    ref = [x.double().requires_grad_(True) for x in (q, k, v)]
+    orc.variant_attention_f64(*ref, bid, share, SHIFT).backward(do.double())
+    xs = [x.cuda().requires_grad_(True) for x in (q, k, v)]
+    kb.dilution_attention(*xs, dot_precision="ieee", **kw).backward(do.cuda())
+    gbound = 5e-3 if bid == "relu2" else 2e-3
+    for name, r, x in zip(("dq", "dk", "dv"), ref, xs):
+        if share == "exclusive" and name != "dv":
+            continue
+        rel = max_abs(x.grad, r.grad) / (r.grad.abs().max().item() + 1e-6)
+        assert rel < gbound, f"{bid} {share} d{head_dim} {name} relative error {rel}"
+
+    qb, kb16, vb = (x.to(torch.bfloat16) for x in (q, k, v))
+    gotb = kb.dilution_attention_forward(qb.cuda(), kb16.cuda(), vb.cuda(), dot_precision="bf16", **kw)
+    assert max_abs(gotb, orc.variant_attention_f64(qb, kb16, vb, bid, share, SHIFT)) < 2e-2
+
+    committed = torch.zeros(1, 3, t, device="cuda")
+    _, auxp = kb.dilution_attention_forward(q[:, :, :t - 1].cuda(), k[:, :, :t - 1].cuda(),
+                                            v[:, :, :t - 1].cuda(), return_aux=True, **kw)
+    committed[:, :, :t - 1] = auxp["committed_total"]
+    y = kb.dilution_decode_step(q[:, :, t - 1:].contiguous().cuda(), k.cuda(), v.cuda(), committed, t, **kw)
+    assert max_abs(y[:, :, 0], want[:, :, t - 1]) < 1e-4
+
+
 def test_variant_argument_errors():
     from dilution import kernels_bid as kb
 
-    q = torch.zeros(1, 1, 8, 32, device="cuda")
+    q = torch.zeros(1, 1, 8, 48, device="cuda")
     with pytest.raises(ValueError):
-        kb.dilution_attention_forward(q, q, q, bid="relu")          # variants are built for d = 64
+        kb.dilution_attention_forward(q, q, q, bid="relu")          # head_dim 48: not built
     q64 = torch.zeros(1, 1, 8, 64, device="cuda")
     with pytest.raises(ValueError):
         kb.dilution_attention_forward(q64, q64, q64, bid="tanh")

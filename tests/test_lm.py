@@ -53,7 +53,8 @@ def test_config_validation():
     with pytest.raises(ValueError):
         LMConfig(share_cumsum="inclusive")
     with pytest.raises(ValueError):
-        LMConfig(d_model=256, n_heads=8, bid="relu")             # head_dim 32: no variant build
+        LMConfig(d_model=384, n_heads=8, bid="relu")             # head_dim 48: no variant build
+    assert not LMConfig(d_model=256, n_heads=8, bid="relu").production_operator()   # head_dim 32
     assert LMConfig(d_model=256, n_heads=8).production_operator()
     assert not LMConfig(d_model=256, n_heads=4, share_cumsum=False).production_operator()
 
