@@ -490,8 +490,15 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   const int cw = threadIdx.x >> 6, cj = threadIdx.x & 63;
   const int64_t c_rb = min(static_cast<int64_t>(g) * 4 + cw, P.nb - 1);
   const float* c_row = P.carry + (slice * P.nb + c_rb) * P.Tk;
-  float cr = 0.f;
-  bool cr_ok = false;
+  // bf16 up to head_dim 64: the tile fetch runs two stages ahead into two
+  // register sets (picked by the stage's parity, a constant in the unrolled
+  // loop), because one stage of compute did not always cover the K/V load
+  // latency (fwd_out -1.5% at B1 H16 T16384).  The other forms keep one set
+  // (no registers to spare: fp32 and split operands would spill).
+  constexpr bool kPf2 = std::is_same_v<CT, __bf16> && D <= 64;
+  constexpr int kSets = kPf2 ? 2 : 1;
+  float cr[kSets] = {};
+  bool cr_ok[kSets] = {};
 
   // N consecutive key tiles kt0 .. kt0 + N - 1 of stage buffer `buf`, their
   // phases interleaved so that one tile's MFMAs overlap the other's VALU work
@@ -576,33 +583,38 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
     }
   };
 
-  KTileLoader<CT, D, false, kLoadClamp> kl[2];  // clamped global loads: measured faster here
-  TTileLoader<CT, D, kLoadClamp> vl[2];
-  auto fetch = [&](int st) {
+  KTileLoader<CT, D, false, kLoadClamp> kl[kSets][2];  // clamped global loads: measured faster here
+  TTileLoader<CT, D, kLoadClamp> vl[kSets][2];
+  auto fetch = [&](int st, int set) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const int64_t key0 = static_cast<int64_t>(2 * st + n) * kTileK;
-      kl[n].load(ks, key0, P.Tk);
-      vl[n].load(vts, key0);
+      kl[set][n].load(ks, key0, P.Tk);
+      vl[set][n].load(vts, key0);
     }
     const int64_t key = static_cast<int64_t>(st) * 2 * kTileK + cj;
-    cr_ok = key < P.Tk;
-    cr = c_row[min(key, P.Tk - 1)];
+    cr_ok[set] = key < P.Tk;
+    cr[set] = c_row[min(key, P.Tk - 1)];
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](int buf, int set) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
-      kl[n].store(ktile[buf][n]);
-      vl[n].store(vttile[buf][n]);
+      kl[set][n].store(ktile[buf][n]);
+      vl[set][n].store(vttile[buf][n]);
     }
-    cs_s[buf][cw][cj] = cr_ok ? cr : 0.f;
+    cs_s[buf][cw][cj] = cr_ok[set] ? cr[set] : 0.f;
   };
-  fetch(0);
-  stash(0);
+  fetch(0, 0);
+  if constexpr (kPf2) fetch(min(1, nst - 1), 1);
+  stash(0, 0);
   __syncthreads();
+  // stage st + 1 sits in register set (st + 1) & 1 = buf ^ 1 (two-stage
+  // prefetch) when its stash comes; the set just stashed takes stage st + 2
   auto iter = [&](int st, int buf) __attribute__((always_inline)) {
     const int kt0 = 2 * st;
-    fetch(min(st + 1, nst - 1));                       // the last stage reloads itself, unused
+    // the last stages reload the final one, unused
+    if constexpr (kPf2) fetch(min(st + 2, nst - 1), buf);
+    else fetch(min(st + 1, nst - 1), 0);
     if (kt0 + 1 < W.kfull) {
       out_tiles(std::integral_constant<int, 2>{}, std::false_type{}, kt0, 0, buf);
     } else {
@@ -614,10 +626,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
           out_tiles(std::integral_constant<int, 1>{}, std::true_type{}, kt0 + n, n, buf);
       }
     }
-    if (st + 1 < nst) stash(buf ^ 1);
+    if (st + 1 < nst) stash(buf ^ 1, kPf2 ? buf ^ 1 : 0);
     sync_lds();
   };
-  double_buffered<(D <= 64)>(0, nst, iter);      // head_dim 128 has no registers to spare
+  // unrolled by two up to head_dim 64, which also makes buf (and the register
+  // set) a constant in each copy; head_dim 128 has no registers to spare
+  double_buffered<(D <= 64)>(0, nst, iter);
 
   // row sums: the two halves of row l32
   const HalfPair rp = halves(rsum);
@@ -710,8 +724,6 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
       for (int s = 0; s < 2; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
     }
   }
-  const bf16x8 ones8 = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
-                        __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
   double run = 0.0;                              // demand entering the current tile (this lane's key)
   float* ccol = P.carry + slice * P.nb * T + min(key, T - 1);
 
@@ -787,12 +799,16 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
     for (int i = 0; i < 16; ++i) xv[i] = xt[i];
     const bf16x8 xf[2] = {acc_frag<CT>(xv, 0), acc_frag<CT>(xv, 1)};
     stage_sh(buf, xf);
-    // row sums of the staged (bf16) shares: all-ones A against the transposed
-    // tile, every register of the result holds its lane's row sum
-    floatx16 gs = floatx16{};
+    // row sums of the staged (bf16) shares: each lane half adds its 16 keys of
+    // the transposed tile (the bf16-rounded values) on the VALU, then the
+    // halves (with the loop unrolled: fwd_keyout -1.5% against all-ones MFMAs)
+    float rv[16];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) gs = Mma<CT>::mma(ones8, xf[s], gs);
-    if (h == 0) rs_s[buf][wave][l32] = gs[0];
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) rv[8 * s + t] = static_cast<float>(xf[s][t]);
+    const HalfPair rp = halves(sum16(rv));
+    if (h == 0) rs_s[buf][wave][l32] = rp.lo + rp.hi;
   };
   auto stage_zero = [&](int buf) {
     const bf16x8 z[2] = {bf16x8{}, bf16x8{}};
@@ -854,7 +870,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
     if (threadIdx.x < 256) product(j > 0 ? qt - 1 : -1, buf ^ 1);
     sync_lds();
   };
-  double_buffered<false>(0, nq - kb0, iter);
+  double_buffered<true>(0, nq - kb0, iter);      // unrolled by two: buffer offsets fold into the LDS instructions
   product(nq - 1, (nq - kb0 - 1) & 1);          // the last tile, staged before the final barrier
   if (h == 0 && key_ok) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
 }
