@@ -43,6 +43,10 @@ The same line carries
   * ``tf32``: the same for the "tf32" mode (the reference model's precision
     for fp32 activations), whose fp32 values run as split bf16 operands (three
     bf16 products per product), priced against a third of the bf16 peak;
+  * ``power``: socket power and graphics clocks sampled with ``amd-smi``
+    while the headline step runs back to back for a few seconds, against the
+    package power cap (the step runs at the cap: its clock, not its
+    instruction issue, sets the step time);
   * ``cpu_baseline``: the fp32 CPU oracle (torch eager, the reference
     formula) timed on this host's cores on one (batch, head) slice of the
     headline workload; ``decode.cpu_baseline``: the oracle's decode step in
@@ -143,6 +147,8 @@ def parse_args():
     ap.add_argument("--lm-train-steps", type=int, default=2)
     ap.add_argument("--lm-decode-tokens", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-power", action="store_true")
+    ap.add_argument("--power-seconds", type=float, default=3.0)
     ap.add_argument("--no-train2k", action="store_true",
                     help="skip the BASELINE configs[1] leg (B8 H16 T2048 fwd+bwd and its SDPA comparator)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -260,7 +266,81 @@ def bench_training(args, dev):
             "note": "per-kernel durations from HIP events in a second pass of the same steps; "
                     "traffic from profiles/hbm_traffic.json"}
     return dict(ms=ms, ms_median=med, value=flops / (ms * 1e-3) / 1e12, roofline=roof, kernels=kernels_out,
-                shape=(batch, heads, seq, d), inputs=(q, k, v, do))
+                shape=(batch, heads, seq, d), inputs=(q, k, v, do), step=step)
+
+
+def _smi_sample():
+    """(socket power W, mean graphics clock MHz) of the first GPU amd-smi lists."""
+    import subprocess
+
+    out = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True, text=True,
+                         timeout=10).stdout
+    data = json.loads(out)
+    gpu = (data.get("gpu_data") or data)[0]
+    watts = float(gpu["power"]["socket_power"]["value"])
+    clocks = [float(c["clk"]["value"]) for name, c in gpu["clock"].items()
+              if name.startswith("gfx") and isinstance(c, dict) and isinstance(c.get("clk"), dict)]
+    return watts, (sum(clocks) / len(clocks) if clocks else None)
+
+
+def _power_cap_w():
+    import re
+    import subprocess
+
+    out = subprocess.run(["rocm-smi", "--showmaxpower"], capture_output=True, text=True, timeout=20).stdout
+    m = re.search(r"Max Graphics Package Power \(W\):\s*([0-9.]+)", out)
+    return float(m.group(1)) if m else None
+
+
+def bench_power(step, seconds: float) -> dict:
+    """Socket power and graphics clocks while `step` runs back to back.
+
+    A host thread samples ``amd-smi metric -p -c`` every ~0.25 s; the first
+    two samples (the clock ramp) are dropped.  Reported beside the package
+    cap from ``rocm-smi --showmaxpower``."""
+    import statistics
+    import threading
+
+    import torch
+
+    samples, errors = [], []
+    done = threading.Event()
+
+    def sampler():
+        while not done.is_set():
+            try:
+                samples.append(_smi_sample())
+            except Exception as exc:  # tool missing or output changed: report, never fail the bench
+                errors.append(f"{type(exc).__name__}: {exc}"[:160])
+                return
+            done.wait(0.25)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    torch.cuda.synchronize()
+    th.start()
+    t0 = time.perf_counter()
+    steps = 0
+    while time.perf_counter() - t0 < seconds or steps < 10:
+        for _ in range(10):
+            step()
+        steps += 10
+        torch.cuda.synchronize()
+    done.set()
+    th.join(timeout=15)
+    if errors and not samples:
+        return {"error": errors[0]}
+    kept = samples[2:] if len(samples) > 4 else samples
+    watts = [w for w, _ in kept]
+    clocks = [c for _, c in kept if c is not None]
+    try:
+        cap = _power_cap_w()
+    except Exception:
+        cap = None
+    return {"socket_w_mean": round(statistics.mean(watts), 1), "socket_w_min": round(min(watts), 1),
+            "socket_w_max": round(max(watts), 1),
+            "gfx_clock_mhz_mean": round(statistics.mean(clocks), 1) if clocks else None,
+            "gfx_clock_mhz_max_spec": 2400, "cap_w": cap, "samples": len(kept), "steps": steps,
+            "how": "amd-smi metric -p -c while the headline step runs back to back"}
 
 
 def bench_sdpa(args, inputs):
@@ -769,6 +849,9 @@ def main() -> int:
     if not args.no_lm:
         torch.cuda.empty_cache()
         line["lm"] = bench_lm(args, dev)
+    if not args.no_power:
+        line["power"] = bench_power(tr["step"], args.power_seconds)
+    del tr["step"]
     if not args.no_cpu_baseline:
         torch.cuda.empty_cache()
         line["cpu_baseline"] = cpu_baseline(tr["shape"])
