@@ -21,7 +21,7 @@ PKG = os.path.join(os.path.dirname(HERE), "dilution")
 OUT = os.path.join(PKG, "libdilution_hip.so")
 BUILD = os.path.join(HERE, "_build")
 SOURCES = ["dil_api.hip", "dil_decode.hip", "dil_forward.hip", "dil_backward.hip", "dil_timing.hip",
-           "dil_noalloc.hip"]
+           "dil_noalloc.hip", "dil_linear.hip"]
 # (object stem, source, extra flags): the ablation variants of each bid
 # function are one object each, built from the same source
 VARIANT_OBJECTS = [(f"dil_variants_b{b}", "dil_variants.hip", [f"-DDIL_VARIANT_BID={b}"]) for b in range(8)]

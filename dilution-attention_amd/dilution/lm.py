@@ -24,7 +24,12 @@ weights).  It follows the reference's module layout and cache protocol
   ``filter_logits``, model.py:289-304);
 * ``continuation_nll``: per-token NLL of continuations given their prompts
   from one causal forward (sampling.py:297-323), the scoring caller of the
-  operator.
+  operator;
+* ``rows_linear``: the decode step's projections at M = batch (<= 8 rows) on
+  the HIP library (``dil_rows_linear``), with the RMSNorms, the residual adds
+  and the SwiGLU activation folded in: a bf16 model's cached decode step (eager
+  and graph-replayed) runs four of them per layer instead of torch's GEMMs and
+  elementwise ops, which read the weights at a fraction of HBM speed at M = 8.
 
 The reference normalises with LayerNorm and sizes SwiGLU at 8/3 d_model; the
 model-level benchmark configuration asks for RMSNorm and a 4x SwiGLU, which
@@ -41,9 +46,38 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
+from . import _hip
 from . import cache as dcache
 from . import kernels
 from . import kernels_bid
+
+# dil_rows_linear modes
+_LIN_PLAIN, _LIN_RESID, _LIN_NORM, _LIN_SWIGLU = 0, 1, 2, 3
+_LIN_MAX_ROWS, _LIN_MAX_K = 8, 4096
+
+
+def rows_linear(x: torch.Tensor, w1: torch.Tensor, mode: int, *, w2: torch.Tensor | None = None,
+                g: torch.Tensor | None = None, resid: torch.Tensor | None = None,
+                eps: float = 0.0) -> torch.Tensor:
+    """A few-row projection on the HIP library (``dil_rows_linear``): for
+    bf16 x (rows, K) with rows <= 8 and nn.Linear weights (N, K), mode 0
+    returns x W1^T, 1 resid + x W1^T, 2 rmsnorm(x; g, eps) W1^T, 3
+    silu(r W1^T) * (r W2^T) with r = rmsnorm(x; g, eps), rounded to bf16 where
+    the separate torch ops round.  (No reference counterpart: the reference
+    model runs these through torch.nn.Linear, model.py:41-93.)"""
+    lib = _hip.lib()
+    rows, k = x.shape
+    n = w1.shape[0]
+    for t in (x, w1, w2, g, resid):
+        if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != x.device):
+            raise ValueError("rows_linear takes contiguous bf16 tensors on one device")
+    out = torch.empty(rows, n, device=x.device, dtype=x.dtype)
+    status = lib.dil_rows_linear(x.data_ptr(), w1.data_ptr(), None if w2 is None else w2.data_ptr(),
+                                 None if g is None else g.data_ptr(), None if resid is None else resid.data_ptr(),
+                                 out.data_ptr(), rows, n, k, mode, 1, float(eps),
+                                 torch.cuda.current_stream(x.device).cuda_stream)
+    _hip.check(status, "dil_rows_linear")
+    return out
 
 
 @dataclass
@@ -273,7 +307,15 @@ class DilutionLM(nn.Module):
         return self.lm_head(self.ln_f(x[:, [-1], :])), caches
 
     @torch.no_grad()
-    def decode_step(self, token: torch.Tensor, caches) -> torch.Tensor:
+    def decode_step(self, token: torch.Tensor, caches, fused: bool = True) -> torch.Tensor:
+        """Logits (B, 1, vocab) of the next position from the caches; a bf16
+        model runs its projections on ``rows_linear`` (``fused=False`` keeps
+        torch's modules, the same computation up to accumulation order)."""
+        batch = token.shape[0]
+        if fused and self.fused_decode_eligible(batch):
+            x2 = self.wte(token).view(batch, -1)
+            x2 = self._fused_layers(x2, lambda i, q1, k1, v1: dcache.step_cache(q1, k1, v1, caches[i]))
+            return self._fused_head(x2)
         x = self.wte(token)
         for block, cache in zip(self.h, caches):
             x = block.step_cache(x, cache)
@@ -283,6 +325,47 @@ class DilutionLM(nn.Module):
         """Every layer runs the production dilution operator (the decode step
         GraphDecoder captures)."""
         return all(isinstance(b.attn, DilutionAttention) and b.attn.production for b in self.h)
+
+    def fused_decode_eligible(self, batch: int) -> bool:
+        """The cached decode step can run on ``rows_linear``: every layer on
+        the production dilution operator, bf16 weights on the GPU, RMSNorm
+        with weights, d_model and the MLP width multiples of 256 up to 4096,
+        and at most 8 sequences."""
+        cfg = self.cfg
+        hidden = int(cfg.mlp_ratio * cfg.d_model)
+        w = self.lm_head.weight
+        return (self.graph_decode_eligible() and kernels.HAS_HIP and w.is_cuda and w.dtype == torch.bfloat16
+                and cfg.norm == "rms" and self.ln_f.weight is not None
+                and all(b.ln_1.weight is not None and b.ln_2.weight is not None for b in self.h)
+                and cfg.d_model % 256 == 0 and cfg.d_model <= _LIN_MAX_K
+                and hidden % 256 == 0 and hidden <= _LIN_MAX_K and 1 <= batch <= _LIN_MAX_ROWS)
+
+    @staticmethod
+    def _norm_eps(norm: nn.Module) -> float:
+        return norm.eps if norm.eps is not None else torch.finfo(torch.bfloat16).eps
+
+    def _fused_layers(self, x2: torch.Tensor, attend) -> torch.Tensor:
+        """The blocks of one decode step on ``rows_linear`` (B, d_model) ->
+        (B, d_model): per layer norm + q/k/v projection, ``attend(i, q1, k1,
+        v1)`` (the layer's cache append and decode step, (B, H, [1,] D)),
+        output projection + residual, norm + gate/up projections + SwiGLU,
+        down projection + residual."""
+        batch, d = x2.shape
+        for i, block in enumerate(self.h):
+            at, mlp = block.attn, block.mlp
+            qkv = rows_linear(x2, at.c_attn.weight, _LIN_NORM, g=block.ln_1.weight, eps=self._norm_eps(block.ln_1))
+            shape = (batch, 1, at.n_heads, d // at.n_heads)
+            q1, k1, v1 = (t.view(shape).transpose(1, 2) for t in qkv.view(batch, 1, 3 * d).split(d, dim=2))
+            y = attend(i, q1, k1, v1).reshape(batch, d)
+            x2 = rows_linear(y, at.c_proj.weight, _LIN_RESID, resid=x2)
+            h = rows_linear(x2, mlp.gate_proj.weight, _LIN_SWIGLU, w2=mlp.up_proj.weight, g=block.ln_2.weight,
+                            eps=self._norm_eps(block.ln_2))
+            x2 = rows_linear(h, mlp.down_proj.weight, _LIN_RESID, resid=x2)
+        return x2
+
+    def _fused_head(self, x2: torch.Tensor) -> torch.Tensor:
+        logits = rows_linear(x2, self.lm_head.weight, _LIN_NORM, g=self.ln_f.weight, eps=self._norm_eps(self.ln_f))
+        return logits.view(x2.shape[0], 1, -1)
 
     @torch.no_grad()
     def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 0.0,
@@ -349,7 +432,7 @@ class GraphDecoder:
     """
 
     def __init__(self, model: "DilutionLM", caches: list, token: torch.Tensor,
-                 vocab_limit: int | None = None):
+                 vocab_limit: int | None = None, fused: bool = True):
         if not model.graph_decode_eligible():
             raise ValueError("GraphDecoder needs every layer on the production dilution operator")
         self.model, self.caches = model, caches
@@ -371,20 +454,31 @@ class GraphDecoder:
         if vocab_limit is not None:
             self.mask = torch.zeros(model.cfg.vocab_size, device=dev)
             self.mask[vocab_limit:] = float("-inf")
+        self.fused = fused and model.fused_decode_eligible(self.batch)
         self.graph = None
+
+    def _attend(self, i: int, q1, k1, v1) -> torch.Tensor:
+        """Layer i's cache append at the device-resident position and its
+        decode step at the device-resident length."""
+        cache = self.caches[i]
+        cache["k"].index_copy_(2, self.pos, k1)
+        cache["v"].index_copy_(2, self.pos, v1)
+        return kernels.decode_step_device_length(q1, cache["k"], cache["v"], cache["committed"], self.live,
+                                                 self.capacity, out=self.outs[i], workspace=self.ws)
 
     def _body(self) -> None:
         m = self.model
-        x = m.wte(self.tok)
-        for block, cache, out in zip(m.h, self.caches, self.outs):
-            q1, k1, v1 = block.attn._split_heads(block.ln_1(x))
-            cache["k"].index_copy_(2, self.pos, k1)
-            cache["v"].index_copy_(2, self.pos, v1)
-            y = kernels.decode_step_device_length(q1, cache["k"], cache["v"], cache["committed"],
-                                                  self.live, self.capacity, out=out, workspace=self.ws)
-            x = x + block.attn._merge_heads(y.to(x.dtype), self.batch, 1)
-            x = x + block.mlp(block.ln_2(x))
-        logits = m.lm_head(m.ln_f(x))
+        if self.fused:
+            x2 = m._fused_layers(m.wte(self.tok).view(self.batch, -1), self._attend)
+            logits = m._fused_head(x2)
+        else:
+            x = m.wte(self.tok)
+            for i, block in enumerate(m.h):
+                q1, k1, v1 = block.attn._split_heads(block.ln_1(x))
+                y = self._attend(i, q1, k1, v1)
+                x = x + block.attn._merge_heads(y.to(x.dtype), self.batch, 1)
+                x = x + block.mlp(block.ln_2(x))
+            logits = m.lm_head(m.ln_f(x))
         self.logits.copy_(logits)
         last = logits[:, -1, :].float()
         if self.mask is not None:

@@ -211,6 +211,28 @@ int dil_decode_step_variant(const void* q1, const void* k_cache, const void* v_c
                             void* stream);
 
 /*
+ * Few-row projections of the LM's decode step.  No counterpart in the
+ * reference, whose model runs these projections through torch.nn.Linear
+ * (model.py:41-93) with the norms and the MLP activation as separate ops: at
+ * M = the decode batch (at most 8 rows) each product streams its weight once,
+ * and a library GEMM tiled for large M reads it at a fraction of HBM speed.
+ *
+ *   mode 0:  out = x W1^T
+ *   mode 1:  out = resid + x W1^T
+ *   mode 2:  out = rmsnorm(x) W1^T,               rmsnorm(x) = x / sqrt(mean(x^2) + eps) * g
+ *   mode 3:  out = silu(r W1^T) * (r W2^T),        r = rmsnorm(x)
+ *
+ * x (rows, k), W1 / W2 (n, k) (nn.Linear weights), g (k), resid and out
+ * (rows, n): row-major, contiguous, dtype bf16 only (dtype code 1; others
+ * return -2).  1 <= rows <= 8, k a multiple of 256 up to 4096, eps >= 0.
+ * Intermediates are rounded to bf16 where the unfused torch ops round them.
+ * Asynchronous on `stream`; no workspace; out must not alias x or resid.
+ */
+int dil_rows_linear(const void* x, const void* w1, const void* w2, const void* g, const void* resid,
+                    void* out, int64_t rows, int64_t n, int64_t k, int mode, int dtype, float eps,
+                    void* stream);
+
+/*
  * Kernel timing for measurement harnesses.  No reference counterpart (the
  * reference times its Triton launches with torch.profiler and CUDA events in
  * scripts/step_profile.py:29-47 and scripts/profile_kernels.py:115-144).

@@ -102,6 +102,29 @@ def test_argument_errors_before_any_launch(lib):
                                  None, None, None, 0, None) == -4
 
 
+def test_rows_linear_argument_errors_before_any_launch(lib):
+    """dil_rows_linear: bf16 only, 1-8 rows, K a multiple of 256 up to 4096,
+    and the buffers its mode reads; the stand-in addresses are never
+    dereferenced (every call returns before launching)."""
+    f = [ctypes.c_void_p(4096 * (i + 1)) for i in range(6)]
+    x, w1, w2, g, res, out = f
+    ok = (8, 64, 1024)
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, *ok, 0, 0, 0.0, None) == -2      # fp32
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, 9, 64, 1024, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, 0, 64, 1024, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, 8, 64, 1000, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, 8, 64, 8192, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, 8, 0, 1024, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, *ok, 4, 1, 0.0, None) == -4     # mode
+    assert lib.dil_rows_linear(None, w1, None, None, None, out, *ok, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, None, None, None, None, out, *ok, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, None, *ok, 0, 1, 0.0, None) == -4
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, *ok, 1, 1, 0.0, None) == -4     # resid
+    assert lib.dil_rows_linear(x, w1, None, None, None, out, *ok, 2, 1, 1e-5, None) == -4    # g
+    assert lib.dil_rows_linear(x, w1, None, g, None, out, *ok, 3, 1, 1e-5, None) == -4       # w2
+    assert lib.dil_rows_linear(x, w1, None, g, None, out, *ok, 2, 1, -1.0, None) == -4       # eps
+
+
 def test_null_pointers_are_argument_errors(lib):
     """A NULL where the header requires a buffer is a status (-4) returned
     before any launch, never a device fault.  The stand-in addresses below are

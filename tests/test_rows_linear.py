@@ -1,0 +1,169 @@
+"""The decode step's few-row projections (dilution.lm.rows_linear, C ABI
+dil_rows_linear) against the unfused torch ops they replace, and the LM's
+decode step on them against the same step on torch's modules.
+
+The kernel accumulates its dot products in fp32 in another order than
+torch's GEMM, and rounds the same intermediates to bf16, so the bar is a
+bf16-rounding bound, not bitwise.  An identity weight isolates the RMSNorm
+stage: each output is then one staged, normalised activation (a dot product
+with a single 1.0), which must equal torch's rms_norm to within one bf16 step
+(the row's sum of squares is added in another order).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from gpu_helpers import needs_gpu
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+
+def _bf(*shape, gen, scale=1.0):
+    return (torch.randn(*shape, generator=gen) * scale).to(torch.bfloat16).cuda()
+
+
+def _check_close(out, ref, what):
+    out, ref = out.float(), ref.float()
+    err = (out - ref).abs()
+    peak = ref.abs().max().item()
+    # a few bf16 roundings of values up to `peak`, plus fp32 order effects
+    assert err.max().item() <= 2.0 ** -6 * peak + 1e-6, (what, err.max().item(), peak)
+    assert err.mean().item() <= 2.0 ** -8 * ref.abs().mean().item() + 1e-6, (what, err.mean().item())
+
+
+@pytest.mark.parametrize("rows", [1, 5, 8])
+@pytest.mark.parametrize("n,k", [(40, 256), (1000, 1024), (3072, 1024), (1024, 4096), (9000, 1024)])
+def test_plain_and_residual_match_torch(rows, n, k):
+    from dilution.lm import rows_linear
+
+    gen = torch.Generator().manual_seed(rows * 7 + n + k)
+    x = _bf(rows, k, gen=gen)
+    w = _bf(n, k, gen=gen, scale=0.02)
+    resid = _bf(rows, n, gen=gen)
+    _check_close(rows_linear(x, w, 0), F.linear(x, w), ("plain", rows, n, k))
+    _check_close(rows_linear(x, w, 1, resid=resid), resid + F.linear(x, w), ("resid", rows, n, k))
+
+
+@pytest.mark.parametrize("rows", [2, 8])
+@pytest.mark.parametrize("n,k", [(3072, 1024), (50304, 1024), (64, 256)])
+def test_norm_projection_matches_torch(rows, n, k):
+    from dilution.lm import rows_linear
+
+    gen = torch.Generator().manual_seed(rows + n)
+    x = _bf(rows, k, gen=gen, scale=3.0)
+    g = (1.0 + 0.1 * torch.randn(k, generator=gen)).to(torch.bfloat16).cuda()
+    w = _bf(n, k, gen=gen, scale=0.02)
+    ref = F.linear(F.rms_norm(x, (k,), g, 1e-5), w)
+    _check_close(rows_linear(x, w, 2, g=g, eps=1e-5), ref, ("norm", rows, n, k))
+
+
+@pytest.mark.parametrize("rows", [3, 8])
+def test_norm_stage_equals_rms_norm(rows):
+    """Identity weight: out = the staged rmsnorm(x) * g, within one bf16 step
+    of torch's rms_norm, and equal to it almost everywhere (both round
+    x / rms(x) * g once; the sum of squares is added in another order)."""
+    from dilution.lm import rows_linear
+
+    k = 1024
+    gen = torch.Generator().manual_seed(rows)
+    x = _bf(rows, k, gen=gen, scale=2.0)
+    g = (1.0 + 0.3 * torch.randn(k, generator=gen)).to(torch.bfloat16).cuda()
+    eye = torch.eye(k, dtype=torch.bfloat16, device="cuda")
+    out = rows_linear(x, eye, 2, g=g, eps=1e-5).float()
+    ref = F.rms_norm(x, (k,), g, 1e-5).float()
+    ulp = ref.abs().clamp_min(1e-30) * 2.0 ** -7
+    assert bool(((out - ref).abs() <= ulp).all())
+    assert (out == ref).float().mean().item() > 0.95
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+@pytest.mark.parametrize("n", [4096, 1000])
+def test_swiglu_matches_torch(rows, n):
+    from dilution.lm import rows_linear
+
+    k = 1024
+    gen = torch.Generator().manual_seed(rows + n + 1)
+    x = _bf(rows, k, gen=gen)
+    g = (1.0 + 0.1 * torch.randn(k, generator=gen)).to(torch.bfloat16).cuda()
+    w1 = _bf(n, k, gen=gen, scale=0.05)
+    w2 = _bf(n, k, gen=gen, scale=0.05)
+    r = F.rms_norm(x, (k,), g, 1e-5)
+    ref = F.silu(F.linear(r, w1)) * F.linear(r, w2)
+    _check_close(rows_linear(x, w1, 3, w2=w2, g=g, eps=1e-5), ref, ("swiglu", rows, n))
+
+
+def test_rows_past_the_batch_are_untouched():
+    """out has exactly `rows` rows: a poisoned buffer around a view is not written."""
+    from dilution import _hip
+    from dilution.lm import rows_linear  # noqa: F401  (loads the library)
+
+    gen = torch.Generator().manual_seed(3)
+    x = _bf(3, 256, gen=gen)
+    w = _bf(48, 256, gen=gen, scale=0.1)
+    buf = torch.full((5, 48), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out = buf[1:4]
+    status = _hip.lib().dil_rows_linear(x.data_ptr(), w.data_ptr(), None, None, None, out.data_ptr(),
+                                        3, 48, 256, 0, 1, 0.0, torch.cuda.current_stream().cuda_stream)
+    assert status == 0
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(buf[0]).all()) and bool(torch.isnan(buf[4]).all())
+    _check_close(out, F.linear(x, w), "view")
+
+
+def _lm():
+    from dilution.lm import DilutionLM, LMConfig
+
+    cfg = LMConfig(vocab_size=1000, n_layers=2, d_model=256, n_heads=4, prefill_chunk=32)
+    torch.manual_seed(0)
+    return DilutionLM(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
+
+
+def _clone_caches(caches):
+    return [{key: (val.clone() if torch.is_tensor(val) else val) for key, val in c.items()} for c in caches]
+
+
+def test_fused_decode_step_matches_torch_modules():
+    """The bf16 decode step on rows_linear against the same step on torch's
+    modules from the same caches, several steps in a row: logits within the
+    bf16 bound of the last layer's inputs, identical caches growth."""
+    model = _lm()
+    assert model.fused_decode_eligible(3) and not model.fused_decode_eligible(9)
+    gen = torch.Generator().manual_seed(11)
+    idx = torch.randint(0, 1000, (3, 45), generator=gen).cuda()
+    logits, caches_f = model.prefill(idx, capacity=45 + 6)
+    caches_t = _clone_caches(caches_f)
+    tok = logits[:, -1, :].float().argmax(dim=-1, keepdim=True)
+    for step in range(6):
+        lf = model.decode_step(tok, caches_f)
+        lt = model.decode_step(tok, caches_t, fused=False)
+        assert lf.shape == lt.shape == (3, 1, 1000)
+        err = (lf.float() - lt.float()).abs().max().item()
+        assert err <= 3e-2 * lt.float().abs().max().item(), (step, err)
+        tok = lt[:, -1, :].float().argmax(dim=-1, keepdim=True)
+    for cf, ct in zip(caches_f, caches_t):
+        assert cf["len"] == ct["len"] == 45 + 6
+
+
+def test_graph_decode_runs_fused_and_matches_eager_fused():
+    """GraphDecoder on a fused-eligible model replays the fused step: every
+    replay bitwise equal to the eager fused step (same kernels, same order)."""
+    from dilution.lm import GraphDecoder
+
+    model = _lm()
+    gen = torch.Generator().manual_seed(12)
+    idx = torch.randint(0, 1000, (2, 40), generator=gen).cuda()
+    logits_e, caches_e = model.prefill(idx, capacity=48)
+    _, caches_g = model.prefill(idx, capacity=48)
+    tok = logits_e[:, -1, :].float().argmax(dim=-1, keepdim=True)
+    dec = GraphDecoder(model, caches_g, tok)
+    assert dec.fused
+    for step in range(8):
+        le = model.decode_step(tok, caches_e)
+        tg = dec.step()
+        torch.cuda.synchronize()
+        assert torch.equal(dec.logits, le), step
+        tok = le[:, -1, :].float().argmax(dim=-1, keepdim=True)
+        assert torch.equal(tg, tok), step
