@@ -80,6 +80,38 @@ def rows_linear(x: torch.Tensor, w1: torch.Tensor, mode: int, *, w2: torch.Tenso
     return out
 
 
+def rows_linear_qkv(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor, eps: float, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor, pos) -> torch.Tensor:
+    """The decode step's RMSNorm + q/k/v projection with the cache append
+    folded in (``dil_rows_linear_qkv``): [q | k | v] = rmsnorm(x; g, eps)
+    w^T for c_attn's weight w (3 d_model, d_model); k and v go to row `pos`
+    of the (B, H, capacity, D) caches, q is returned as (B, d_model).  `pos`
+    is a Python int or a one-element int64 tensor on the device (read when
+    the kernel runs, as in a graph replay).  (No reference counterpart: the
+    reference projects with c_attn and writes its cache as separate ops,
+    model.py:41-93.)"""
+    lib = _hip.lib()
+    rows, k = x.shape
+    batch, heads, capacity, head_dim = k_cache.shape
+    for t in (x, w, g, k_cache, v_cache):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != x.device:
+            raise ValueError("rows_linear_qkv takes contiguous bf16 tensors on one device")
+    if batch != rows or v_cache.shape != k_cache.shape or w.shape != (3 * heads * head_dim, k):
+        raise ValueError("rows_linear_qkv: x, w and the caches disagree in shape")
+    q = torch.empty(rows, heads * head_dim, device=x.device, dtype=x.dtype)
+    if torch.is_tensor(pos):
+        if pos.dtype != torch.int64 or pos.numel() != 1 or pos.device != x.device:
+            raise ValueError("a device position is a one-element int64 tensor on the inputs' device")
+        pos_dev, pos_host = pos.data_ptr(), 0
+    else:
+        pos_dev, pos_host = None, int(pos)
+    status = lib.dil_rows_linear_qkv(x.data_ptr(), w.data_ptr(), g.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
+                                     v_cache.data_ptr(), rows, heads, head_dim, capacity, pos_dev, pos_host, k, 1,
+                                     float(eps), torch.cuda.current_stream(x.device).cuda_stream)
+    _hip.check(status, "dil_rows_linear_qkv")
+    return q
+
+
 @dataclass
 class LMConfig:
     vocab_size: int = 50304
@@ -313,8 +345,19 @@ class DilutionLM(nn.Module):
         torch's modules, the same computation up to accumulation order)."""
         batch = token.shape[0]
         if fused and self.fused_decode_eligible(batch):
-            x2 = self.wte(token).view(batch, -1)
-            x2 = self._fused_layers(x2, lambda i, q1, k1, v1: dcache.step_cache(q1, k1, v1, caches[i]))
+            def slot(i):
+                cache = caches[i]
+                t = cache["len"]
+                if t >= cache["k"].shape[2]:
+                    raise ValueError("decode step past the cache capacity (context_length)")
+                cache["len"] = t + 1
+                return cache["k"], cache["v"], t
+
+            def attend(i, q1):
+                c = caches[i]
+                return kernels.dilution_decode_step(q1, c["k"], c["v"], c["committed"], c["len"])
+
+            x2 = self._fused_layers(self.wte(token).view(batch, -1), slot, attend)
             return self._fused_head(x2)
         x = self.wte(token)
         for block, cache in zip(self.h, caches):
@@ -344,19 +387,20 @@ class DilutionLM(nn.Module):
     def _norm_eps(norm: nn.Module) -> float:
         return norm.eps if norm.eps is not None else torch.finfo(torch.bfloat16).eps
 
-    def _fused_layers(self, x2: torch.Tensor, attend) -> torch.Tensor:
+    def _fused_layers(self, x2: torch.Tensor, slot, attend) -> torch.Tensor:
         """The blocks of one decode step on ``rows_linear`` (B, d_model) ->
-        (B, d_model): per layer norm + q/k/v projection, ``attend(i, q1, k1,
-        v1)`` (the layer's cache append and decode step, (B, H, [1,] D)),
-        output projection + residual, norm + gate/up projections + SwiGLU,
-        down projection + residual."""
+        (B, d_model): per layer norm + q/k/v projection with k and v written
+        to ``slot(i)`` = (k_cache, v_cache, position) (an int or a device
+        tensor), ``attend(i, q1)`` (the layer's decode step over the cache with
+        the new row, (B, H, 1, D)), output projection + residual, norm +
+        gate/up projections + SwiGLU, down projection + residual."""
         batch, d = x2.shape
         for i, block in enumerate(self.h):
             at, mlp = block.attn, block.mlp
-            qkv = rows_linear(x2, at.c_attn.weight, _LIN_NORM, g=block.ln_1.weight, eps=self._norm_eps(block.ln_1))
-            shape = (batch, 1, at.n_heads, d // at.n_heads)
-            q1, k1, v1 = (t.view(shape).transpose(1, 2) for t in qkv.view(batch, 1, 3 * d).split(d, dim=2))
-            y = attend(i, q1, k1, v1).reshape(batch, d)
+            k_cache, v_cache, pos = slot(i)
+            q = rows_linear_qkv(x2, at.c_attn.weight, block.ln_1.weight, self._norm_eps(block.ln_1), k_cache,
+                                v_cache, pos)
+            y = attend(i, q.view(batch, at.n_heads, 1, d // at.n_heads)).reshape(batch, d)
             x2 = rows_linear(y, at.c_proj.weight, _LIN_RESID, resid=x2)
             h = rows_linear(x2, mlp.gate_proj.weight, _LIN_SWIGLU, w2=mlp.up_proj.weight, g=block.ln_2.weight,
                             eps=self._norm_eps(block.ln_2))
@@ -466,10 +510,19 @@ class GraphDecoder:
         return kernels.decode_step_device_length(q1, cache["k"], cache["v"], cache["committed"], self.live,
                                                  self.capacity, out=self.outs[i], workspace=self.ws)
 
+    def _slot(self, i: int):
+        cache = self.caches[i]
+        return cache["k"], cache["v"], self.pos
+
+    def _attend_q(self, i: int, q1) -> torch.Tensor:
+        cache = self.caches[i]
+        return kernels.decode_step_device_length(q1, cache["k"], cache["v"], cache["committed"], self.live,
+                                                 self.capacity, out=self.outs[i], workspace=self.ws)
+
     def _body(self) -> None:
         m = self.model
         if self.fused:
-            x2 = m._fused_layers(m.wte(self.tok).view(self.batch, -1), self._attend)
+            x2 = m._fused_layers(m.wte(self.tok).view(self.batch, -1), self._slot, self._attend_q)
             logits = m._fused_head(x2)
         else:
             x = m.wte(self.tok)

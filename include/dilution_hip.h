@@ -233,6 +233,28 @@ int dil_rows_linear(const void* x, const void* w1, const void* w2, const void* g
                     void* stream);
 
 /*
+ * The decode step's norm + q/k/v projection with the cache append folded in.
+ * No counterpart in the reference, whose attention block projects with
+ * c_attn (model.py:41-93) and then writes k and v into its cache
+ * (model.py:86-93) as separate ops.  w is c_attn's weight (3 heads head_dim,
+ * k) with the q, k and v rows in that order; g the RMSNorm weight:
+ *
+ *   [q | k | v] = rmsnorm(x) w^T              (rows, 3 heads head_dim)
+ *   q_out[m, :]                  = q[m, :]     (rows, heads * head_dim)
+ *   k_cache[m, h, pos, :]        = k[m, h * head_dim : (h + 1) * head_dim]
+ *   v_cache[m, h, pos, :]        = v[m, ...]   likewise
+ *
+ * The caches are (rows, heads, capacity, head_dim) contiguous.  pos is read
+ * from device memory when pos_dev is not null (graph replay), else taken
+ * from `pos` (0 <= pos < capacity, checked); a device position outside
+ * [0, capacity) stores no cache row.  Same dtype, rows and k rules as
+ * dil_rows_linear.
+ */
+int dil_rows_linear_qkv(const void* x, const void* w, const void* g, void* q_out, void* k_cache,
+                        void* v_cache, int64_t rows, int64_t heads, int64_t head_dim, int64_t capacity,
+                        const int64_t* pos_dev, int64_t pos, int64_t k, int dtype, float eps, void* stream);
+
+/*
  * Kernel timing for measurement harnesses.  No reference counterpart (the
  * reference times its Triton launches with torch.profiler and CUDA events in
  * scripts/step_profile.py:29-47 and scripts/profile_kernels.py:115-144).

@@ -125,6 +125,25 @@ def test_rows_linear_argument_errors_before_any_launch(lib):
     assert lib.dil_rows_linear(x, w1, None, g, None, out, *ok, 2, 1, -1.0, None) == -4       # eps
 
 
+def test_rows_linear_qkv_argument_errors_before_any_launch(lib):
+    """dil_rows_linear_qkv: the rows / K / dtype rules of dil_rows_linear,
+    every buffer required, and a host position inside the cache; the stand-in
+    addresses are never dereferenced."""
+    x, w, g, q, kc, vc = (ctypes.c_void_p(4096 * (i + 1)) for i in range(6))
+    bufs = [x, w, g, q, kc, vc]
+
+    def call(*, b=bufs, rows=8, heads=16, hd=64, cap=100, pdev=None, pos=5, k=1024, dt=1, eps=1e-5):
+        return lib.dil_rows_linear_qkv(*b, rows, heads, hd, cap, pdev, pos, k, dt, eps, None)
+
+    assert call(dt=0) == -2
+    assert call(rows=9) == -4 and call(rows=0) == -4 and call(k=1000) == -4 and call(k=8192) == -4
+    assert call(heads=0) == -4 and call(hd=0) == -4 and call(cap=0) == -4
+    assert call(pos=100) == -4 and call(pos=-1) == -4              # host position outside the cache
+    assert call(eps=-1.0) == -4
+    for hole in range(6):
+        assert call(b=[None if i == hole else p for i, p in enumerate(bufs)]) == -4, hole
+
+
 def test_null_pointers_are_argument_errors(lib):
     """A NULL where the header requires a buffer is a status (-4) returned
     before any launch, never a device fault.  The stand-in addresses below are

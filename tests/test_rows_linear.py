@@ -113,6 +113,58 @@ def test_rows_past_the_batch_are_untouched():
     _check_close(out, F.linear(x, w), "view")
 
 
+@pytest.mark.parametrize("rows", [1, 8])
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_qkv_projection_writes_the_cache_row(rows, device_pos):
+    """rows_linear_qkv: q = the first third of rmsnorm(x) W^T; the k and v
+    thirds land in row `pos` of the (B, H, capacity, D) caches, every other
+    cache row untouched."""
+    from dilution.lm import rows_linear_qkv
+
+    heads, hd, cap, pos = 16, 64, 40, 17
+    d = heads * hd
+    gen = torch.Generator().manual_seed(rows + 40)
+    x = _bf(rows, d, gen=gen, scale=2.0)
+    g = (1.0 + 0.1 * torch.randn(d, generator=gen)).to(torch.bfloat16).cuda()
+    w = _bf(3 * d, d, gen=gen, scale=0.02)
+    kc = _bf(rows, heads, cap, hd, gen=gen)
+    vc = _bf(rows, heads, cap, hd, gen=gen)
+    k0, v0 = kc.clone(), vc.clone()
+    p = torch.tensor([pos], dtype=torch.int64, device="cuda") if device_pos else pos
+    q = rows_linear_qkv(x, w, g, 1e-5, kc, vc, p)
+    ref = F.linear(F.rms_norm(x, (d,), g, 1e-5), w)
+    _check_close(q, ref[:, :d], ("q", rows))
+    _check_close(kc[:, :, pos], ref[:, d:2 * d].view(rows, heads, hd), ("k", rows))
+    _check_close(vc[:, :, pos], ref[:, 2 * d:].view(rows, heads, hd), ("v", rows))
+    keep = torch.ones(cap, dtype=torch.bool)
+    keep[pos] = False
+    assert torch.equal(kc[:, :, keep], k0[:, :, keep]) and torch.equal(vc[:, :, keep], v0[:, :, keep])
+    # the same product as the plain norm projection, bitwise (same kernel body)
+    from dilution.lm import rows_linear
+    full = rows_linear(x, w, 2, g=g, eps=1e-5)
+    assert torch.equal(q, full[:, :d])
+    assert torch.equal(kc[:, :, pos], full[:, d:2 * d].view(rows, heads, hd))
+
+
+def test_qkv_device_position_outside_the_cache_stores_no_row():
+    from dilution.lm import rows_linear_qkv
+
+    heads, hd, cap, rows = 4, 64, 8, 3
+    d = heads * hd
+    gen = torch.Generator().manual_seed(7)
+    x = _bf(rows, d, gen=gen)
+    g = torch.ones(d, dtype=torch.bfloat16, device="cuda")
+    w = _bf(3 * d, d, gen=gen, scale=0.05)
+    kc = _bf(rows, heads, cap, hd, gen=gen)
+    vc = _bf(rows, heads, cap, hd, gen=gen)
+    k0, v0 = kc.clone(), vc.clone()
+    for bad in (cap, -1):
+        q = rows_linear_qkv(x, w, g, 1e-5, kc, vc, torch.tensor([bad], dtype=torch.int64, device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(kc, k0) and torch.equal(vc, v0), bad
+        _check_close(q, F.linear(F.rms_norm(x, (d,), g, 1e-5), w)[:, :d], "q")
+
+
 def _lm():
     from dilution.lm import DilutionLM, LMConfig
 
