@@ -5,9 +5,10 @@
 
 namespace dil {
 
+// Sized for a device-resident length up to `length` (the larger chunk count),
+// so one size serves dil_decode_step and dil_decode_step_dlen.
 int64_t decode_workspace_bytes(int64_t n, int64_t length, int head_dim) {
-  const int64_t chunk = decode_chunk(n, length);
-  const int64_t nchunk = (length + chunk - 1) / chunk;
+  const int64_t nchunk = decode_chunks(n, length, true);
   return static_cast<int64_t>(align_up(sizeof(float) * n * length) +
                               align_up(sizeof(float2) * n * nchunk) +
                               align_up(sizeof(float) * n * nchunk * (head_dim + 1)));

@@ -38,6 +38,41 @@ constexpr int kDecThreads = 1024;
 constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecUnroll = 2;          // cached rows in flight per lane
 
+// Keys per workgroup.  At most 2048 (the sweep above), and as many chunks as
+// fill whole rounds of the workgroups the GPU holds at once (two 1024-thread
+// workgroups per CU, 256 CUs): a partial last round streams at a fraction of
+// HBM speed, and a small batch x context would leave CUs idle.  At least 256
+// keys.  The rule is computed alike on the host and, for a length held in
+// device memory, by the kernels, so both give the same chunks (and the same
+// bits) at the same live length.
+constexpr int64_t kDecResident = 512;
+constexpr int64_t kDecMaxChunk = 2048;
+constexpr int64_t kDecMinChunk = 256;
+
+__host__ __device__ inline int64_t decode_chunk(int64_t n, int64_t length) {
+  if (length < 1 || n < 1) return kDecMinChunk;
+  const int64_t base = (length + kDecMaxChunk - 1) / kDecMaxChunk;     // chunks at the largest size
+  const int64_t rounds = (n * base + kDecResident - 1) / kDecResident;
+  int64_t target = rounds * kDecResident / n;                          // chunks that fill `rounds`
+  if (target < base) target = base;
+  const int64_t chunk = (length + target - 1) / target;
+  return chunk < kDecMinChunk ? kDecMinChunk : chunk;
+}
+
+// Chunks per slice in the grid and the scratch: exact for a host length; for
+// a device-resident live length up to `length`, a bound on every live length's
+// count (at most the 2048-key count plus one round's share per slice, and at
+// most one chunk per 256 keys).
+inline int64_t decode_chunks(int64_t n, int64_t length, bool device_length) {
+  if (!device_length) {
+    const int64_t chunk = decode_chunk(n, length);
+    return (length + chunk - 1) / chunk;
+  }
+  const int64_t per_min = (length + kDecMinChunk - 1) / kDecMinChunk;
+  const int64_t bound = (length + kDecMaxChunk - 1) / kDecMaxChunk + (kDecResident + n - 1) / n;
+  return per_min < bound ? per_min : bound;
+}
+
 template <int D>
 struct DecLayout {
   static constexpr int kLanesPerRow = D / 8;          // each lane owns 8 consecutive d
@@ -99,13 +134,14 @@ template <int D, int DT, int BID = BID_SOFTMAX>
 __global__ __launch_bounds__(kDecThreads) void dec_stats(
     const void* __restrict__ q1, int qdt, int64_t q_sn, const void* __restrict__ kc, int64_t kv_sn,
     float* __restrict__ aff, float2* __restrict__ part, int64_t length, int64_t chunk, int nchunk,
-    float qscale, int64_t slice0, const int64_t* __restrict__ dlen) {
+    float qscale, int64_t slice0, int64_t nslices, const int64_t* __restrict__ dlen) {
   using L = DecLayout<D>;
   const int64_t slice = slice0 + blockIdx.y;
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % L::kLanesPerRow, rw = lane / L::kLanesPerRow;
   const int64_t live = live_length(dlen, length);
+  if (dlen != nullptr) chunk = decode_chunk(nslices, live);
   if (c >= live_chunks(live, chunk)) return;             // past the live length: no statistics
   const int64_t j0 = c * chunk;
   const int64_t j1 = min(j0 + chunk, live);
@@ -200,7 +236,7 @@ template <int D, int DT, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 __global__ __launch_bounds__(kDecThreads) void dec_apply(
     const void* __restrict__ vc, int64_t kv_sn, float* __restrict__ committed, int64_t c_sn,
     const float* __restrict__ aff, const float2* __restrict__ part, float* __restrict__ part_out,
-    int64_t length, int64_t chunk, int nchunk, float shift, int64_t slice0,
+    int64_t length, int64_t chunk, int nchunk, float shift, int64_t slice0, int64_t nslices,
     const int64_t* __restrict__ dlen) {
   using L = DecLayout<D>;
   const int64_t slice = slice0 + blockIdx.y;
@@ -210,6 +246,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
   // the scratch strides keep `length` and `nchunk` (the maxima); the walk
   // covers the live length only
   const int64_t live = live_length(dlen, length);
+  if (dlen != nullptr) chunk = decode_chunk(nslices, live);
   const int nlive = live_chunks(live, chunk);
   if (c >= nlive) return;
 
@@ -311,7 +348,9 @@ __global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part
                                                   const int64_t* __restrict__ dlen) {
   const int64_t slice = blockIdx.x;
   const float* base = part_out + slice * nchunk * (D + 1);      // slice stride: the maximum
-  nchunk = live_chunks(live_length(dlen, length), chunk);
+  const int64_t live = live_length(dlen, length);
+  if (dlen != nullptr) chunk = decode_chunk(gridDim.x, live);   // one workgroup per slice
+  nchunk = live_chunks(live, chunk);
   __shared__ float tot_s;
   if (threadIdx.x == D) {
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -341,17 +380,13 @@ __global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part
   if (d < D) store_as(out, slice * o_sn + d, dt, ((t0 + t1) + (t2 + t3)) / (tot_s + kEps));
 }
 
-// Keys per workgroup (see kDecThreads).
-int64_t decode_chunk(int64_t n, int64_t length) {
-  (void)n;
-  (void)length;
-  return 2048;
-}
 
 template <int D, int DT, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 int launch_decode(const DecodeArgs& a) {
+  // with a device-resident length the kernels choose the chunk from the live
+  // length; the grid and scratch cover every live length up to a.length
   const int64_t chunk = decode_chunk(a.n, a.length);
-  const int nchunk = static_cast<int>((a.length + chunk - 1) / chunk);
+  const int nchunk = static_cast<int>(decode_chunks(a.n, a.length, a.dlen != nullptr));
   char* ws = static_cast<char*>(a.workspace);
   float* aff = reinterpret_cast<float*>(ws);
   size_t off = align_up(sizeof(float) * a.n * a.length);
@@ -365,13 +400,13 @@ int launch_decode(const DecodeArgs& a) {
     DIL_TIMED("dec_stats", st,
               (dec_stats<D, DT, BID><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
                   a.q1, a.q_dtype, a.q_sn, a.k_cache, a.kv_sn, aff, part, a.length, chunk, nchunk,
-                  qscale, s0, a.dlen)));
+                  qscale, s0, a.n, a.dlen)));
   });
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("dec_apply", st,
               (dec_apply<D, DT, BID, SHARE><<<dim3(nchunk, ns), kDecThreads, 0, st>>>(
                   a.v_cache, a.kv_sn, a.committed, a.c_sn, aff, part, part_out, a.length, chunk, nchunk,
-                  a.var.shift, s0, a.dlen)));
+                  a.var.shift, s0, a.n, a.dlen)));
   });
   DIL_TIMED("dec_finish", st,
             dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
