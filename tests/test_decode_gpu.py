@@ -146,6 +146,33 @@ def test_device_length_decode_is_the_decode_step(dtype, head_dim):
         assert torch.equal(c_dev, c_ref), length
 
 
+def test_device_length_decode_keeps_the_chunks_of_the_live_length():
+    """B8 H16: the key chunks follow the batch and the live length (2048 keys
+    at 16384, 1409 at 16900, where 2048-key chunks would leave a part-filled
+    round; 513 at 2049).  The replayed form picks them from the device-resident
+    length, so it stays bitwise equal to the host-length step at every length
+    while its grid and workspace are sized once for the capacity."""
+    from dilution import kernels
+
+    batch, heads, cap, d = 8, 16, 17000, 64
+    g = torch.Generator(device="cuda").manual_seed(21)
+    kc = torch.randn(batch, heads, cap, d, device="cuda", generator=g).bfloat16()
+    vc = torch.randn(batch, heads, cap, d, device="cuda", generator=g).bfloat16()
+    base = torch.rand(batch, heads, cap, device="cuda", generator=g) * 3
+    ws = kernels.decode_workspace(batch, heads, cap, d, "cuda")
+    for length in (300, 2049, 8192, 16384, 16385, 16900, 17000):
+        q1 = torch.randn(batch, heads, 1, d, device="cuda", generator=g).bfloat16()
+        c_ref = base.clone()
+        c_ref[..., length - 1] = 0
+        c_dev = c_ref.clone()
+        want = kernels.dilution_decode_step(q1, kc, vc, c_ref, length)
+        got = kernels.decode_step_device_length(q1, kc, vc, c_dev, torch.tensor([length], device="cuda"), cap,
+                                                workspace=ws)
+        assert torch.equal(got, want), length
+        assert torch.equal(c_dev, c_ref), length
+        assert torch.equal(c_dev[..., length:], base[..., length:]), length
+
+
 def test_device_length_decode_clamps_the_live_length():
     """A live length past max_length runs as max_length; 0 leaves the demand
     untouched and outputs zeros.  Nothing past max_length is read or written."""
