@@ -49,28 +49,36 @@ constexpr int64_t kDecResident = 512;
 constexpr int64_t kDecMaxChunk = 2048;
 constexpr int64_t kDecMinChunk = 256;
 
-__host__ __device__ inline int64_t decode_chunk(int64_t n, int64_t length) {
-  if (length < 1 || n < 1) return kDecMinChunk;
+// The chunk count that fills whole rounds: never below the 2048-key count,
+// and non-decreasing in `length`.
+__host__ __device__ inline int64_t decode_target_chunks(int64_t n, int64_t length) {
   const int64_t base = (length + kDecMaxChunk - 1) / kDecMaxChunk;     // chunks at the largest size
   const int64_t rounds = (n * base + kDecResident - 1) / kDecResident;
-  int64_t target = rounds * kDecResident / n;                          // chunks that fill `rounds`
-  if (target < base) target = base;
+  const int64_t target = rounds * kDecResident / n;
+  return target < base ? base : target;
+}
+
+__host__ __device__ inline int64_t decode_chunk(int64_t n, int64_t length) {
+  if (length < 1 || n < 1) return kDecMinChunk;
+  const int64_t target = decode_target_chunks(n, length);
   const int64_t chunk = (length + target - 1) / target;
   return chunk < kDecMinChunk ? kDecMinChunk : chunk;
 }
 
 // Chunks per slice in the grid and the scratch: exact for a host length; for
-// a device-resident live length up to `length`, a bound on every live length's
-// count (at most the 2048-key count plus one round's share per slice, and at
-// most one chunk per 256 keys).
+// a device-resident live length up to `length`, the largest count of any live
+// length.  A live length L <= length has at most target(L) <= target(length)
+// chunks (the target does not decrease with the length), and at most one per
+// 256 keys.
 inline int64_t decode_chunks(int64_t n, int64_t length, bool device_length) {
+  if (length < 1) return 1;
   if (!device_length) {
     const int64_t chunk = decode_chunk(n, length);
     return (length + chunk - 1) / chunk;
   }
   const int64_t per_min = (length + kDecMinChunk - 1) / kDecMinChunk;
-  const int64_t bound = (length + kDecMaxChunk - 1) / kDecMaxChunk + (kDecResident + n - 1) / n;
-  return per_min < bound ? per_min : bound;
+  const int64_t target = decode_target_chunks(n < 1 ? 1 : n, length);
+  return per_min < target ? per_min : target;
 }
 
 template <int D>
