@@ -269,6 +269,73 @@ int launch_rows_linear(const __bf16* x, const __bf16* w1, const __bf16* w2, cons
   return static_cast<int>(hipGetLastError());
 }
 
+// Greedy selection over the head's logits: per row, the index of the largest
+// of the first `limit` values, as torch.argmax picks it (a NaN counts as the
+// largest value, and among equal values the smallest index wins).  One
+// 1024-thread workgroup per row; 16-byte loads when the rows are aligned.
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
+  const bool an = a != a, bn = b != b;
+  if (an != bn) return an;
+  if (!an && a != b) return a > b;
+  return ia < ib;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kArgThreads) void rows_argmax(const __bf16* __restrict__ logits, int64_t stride,
+                                                           int limit, int64_t* __restrict__ out) {
+  const __bf16* p = logits + static_cast<int64_t>(blockIdx.x) * stride;
+  const int t = threadIdx.x;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  if constexpr (VEC) {
+    const int nvec = limit / 8;
+    constexpr int kU = 8;
+    for (int c0 = t; c0 < nvec; c0 += kU * kArgThreads) {
+      bf16x8 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (c0 + u * kArgThreads < nvec) v[u] = reinterpret_cast<const bf16x8*>(p)[c0 + u * kArgThreads];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int c = c0 + u * kArgThreads;
+        if (c < nvec) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = static_cast<float>(v[u][e]);
+            if (arg_better(x, 8 * c + e, best, bi)) { best = x; bi = 8 * c + e; }
+          }
+        }
+      }
+    }
+    for (int i = 8 * nvec + t; i < limit; i += kArgThreads) {
+      const float x = static_cast<float>(p[i]);
+      if (arg_better(x, i, best, bi)) { best = x; bi = i; }
+    }
+  } else {
+    for (int i = t; i < limit; i += kArgThreads) {
+      const float x = static_cast<float>(p[i]);
+      if (arg_better(x, i, best, bi)) { best = x; bi = i; }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (arg_better(ob, oi, best, bi)) { best = ob; bi = oi; }
+  }
+  __shared__ float sb[kArgThreads / 64];
+  __shared__ int si[kArgThreads / 64];
+  if ((t & 63) == 0) { sb[t >> 6] = best; si[t >> 6] = bi; }
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < kArgThreads / 64; ++w)
+      if (arg_better(sb[w], si[w], best, bi)) { best = sb[w]; bi = si[w]; }
+    out[blockIdx.x] = bi;
+  }
+}
+
 bool rows_k_ok(int64_t rows, int64_t k) {
   return rows >= 1 && rows <= kLinRows && k >= 256 && k <= kLinMaxK && k % 256 == 0;
 }
@@ -323,4 +390,22 @@ extern "C" int dil_rows_linear_qkv(const void* x, const void* w, const void* g, 
                                     static_cast<const __bf16*>(g), nullptr, static_cast<__bf16*>(q_out),
                                     static_cast<int>(rows), 3 * heads * head_dim, static_cast<int>(k), eps, dst,
                                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dil_rows_argmax(const void* logits, int64_t rows, int64_t row_stride, int64_t limit, void* out,
+                               int dtype, void* stream) {
+  if (dtype != dil::DT_BF16) return dil::kErrDtype;
+  if (logits == nullptr || out == nullptr || rows < 1 || rows > 65535 || limit < 1 || limit > 0x7fffffff ||
+      row_stride < limit)
+    return dil::kErrShape;
+  const auto* lb = static_cast<const __bf16*>(logits);
+  auto* ob = static_cast<int64_t*>(out);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = row_stride % 8 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (vec)
+    dil::rows_argmax<true><<<grid, dil::kArgThreads, 0, st>>>(lb, row_stride, static_cast<int>(limit), ob);
+  else
+    dil::rows_argmax<false><<<grid, dil::kArgThreads, 0, st>>>(lb, row_stride, static_cast<int>(limit), ob);
+  return static_cast<int>(hipGetLastError());
 }

@@ -54,6 +54,7 @@ SIGNATURES = {
                                  ctypes.c_float, _vp]),
     "dil_rows_linear_qkv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _c_int64, _vp,
                                      _c_int64, _c_int64, _c_int, ctypes.c_float, _vp]),
+    "dil_rows_argmax": (_c_int, [_vp, _c_int64, _c_int64, _c_int64, _vp, _c_int, _vp]),
     "dil_timing_enable": (_c_int, [_c_int]),
     "dil_timing_reset": (_c_int, []),
     "dil_timing_count": (_c_int, []),

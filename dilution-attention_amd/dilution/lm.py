@@ -58,7 +58,7 @@ _LIN_MAX_ROWS, _LIN_MAX_K = 8, 4096
 
 def rows_linear(x: torch.Tensor, w1: torch.Tensor, mode: int, *, w2: torch.Tensor | None = None,
                 g: torch.Tensor | None = None, resid: torch.Tensor | None = None,
-                eps: float = 0.0) -> torch.Tensor:
+                eps: float = 0.0, out: torch.Tensor | None = None) -> torch.Tensor:
     """A few-row projection on the HIP library (``dil_rows_linear``): for
     bf16 x (rows, K) with rows <= 8 and nn.Linear weights (N, K), mode 0
     returns x W1^T, 1 resid + x W1^T, 2 rmsnorm(x; g, eps) W1^T, 3
@@ -71,7 +71,10 @@ def rows_linear(x: torch.Tensor, w1: torch.Tensor, mode: int, *, w2: torch.Tenso
     for t in (x, w1, w2, g, resid):
         if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != x.device):
             raise ValueError("rows_linear takes contiguous bf16 tensors on one device")
-    out = torch.empty(rows, n, device=x.device, dtype=x.dtype)
+    if out is None:
+        out = torch.empty(rows, n, device=x.device, dtype=x.dtype)
+    elif out.shape != (rows, n) or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != x.device:
+        raise ValueError("out must be a contiguous bf16 (rows, N) tensor on the inputs' device")
     status = lib.dil_rows_linear(x.data_ptr(), w1.data_ptr(), None if w2 is None else w2.data_ptr(),
                                  None if g is None else g.data_ptr(), None if resid is None else resid.data_ptr(),
                                  out.data_ptr(), rows, n, k, mode, 1, float(eps),
@@ -111,6 +114,26 @@ def rows_linear_qkv(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor, eps: floa
     _hip.check(status, "dil_rows_linear_qkv")
     return q
 
+
+def rows_argmax(logits: torch.Tensor, limit: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy tokens from bf16 logits (rows, V) on the HIP library
+    (``dil_rows_argmax``): per row the index of the largest of the first
+    ``limit`` (default V) values, as torch.argmax picks it; returned as an
+    int64 (rows, 1) tensor, written into ``out`` when given.  (No reference
+    counterpart: the reference's sampler calls torch.argmax,
+    model.py:473-509.)"""
+    rows, vocab = logits.shape
+    limit = vocab if limit is None else int(limit)
+    if logits.dtype != torch.bfloat16 or logits.stride(1) != 1 or not 0 < limit <= vocab:
+        raise ValueError("rows_argmax takes bf16 (rows, V) logits with unit column stride and 0 < limit <= V")
+    if out is None:
+        out = torch.empty(rows, 1, device=logits.device, dtype=torch.int64)
+    elif out.dtype != torch.int64 or out.numel() != rows or not out.is_contiguous() or out.device != logits.device:
+        raise ValueError("out must be a contiguous int64 tensor of one element per row")
+    status = _hip.lib().dil_rows_argmax(logits.data_ptr(), rows, logits.stride(0), limit, out.data_ptr(), 1,
+                                        torch.cuda.current_stream(logits.device).cuda_stream)
+    _hip.check(status, "dil_rows_argmax")
+    return out
 
 @dataclass
 class LMConfig:
@@ -407,8 +430,9 @@ class DilutionLM(nn.Module):
             x2 = rows_linear(h, mlp.down_proj.weight, _LIN_RESID, resid=x2)
         return x2
 
-    def _fused_head(self, x2: torch.Tensor) -> torch.Tensor:
-        logits = rows_linear(x2, self.lm_head.weight, _LIN_NORM, g=self.ln_f.weight, eps=self._norm_eps(self.ln_f))
+    def _fused_head(self, x2: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        logits = rows_linear(x2, self.lm_head.weight, _LIN_NORM, g=self.ln_f.weight, eps=self._norm_eps(self.ln_f),
+                             out=out)
         return logits.view(x2.shape[0], 1, -1)
 
     @torch.no_grad()
@@ -495,6 +519,7 @@ class GraphDecoder:
         self.ws = kernels.decode_workspace(self.batch, self.heads, self.capacity, self.head_dim, dev)
         self.logits = torch.empty(self.batch, 1, model.cfg.vocab_size, device=dev, dtype=qdt)
         self.mask = None
+        self.limit = model.cfg.vocab_size if vocab_limit is None else int(vocab_limit)
         if vocab_limit is not None:
             self.mask = torch.zeros(model.cfg.vocab_size, device=dev)
             self.mask[vocab_limit:] = float("-inf")
@@ -522,8 +547,11 @@ class GraphDecoder:
     def _body(self) -> None:
         m = self.model
         if self.fused:
+            # the head writes the logits buffer and the greedy pick the token
+            # buffer directly: no copies, no fp32 logits
             x2 = m._fused_layers(m.wte(self.tok).view(self.batch, -1), self._slot, self._attend_q)
-            logits = m._fused_head(x2)
+            m._fused_head(x2, out=self.logits.view(self.batch, -1))
+            rows_argmax(self.logits.view(self.batch, -1), self.limit, out=self.tok)
         else:
             x = m.wte(self.tok)
             for i, block in enumerate(m.h):
@@ -532,11 +560,11 @@ class GraphDecoder:
                 x = x + block.attn._merge_heads(y.to(x.dtype), self.batch, 1)
                 x = x + block.mlp(block.ln_2(x))
             logits = m.lm_head(m.ln_f(x))
-        self.logits.copy_(logits)
-        last = logits[:, -1, :].float()
-        if self.mask is not None:
-            last = last + self.mask
-        self.tok.copy_(last.argmax(dim=-1, keepdim=True))
+            self.logits.copy_(logits)
+            last = logits[:, -1, :].float()
+            if self.mask is not None:
+                last = last + self.mask
+            self.tok.copy_(last.argmax(dim=-1, keepdim=True))
         self.pos.add_(1)
         self.live.add_(1)
 

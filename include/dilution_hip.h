@@ -255,6 +255,19 @@ int dil_rows_linear_qkv(const void* x, const void* w, const void* g, void* q_out
                         const int64_t* pos_dev, int64_t pos, int64_t k, int dtype, float eps, void* stream);
 
 /*
+ * Greedy token selection for the decode step.  No counterpart in the
+ * reference, whose sampler takes torch.argmax of the last position's logits
+ * (model.py:473-509).  out[r] (int64) = the index of the largest of
+ * logits[r, 0:limit] for r < rows, with torch.argmax's choice: a NaN counts
+ * as the largest value, and among equal values the smallest index wins.
+ * logits are bf16 (dtype code 1; others return -2), row r at
+ * logits + r * row_stride elements; 1 <= rows <= 65535,
+ * 1 <= limit <= row_stride, limit < 2^31.  Asynchronous on `stream`.
+ */
+int dil_rows_argmax(const void* logits, int64_t rows, int64_t row_stride, int64_t limit, void* out, int dtype,
+                    void* stream);
+
+/*
  * Kernel timing for measurement harnesses.  No reference counterpart (the
  * reference times its Triton launches with torch.profiler and CUDA events in
  * scripts/step_profile.py:29-47 and scripts/profile_kernels.py:115-144).

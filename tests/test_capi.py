@@ -144,6 +144,16 @@ def test_rows_linear_qkv_argument_errors_before_any_launch(lib):
         assert call(b=[None if i == hole else p for i, p in enumerate(bufs)]) == -4, hole
 
 
+def test_rows_argmax_argument_errors_before_any_launch(lib):
+    lg, out = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    assert lib.dil_rows_argmax(lg, 8, 100, 100, out, 0, None) == -2          # fp32
+    assert lib.dil_rows_argmax(None, 8, 100, 100, out, 1, None) == -4
+    assert lib.dil_rows_argmax(lg, 8, 100, 100, None, 1, None) == -4
+    assert lib.dil_rows_argmax(lg, 0, 100, 100, out, 1, None) == -4
+    assert lib.dil_rows_argmax(lg, 8, 100, 0, out, 1, None) == -4
+    assert lib.dil_rows_argmax(lg, 8, 100, 101, out, 1, None) == -4         # limit past the row
+
+
 def test_null_pointers_are_argument_errors(lib):
     """A NULL where the header requires a buffer is a status (-4) returned
     before any launch, never a device fault.  The stand-in addresses below are

@@ -165,6 +165,33 @@ def test_qkv_device_position_outside_the_cache_stores_no_row():
         _check_close(q, F.linear(F.rms_norm(x, (d,), g, 1e-5), w)[:, :d], "q")
 
 
+@pytest.mark.parametrize("rows,vocab,limit,offset", [(1, 50304, None, 0), (8, 50304, 50000, 0), (3, 1000, 999, 0),
+                                                     (8, 4099, None, 0), (2, 64, 7, 3)])
+def test_rows_argmax_is_torch_argmax(rows, vocab, limit, offset):
+    """dil_rows_argmax against torch.argmax over the first `limit` logits:
+    random rows, rows with a repeated maximum (the first index wins), a row
+    whose maximum lies past the limit, a row with a NaN, and an unaligned
+    view (offset columns: the scalar path)."""
+    from dilution.lm import rows_argmax
+
+    gen = torch.Generator().manual_seed(rows + vocab)
+    full = _bf(rows, vocab + offset, gen=gen, scale=3.0)
+    lg = full[:, offset:]
+    lim = vocab if limit is None else limit
+    if rows > 1:
+        lg[1, 5] = lg[1, lim - 2] = 100.0                     # a tie: index 5 wins
+    if rows > 2:
+        lg[2, :] = -1.0
+        lg[2, lim - 1] = float("nan")                          # a NaN counts as the largest
+    if lim < vocab:
+        lg[0, vocab - 1] = 1000.0                              # past the limit: ignored
+    got = rows_argmax(lg, limit)
+    want = lg[:, :lim].float().argmax(dim=-1, keepdim=True)
+    assert torch.equal(got, want), (got.flatten().tolist(), want.flatten().tolist())
+    if rows > 1:
+        assert got[1, 0].item() == 5
+
+
 def _lm():
     from dilution.lm import DilutionLM, LMConfig
 
