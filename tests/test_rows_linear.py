@@ -35,7 +35,8 @@ def _check_close(out, ref, what):
 
 
 @pytest.mark.parametrize("rows", [1, 5, 8])
-@pytest.mark.parametrize("n,k", [(40, 256), (1000, 1024), (3072, 1024), (1024, 4096), (9000, 1024)])
+@pytest.mark.parametrize("n,k", [(40, 256), (1000, 1024), (3072, 1024), (1024, 4096), (9000, 1024), (600, 2048),
+                                 (2048, 1536), (8192, 4096)])
 def test_plain_and_residual_match_torch(rows, n, k):
     from dilution.lm import rows_linear
 
@@ -48,7 +49,7 @@ def test_plain_and_residual_match_torch(rows, n, k):
 
 
 @pytest.mark.parametrize("rows", [2, 8])
-@pytest.mark.parametrize("n,k", [(3072, 1024), (50304, 1024), (64, 256)])
+@pytest.mark.parametrize("n,k", [(3072, 1024), (50304, 1024), (64, 256), (1000, 2048), (5000, 4096), (9000, 3072)])
 def test_norm_projection_matches_torch(rows, n, k):
     from dilution.lm import rows_linear
 
@@ -80,11 +81,10 @@ def test_norm_stage_equals_rms_norm(rows):
 
 
 @pytest.mark.parametrize("rows", [1, 8])
-@pytest.mark.parametrize("n", [4096, 1000])
-def test_swiglu_matches_torch(rows, n):
+@pytest.mark.parametrize("n,k", [(4096, 1024), (1000, 1024), (2048, 4096)])
+def test_swiglu_matches_torch(rows, n, k):
     from dilution.lm import rows_linear
 
-    k = 1024
     gen = torch.Generator().manual_seed(rows + n + 1)
     x = _bf(rows, k, gen=gen)
     g = (1.0 + 0.1 * torch.randn(k, generator=gen)).to(torch.bfloat16).cuda()
@@ -113,17 +113,18 @@ def test_rows_past_the_batch_are_untouched():
     _check_close(out, F.linear(x, w), "view")
 
 
-@pytest.mark.parametrize("rows", [1, 8])
+@pytest.mark.parametrize("rows,heads", [(1, 16), (8, 16), (8, 32), (3, 64)])
 @pytest.mark.parametrize("device_pos", [False, True])
-def test_qkv_projection_writes_the_cache_row(rows, device_pos):
+def test_qkv_projection_writes_the_cache_row(rows, heads, device_pos):
     """rows_linear_qkv: q = the first third of rmsnorm(x) W^T; the k and v
     thirds land in row `pos` of the (B, H, capacity, D) caches, every other
-    cache row untouched."""
+    cache row untouched.  d_model 1024, 2048 and 4096 (N = 3 d_model from
+    12288 takes the one-row-per-lane-group form)."""
     from dilution.lm import rows_linear_qkv
 
-    heads, hd, cap, pos = 16, 64, 40, 17
+    hd, cap, pos = 64, 40, 17
     d = heads * hd
-    gen = torch.Generator().manual_seed(rows + 40)
+    gen = torch.Generator().manual_seed(rows + heads + 40)
     x = _bf(rows, d, gen=gen, scale=2.0)
     g = (1.0 + 0.1 * torch.randn(d, generator=gen)).to(torch.bfloat16).cuda()
     w = _bf(3 * d, d, gen=gen, scale=0.02)
