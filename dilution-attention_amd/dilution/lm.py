@@ -463,14 +463,19 @@ class DilutionLM(nn.Module):
                     out.append(dec.step().clone())
             return torch.cat([tokens, *out], dim=1)
         for step in range(max_new_tokens):
-            last = logits[:, -1, :].float()
-            if vocab_limit is not None:
-                last[:, vocab_limit:] = float("-inf")
-            if temperature and temperature > 0.0:
-                probs = filter_logits(last / temperature, top_k=top_k, top_p=top_p).softmax(dim=-1)
-                nxt = torch.multinomial(probs, 1, generator=generator)
+            greedy = not (temperature and temperature > 0.0)
+            if greedy and logits.dtype == torch.bfloat16 and logits.is_cuda and kernels.HAS_HIP:
+                # torch.argmax's pick over the first vocab_limit logits, on the device
+                nxt = rows_argmax(logits[:, -1, :], vocab_limit)
             else:
-                nxt = last.argmax(dim=-1, keepdim=True)
+                last = logits[:, -1, :].float()
+                if vocab_limit is not None:
+                    last[:, vocab_limit:] = float("-inf")
+                if greedy:
+                    nxt = last.argmax(dim=-1, keepdim=True)
+                else:
+                    probs = filter_logits(last / temperature, top_k=top_k, top_p=top_p).softmax(dim=-1)
+                    nxt = torch.multinomial(probs, 1, generator=generator)
             tokens = torch.cat([tokens, nxt], dim=1)
             if step + 1 < max_new_tokens:
                 logits = self.decode_step(nxt, caches)

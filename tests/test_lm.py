@@ -238,8 +238,13 @@ def test_graph_decode_replays_match_eager_decode(dtype):
 
 @pytest.mark.gpu
 @needs_gpu
-def test_generate_graph_matches_eager():
-    model = _small()
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_generate_graph_matches_eager(dtype):
+    """Greedy generation replayed and eager give the same tokens, also under a
+    vocabulary limit.  A bf16 model's eager steps pick on the device
+    (rows_argmax) while its replayed steps at this width take torch.argmax
+    of the fp32 logits."""
+    model = _small(dtype=dtype)
     idx = torch.zeros(2, 5, dtype=torch.long, device="cuda")
     assert torch.equal(model.generate(idx, 9, graph=True), model.generate(idx, 9))
     assert torch.equal(model.generate(idx, 9, graph=True, vocab_limit=10),
