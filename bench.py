@@ -604,12 +604,15 @@ def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
     logits, caches = model.prefill(prompt, capacity=pt + decode_tokens * (2 if graph else 1))
     torch.cuda.synchronize()
     ms_prefill = (time.perf_counter() - t0) * 1e3
-    tok = logits[:, -1].float().argmax(-1, keepdim=True)
+    from dilution.lm import rows_argmax
+
+    # greedy pick as generate() makes it for a bf16 model (torch.argmax's choice, on the device)
+    tok = rows_argmax(logits[:, -1])
 
     def decode_one():
         nonlocal logits, tok
         logits = model.decode_step(tok, caches)
-        tok = logits[:, -1].float().argmax(-1, keepdim=True)
+        tok = rows_argmax(logits[:, -1])
 
     decode_one()
     ms_decode = timed(decode_one, decode_tokens - 2)
