@@ -628,6 +628,22 @@ def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
         ctx0 = caches[0]["len"]
         ms_graph = timed(dec.step, decode_tokens - 2)
         log(f"lm[{kind}] graph decode {ms_graph:.3f} ms/token-step")
+        # one sequence (the serving-latency case): the same prompt's first row
+        logits1, caches1 = model.prefill(prompt[:1], capacity=pt + 262)
+        tok1 = rows_argmax(logits1[:, -1])
+
+        def decode_b1():
+            nonlocal logits1, tok1
+            logits1 = model.decode_step(tok1, caches1)
+            tok1 = rows_argmax(logits1[:, -1])
+
+        decode_b1()
+        ms_b1 = timed(decode_b1, 128)
+        dec1 = GraphDecoder(model, caches1, tok1)
+        dec1.step()                                         # warm-up and capture
+        ms_b1_graph = timed(dec1.step, 128)
+        log(f"lm[{kind}] decode B1 {ms_b1:.3f} ms/token, replayed {ms_b1_graph:.3f} ms/token")
+        del dec1, caches1, logits1
     out = {"train": {"tokens_per_s": round(tb * tt / (ms_train * 1e-3), 1),
                      "ms_per_step": round(ms_train, 2), "steps": args.lm_train_steps,
                      "first_loss": round(loss0, 4), "batch": tb, "seq_len": tt,
@@ -647,6 +663,11 @@ def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
                                   "timed_steps": decode_tokens - 2,
                                   "context": f"{ctx0 + 1}..{ctx0 + decode_tokens - 2}",
                                   "how": "GraphDecoder: each step one HIP graph replay, length on the device"}
+        out["decode"]["b1"] = {"tokens_per_s": round(1.0 / (ms_b1 * 1e-3), 1), "ms_per_token": round(ms_b1, 4),
+                               "timed_steps": 128, "context": f"{pt + 2}..{pt + 129}", "greedy": True,
+                               "graph": {"tokens_per_s": round(1.0 / (ms_b1_graph * 1e-3), 1),
+                                         "ms_per_token": round(ms_b1_graph, 4), "timed_steps": 128,
+                                         "context": f"{pt + 131}..{pt + 258}"}}
     out["config"] = {"workload": "C5 whole-LM", "attention": kind, "layers": cfg.n_layers,
                      "d_model": cfg.d_model, "heads": cfg.n_heads,
                      "head_dim": cfg.d_model // cfg.n_heads, "mlp": "SwiGLU 4x",
