@@ -24,6 +24,7 @@ and ignored: tiles are fixed for gfx950.
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -131,8 +132,21 @@ def _rows(x: torch.Tensor, n: int, t: int, d: int, dtype: torch.dtype) -> torch.
 
 
 def _stream(dev: torch.device) -> int:
-    """The caller's current stream on the inputs' device; launches go there."""
-    return torch.cuda.current_stream(dev).cuda_stream
+    """The caller's current stream on the inputs' device; launches go there.
+    (The raw handle, without building a torch Stream object: a decode step
+    asks for it about 60 times.)"""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
+
+
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def _on(dev: torch.device):
+    """The inputs' device made current for a launch; no switch when it already is."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _NO_SWITCH
+    return torch.cuda.device(dev)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -210,7 +224,7 @@ def dilution_attention_forward(
         tail = (out[a:b].data_ptr(), rmax[a:b].data_ptr(), rden[a:b].data_ptr(),
                 ssum[a:b].data_ptr(), carry.data_ptr(), total[a:b].data_ptr(),
                 None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
-        with torch.cuda.device(dev):
+        with _on(dev):
             if tuple(_variant) == _PRODUCTION:
                 status = lib.dil_forward(*head, *tail)
             else:
@@ -278,7 +292,7 @@ def _backward(saved, dout, dot_precision: str, variant: tuple):
             rmax.data_ptr(), rden.data_ptr(), ssum.data_ptr(), carry.data_ptr(), pk.data_ptr(),
             n, seq, head_dim, _DTYPES[dt], _DTYPES[ddt], _DTYPES[gdt], prec)
     tail = (dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
-    with torch.cuda.device(dev):
+    with _on(dev):
         if tuple(variant) == _PRODUCTION:
             status = lib.dil_backward(*head, *tail)
         else:
@@ -367,7 +381,7 @@ def dilution_prefill_chunk(
     ssum = torch.empty(n, chunk, **f32)
     carry = torch.empty(n, nb, start + chunk, **f32)
     ws = _workspace(lib.dil_prefill_workspace_bytes(n, chunk, start, head_dim, _DTYPES[dt], prec), dev)
-    with torch.cuda.device(dev):
+    with _on(dev):
         status = lib.dil_prefill_chunk(
             qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), n, chunk, start, capacity, head_dim,
             _DTYPES[dt], prec, cf.data_ptr(), out.data_ptr(), rmax.data_ptr(), rden.data_ptr(),
@@ -431,7 +445,7 @@ def dilution_decode_step(
     head = (qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), cf.data_ptr(), out.data_ptr(), n,
             capacity, length, head_dim, _DTYPES[dt], _DTYPES[qdt])
     tail = (ws.data_ptr(), ws.numel(), _stream(q1.device))
-    with torch.cuda.device(q1.device):
+    with _on(q1.device):
         if tuple(_variant) == _PRODUCTION:
             status = lib.dil_decode_step(*head, *tail)
         else:

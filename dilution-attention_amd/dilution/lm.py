@@ -78,7 +78,7 @@ def rows_linear(x: torch.Tensor, w1: torch.Tensor, mode: int, *, w2: torch.Tenso
     status = lib.dil_rows_linear(x.data_ptr(), w1.data_ptr(), None if w2 is None else w2.data_ptr(),
                                  None if g is None else g.data_ptr(), None if resid is None else resid.data_ptr(),
                                  out.data_ptr(), rows, n, k, mode, 1, float(eps),
-                                 torch.cuda.current_stream(x.device).cuda_stream)
+                                 kernels._stream(x.device))
     _hip.check(status, "dil_rows_linear")
     return out
 
@@ -110,7 +110,7 @@ def rows_linear_qkv(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor, eps: floa
         pos_dev, pos_host = None, int(pos)
     status = lib.dil_rows_linear_qkv(x.data_ptr(), w.data_ptr(), g.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
                                      v_cache.data_ptr(), rows, heads, head_dim, capacity, pos_dev, pos_host, k, 1,
-                                     float(eps), torch.cuda.current_stream(x.device).cuda_stream)
+                                     float(eps), kernels._stream(x.device))
     _hip.check(status, "dil_rows_linear_qkv")
     return q
 
@@ -131,7 +131,7 @@ def rows_argmax(logits: torch.Tensor, limit: int | None = None, out: torch.Tenso
     elif out.dtype != torch.int64 or out.numel() != rows or not out.is_contiguous() or out.device != logits.device:
         raise ValueError("out must be a contiguous int64 tensor of one element per row")
     status = _hip.lib().dil_rows_argmax(logits.data_ptr(), rows, logits.stride(0), limit, out.data_ptr(), 1,
-                                        torch.cuda.current_stream(logits.device).cuda_stream)
+                                        kernels._stream(logits.device))
     _hip.check(status, "dil_rows_argmax")
     return out
 
