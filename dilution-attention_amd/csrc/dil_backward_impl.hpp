@@ -926,8 +926,16 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 // operand is jac dp, the ratio bids' ghat partials are the row sums of p dp
 // (a second transposed tile), and the elementwise bids have none.
 
+// Storage type of the dq partials: bf16 by default; fp32 when built with
+// -DDIL_KEYQ_F32_PARTIALS=1 (twice the bytes written and read back), the
+// comparison build for the accuracy of the bf16 partials.
+#ifndef DIL_KEYQ_F32_PARTIALS
+#define DIL_KEYQ_F32_PARTIALS 0
+#endif
+using KqPart = std::conditional_t<DIL_KEYQ_F32_PARTIALS != 0, float, __bf16>;
+
 template <int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
-__global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* __restrict__ dqp,
+__global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, KqPart* __restrict__ dqp,
                                                            float* __restrict__ ghp, int64_t ntiles) {
   static_assert(D == 64, "the dq-forming key pass is built for head_dim 64");
   using CT = __bf16;
@@ -1203,7 +1211,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
   // dq contribution of the group's 256 keys to query tile qt: wave w forms
   // rows 16 (w & 1) + [0, 16) x head dims 16 (w >> 1) + [0, 16)
   const int rh = wave & 1, dq4 = wave >> 1;
-  __bf16* dqp_s = dqp + slice * ntiles * (D * kTileQ);
+  KqPart* dqp_s = dqp + slice * ntiles * (D * kTileQ);
   float* ghp_s = ghp + slice * ntiles * kTileQ;
   const int64_t gbase = keyq_tile_base(kg, nq) - static_cast<int64_t>(kKqTilesPerGroup) * kg;
   auto dq_product = [&](int qt, int buf) {
@@ -1218,13 +1226,16 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
     // output: lane <-> head dim 16 dq4 + (lane & 15), register j <-> row 16 rh + 4 (lane >> 4) + j;
     // the partial tile is stored [d][32 rows]
     const int64_t tile = gbase + qt;
-    const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
-    const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
-    const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
+    KqPart* dst = dqp_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ + 16 * rh + 4 * (lane >> 4);
     // streamed past the caches: the partials are read once, by bwd_dq_reduce
-    __builtin_nontemporal_store(__builtin_bit_cast(floatx2, v),
-                                reinterpret_cast<floatx2*>(dqp_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ +
-                                                           16 * rh + 4 * (lane >> 4)));
+    if constexpr (std::is_same_v<KqPart, float>) {
+      __builtin_nontemporal_store(acc, reinterpret_cast<floatx4*>(dst));
+    } else {
+      const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
+      const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
+      const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
+      __builtin_nontemporal_store(__builtin_bit_cast(floatx2, v), reinterpret_cast<floatx2*>(dst));
+    }
     if (threadIdx.x < kTileQ) {
       float s = 0.f;
 #pragma unroll
@@ -1291,7 +1302,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, __bf16* _
 // tiles with the most key groups first.  Thread t sums elements [8 t, 8 t + 8)
 // of the [d][32 rows] partial tiles.
 template <int D, bool GHAT = true>
-__global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restrict__ dqp,
+__global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const KqPart* __restrict__ dqp,
                                                           const float* __restrict__ ghp, int64_t ntiles,
                                                           int64_t T, const float* __restrict__ pk,
                                                           const __bf16* __restrict__ qt, int64_t t_pad,
@@ -1305,25 +1316,42 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const __bf16* __restri
   const int tq = nq - 1 - static_cast<int>(blockIdx.x);
   const int ng = min(static_cast<int>(keyq_groups(T)) - 1, tq / kKqTilesPerGroup) + 1;
   const int t = threadIdx.x;
-  const __bf16* base = dqp + slice * ntiles * (D * kTileQ) + 8 * t;
+  const KqPart* base = dqp + slice * ntiles * (D * kTileQ) + 8 * t;
   // groups in order, four loads in flight (the partial sums are added in
   // group order: deterministic)
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   auto tile_of = [&](int g) { return keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g; };
+  auto load8 = [&](int g, float (&v)[8]) {
+    const KqPart* p = base + tile_of(g) * (D * kTileQ);
+    if constexpr (std::is_same_v<KqPart, float>) {
+      const floatx4 a = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
+      const floatx4 b = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p) + 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = b[e];
+      }
+    } else {
+      const bf16x8 x = load_once(p);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(x[e]);
+    }
+  };
   int g = 0;
   for (; g + 4 <= ng; g += 4) {
-    bf16x8 v[4];
+    float v[4][8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = load_once(base + tile_of(g + u) * (D * kTileQ));
+    for (int u = 0; u < 4; ++u) load8(g + u, v[u]);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
+      for (int e = 0; e < 8; ++e) acc[e] += v[u][e];
   }
   for (; g < ng; ++g) {
-    const bf16x8 v = load_once(base + tile_of(g) * (D * kTileQ));
+    float v[8];
+    load8(g, v);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
+    for (int e = 0; e < 8; ++e) acc[e] += v[e];
   }
   const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
 #pragma unroll
@@ -1389,7 +1417,7 @@ struct BwdWorkspace {
 constexpr int64_t kKeyqBudgetBytes = int64_t{24} << 30;
 
 inline int64_t keyq_partial_bytes(int64_t n, int64_t T, int D) {
-  return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
+  return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * sizeof(KqPart) + kTileQ * 4);
 }
 inline bool keyq_eligible(int64_t n, int64_t T, int D, int prec) {
   // bwd_keyq reads the Q, dO' rows and their transposed copies through one
@@ -1421,7 +1449,7 @@ BwdWorkspace bwd_layout(int64_t n, int64_t T, int D, int dtype, int dout_dtype, 
   w.dqp = w.sufk;
   w.ghp = w.sufk;
   if (keyq_eligible(n, T, D, prec)) {
-    const size_t dqb = align_up(static_cast<size_t>(n * keyq_tiles(T) * D * kTileQ * 2));
+    const size_t dqb = align_up(static_cast<size_t>(n * keyq_tiles(T) * D * kTileQ * sizeof(KqPart)));
     w.ghp = w.dqp + dqb;
     region = std::max(region, dqb + align_up(static_cast<size_t>(n * keyq_tiles(T) * kTileQ * 4)));
   }
@@ -1515,7 +1543,7 @@ int launch_backward(const BackwardArgs& a) {
     if (keyq_eligible(a.n, a.T, D, kOperandPrec<CT>)) {
       // one key pass forms dv, dk_main and the dq partials; the reduction
       // finishes dq and writes the (ghat q)^T tiles of the dk correction
-      __bf16* dqp = reinterpret_cast<__bf16*>(ws + w.dqp);
+      KqPart* dqp = reinterpret_cast<KqPart*>(ws + w.dqp);
       float* ghp = reinterpret_cast<float*>(ws + w.ghp);
       const int64_t ntiles = keyq_tiles(a.T);
       P.kgroups = static_cast<int>(keyq_groups(a.T));

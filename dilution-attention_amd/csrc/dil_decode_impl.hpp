@@ -44,7 +44,9 @@ constexpr int kDecUnroll = 2;          // cached rows in flight per lane
 // HBM speed, and a small batch x context would leave CUs idle.  At least 256
 // keys.  The rule is computed alike on the host and, for a length held in
 // device memory, by the kernels, so both give the same chunks (and the same
-// bits) at the same live length.
+// bits) at the same live length.  kDecResident is MI355X's figure (256 CUs x
+// 2 workgroups); on a part with another CU count the rule still gives correct
+// results, only the last round may then be partly filled.
 constexpr int64_t kDecResident = 512;
 constexpr int64_t kDecMaxChunk = 2048;
 constexpr int64_t kDecMinChunk = 256;

@@ -10,7 +10,10 @@
 //   * The array's device address is looked up once per device, on the entry
 //     point's first call with that device current (hipGetSymbolAddress), and
 //     only that address is handed to the kernels: in host code the symbol
-//     itself is a host-side stand-in, not a device address.
+//     itself is a host-side stand-in, not a device address.  The address is
+//     kept for the process; hipDeviceReset() reloads the module and
+//     invalidates it, so the entry point is not for use on a device after a
+//     reset.
 //   * The decode kernels overwrite every scratch word they later read (the
 //     affinities of keys [0, length), the statistics and partials of every
 //     chunk), so nothing is cleared between calls and a call never sees the

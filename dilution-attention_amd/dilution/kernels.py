@@ -49,6 +49,18 @@ _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 _PRODUCTION = (0, 1, 1.0)
 _PRECISIONS = {"ieee": 0, "tf32": 1, "bf16": 2}
 _HEAD_DIMS = (16, 32, 64, 128)
+# The head widths the gfx950 kernels are built for.  The reference's model
+# routes every power of two >= 16 to its kernels (model.py:158-165); at 256 and
+# above this build's register-resident tiles (per wave, the dk and dv
+# accumulators alone are 256 fp32 registers per lane at head_dim 256) do not
+# fit, so a caller narrows its routing with head_dim_supported() and keeps its
+# eager path for wider heads.
+SUPPORTED_HEAD_DIMS = _HEAD_DIMS
+
+
+def head_dim_supported(head_dim: int) -> bool:
+    """Whether the HIP kernels take this head width (16, 32, 64 or 128)."""
+    return int(head_dim) in _HEAD_DIMS
 
 
 def dilution_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -114,7 +126,8 @@ def _check_head_dim(head_dim: int) -> None:
     if head_dim & (head_dim - 1):
         raise ValueError("head_dim must be a power of two")
     if head_dim not in _HEAD_DIMS:
-        raise ValueError(f"head_dim must be one of {_HEAD_DIMS} on the gfx950 kernels")
+        raise ValueError(f"head_dim must be one of {_HEAD_DIMS} on the gfx950 kernels "
+                         f"(head_dim_supported(); got {head_dim})")
 
 
 def _common_dtype(*ts: torch.Tensor) -> torch.dtype:

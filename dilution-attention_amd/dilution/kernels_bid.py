@@ -37,6 +37,11 @@ VARIANT_HEAD_DIMS = (16, 32, 64, 128)
 """head dims the ablation variants are built for (those of the production operator)."""
 
 
+def head_dim_supported(head_dim: int) -> bool:
+    """Whether the variant kernels take this head width (16, 32, 64 or 128)."""
+    return int(head_dim) in VARIANT_HEAD_DIMS
+
+
 def _bid_code(bid: str) -> int:
     if bid not in BID_TYPES:
         raise ValueError(f"bid must be one of {BID_TYPES}")

@@ -65,12 +65,29 @@ def rows_linear(x: torch.Tensor, w1: torch.Tensor, mode: int, *, w2: torch.Tenso
     silu(r W1^T) * (r W2^T) with r = rmsnorm(x; g, eps), rounded to bf16 where
     the separate torch ops round.  (No reference counterpart: the reference
     model runs these through torch.nn.Linear, model.py:41-93.)"""
-    lib = _hip.lib()
+    if x.dim() != 2 or w1.dim() != 2:
+        raise ValueError("rows_linear takes x (rows, K) and a weight (N, K)")
     rows, k = x.shape
     n = w1.shape[0]
     for t in (x, w1, w2, g, resid):
         if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != x.device):
             raise ValueError("rows_linear takes contiguous bf16 tensors on one device")
+    # the kernel indexes every operand with the rows, N and K given here
+    if w1.shape[1] != k:
+        raise ValueError(f"rows_linear: weight {tuple(w1.shape)} does not match x {tuple(x.shape)}")
+    if w2 is not None and w2.shape != w1.shape:
+        raise ValueError(f"rows_linear: w2 {tuple(w2.shape)} must have w1's shape {tuple(w1.shape)}")
+    if g is not None and g.shape != (k,):
+        raise ValueError(f"rows_linear: the norm weight must have shape ({k},), got {tuple(g.shape)}")
+    if resid is not None and resid.shape != (rows, n):
+        raise ValueError(f"rows_linear: resid must have shape ({rows}, {n}), got {tuple(resid.shape)}")
+    if mode in (_LIN_NORM, _LIN_SWIGLU) and g is None:
+        raise ValueError("rows_linear: the normed modes need the norm weight g")
+    if mode == _LIN_SWIGLU and w2 is None:
+        raise ValueError("rows_linear: the SwiGLU mode needs w2")
+    if mode == _LIN_RESID and resid is None:
+        raise ValueError("rows_linear: the residual mode needs resid")
+    lib = _hip.lib()
     if out is None:
         out = torch.empty(rows, n, device=x.device, dtype=x.dtype)
     elif out.shape != (rows, n) or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != x.device:
@@ -93,7 +110,8 @@ def rows_linear_qkv(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor, eps: floa
     the kernel runs, as in a graph replay).  (No reference counterpart: the
     reference projects with c_attn and writes its cache as separate ops,
     model.py:41-93.)"""
-    lib = _hip.lib()
+    if x.dim() != 2 or k_cache.dim() != 4:
+        raise ValueError("rows_linear_qkv takes x (B, d_model) and (B, H, capacity, D) caches")
     rows, k = x.shape
     batch, heads, capacity, head_dim = k_cache.shape
     for t in (x, w, g, k_cache, v_cache):
@@ -101,6 +119,9 @@ def rows_linear_qkv(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor, eps: floa
             raise ValueError("rows_linear_qkv takes contiguous bf16 tensors on one device")
     if batch != rows or v_cache.shape != k_cache.shape or w.shape != (3 * heads * head_dim, k):
         raise ValueError("rows_linear_qkv: x, w and the caches disagree in shape")
+    if g.shape != (k,):
+        raise ValueError(f"rows_linear_qkv: the norm weight must have shape ({k},), got {tuple(g.shape)}")
+    lib = _hip.lib()
     q = torch.empty(rows, heads * head_dim, device=x.device, dtype=x.dtype)
     if torch.is_tensor(pos):
         if pos.dtype != torch.int64 or pos.numel() != 1 or pos.device != x.device:
@@ -451,7 +472,7 @@ class DilutionLM(nn.Module):
             raise ValueError(f"vocab_limit must be in (0, {self.cfg.vocab_size}]")
         logits, caches = self.prefill(idx, capacity=idx.shape[1] + max_new_tokens)
         tokens = idx
-        if graph and not (temperature and temperature > 0.0) and self.graph_decode_eligible():
+        if graph and max_new_tokens > 0 and not (temperature and temperature > 0.0) and self.graph_decode_eligible():
             last = logits[:, -1, :].float()
             if vocab_limit is not None:
                 last[:, vocab_limit:] = float("-inf")
@@ -526,8 +547,8 @@ class GraphDecoder:
         self.mask = None
         self.limit = model.cfg.vocab_size if vocab_limit is None else int(vocab_limit)
         if vocab_limit is not None:
-            self.mask = torch.zeros(model.cfg.vocab_size, device=dev)
-            self.mask[vocab_limit:] = float("-inf")
+            self.mask = torch.zeros(model.cfg.vocab_size, dtype=torch.bool, device=dev)
+            self.mask[vocab_limit:] = True          # positions that never win (NaN included)
         self.fused = fused and model.fused_decode_eligible(self.batch)
         self.graph = None
 
@@ -568,7 +589,7 @@ class GraphDecoder:
             self.logits.copy_(logits)
             last = logits[:, -1, :].float()
             if self.mask is not None:
-                last = last + self.mask
+                last = last.masked_fill(self.mask, float("-inf"))
             self.tok.copy_(last.argmax(dim=-1, keepdim=True))
         self.pos.add_(1)
         self.live.add_(1)

@@ -166,7 +166,10 @@ int dil_decode_step_dlen(const void* q1, const void* k_cache, const void* v_cach
  * dil_decode_workspace_bytes(n, length, head_dim) > DIL_NOALLOC_SCRATCH_BYTES
  * (about n * length <= 16.7M at head_dim 64), returns -7 before any launch.
  * No allocation of any kind is made.  All calls on one GPU share its array:
- * calls that overlap on one GPU (two streams, two host threads) race.
+ * calls that overlap on one GPU (two streams, two host threads) race.  The
+ * array's device address is looked up on the first call per device and kept
+ * for the process: a hipDeviceReset() invalidates it, so a process that
+ * resets a device must not call this entry point on that device afterwards.
  */
 #define DIL_NOALLOC_SCRATCH_BYTES (64LL << 20)
 int dil_decode_step_noalloc(const void* q1, const void* k_cache, const void* v_cache,

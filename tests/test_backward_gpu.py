@@ -2,8 +2,10 @@
 
 Reference patterns: tests/test_kernels.py:109-127 (dq/dk/dv vs autograd
 through the reference), :170-177 (finite grads), :180-202 (bf16 operands).
-Tolerances are the north-star ones: fp32 mode <= 1e-4 max-abs; bf16 mode
-<= 5e-2 max-abs against the fp32 oracle on the bf16-rounded inputs.
+Tolerances: fp32 mode <= 1e-4 max-abs (north star); bf16 mode <= 5e-2
+max-abs (north star) against the fp64 oracle on the bf16-rounded inputs, and
+also within 1e-2 of the largest gradient with a mean error within 1e-2 of the
+mean gradient.
 """
 
 from __future__ import annotations
@@ -15,6 +17,19 @@ from gpu_helpers import max_abs, needs_gpu
 from oracle import dilution_oracle as orc
 
 pytestmark = [pytest.mark.gpu, needs_gpu]
+
+
+def _check_bf16(name, g, want):
+    """A bf16-operand gradient against the fp64 oracle: the north-star 5e-2
+    max-abs bound, within 1e-2 of the largest gradient, and a mean error
+    within 1e-2 of the mean gradient (the measured errors are printed)."""
+    w = torch.as_tensor(want).double()
+    e = (g.double().cpu() - w).abs()
+    err, wmax, merr, wmean = e.max().item(), w.abs().max().item(), e.mean().item(), w.abs().mean().item()
+    print(f"{name}: max-abs {err:.3e} rel-to-max {err / wmax:.3e} mean-rel {merr / wmean:.3e}")
+    assert err < 5e-2, f"{name} bf16 max abs err {err}"
+    assert err < 1e-2 * wmax, f"{name} err {err} above 1e-2 of the largest gradient {wmax}"
+    assert merr < 1e-2 * wmean, f"{name} mean err {merr} vs mean gradient {wmean}"
 
 
 def _run(q, k, v, do, prec):
@@ -62,8 +77,7 @@ def test_backward_bf16_matches_oracle(seq):
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert g.dtype == torch.bfloat16
         assert torch.isfinite(g.float()).all(), name
-        err = max_abs(g, torch.from_numpy(w))
-        assert err < 5e-2, f"{name} bf16 max abs err {err}"
+        _check_bf16(name, g, w)
 
 
 @pytest.mark.parametrize("head_dim", [16, 32, 128])
@@ -76,8 +90,7 @@ def test_backward_bf16_head_dims(head_dim):
     assert max_abs(out, orc.attention_f64(q, k, v)) < 2e-2
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert g.dtype == torch.bfloat16
-        err = max_abs(g, torch.from_numpy(w))
-        assert err < 5e-2, f"{name} bf16 max abs err {err}"
+        _check_bf16(name, g, w)
 
 
 @pytest.mark.parametrize("seq", [4096, 4097])
@@ -90,8 +103,7 @@ def test_backward_bf16_long_rows(seq):
     want, _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert torch.isfinite(g.float()).all(), name
-        err = max_abs(g, torch.from_numpy(w))
-        assert err < 5e-2, f"{name} bf16 max abs err {err}"
+        _check_bf16(name, g, w)
 
 
 def test_backward_fp32_dout_with_bf16_inputs():
@@ -103,7 +115,7 @@ def test_backward_fp32_dout_with_bf16_inputs():
     want, _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (qb, kb, vb)), do.double().numpy())
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert g.dtype == torch.bfloat16
-        assert max_abs(g, torch.from_numpy(w)) < 5e-2, name
+        _check_bf16(name, g, w)
 
 
 def test_backward_finite_and_shift_invariant():
@@ -147,5 +159,4 @@ def test_backward_converted_operands_match_oracle(dtype, head_dim):
     assert max_abs(out, orc.attention_f64(q, k, v)) < 5e-2
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert g.dtype == dtype, name
-        err = max_abs(g, torch.from_numpy(w))
-        assert err < 5e-2, f"{name} max abs err {err}"
+        _check_bf16(name, g, w)

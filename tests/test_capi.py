@@ -256,3 +256,28 @@ def test_tensors_on_two_devices_are_rejected():
         kernels._check_device(on(0), on(1), on(0))
     with pytest.raises(RuntimeError):
         kernels._check_device(on(0), torch.zeros(1))
+
+
+def test_head_dims_beyond_128_are_rejected_before_any_launch():
+    """The reference's model routes every power-of-two head_dim >= 16 to its
+    kernels (model.py:158-165).  The gfx950 kernels take 16-128;
+    head_dim_supported() is the predicate a caller narrows its routing with,
+    and wider heads raise ValueError on the host from every entry point (the
+    reference model then keeps its eager path for them, model.py:182-257)."""
+    import torch
+    from dilution import kernels
+
+    assert kernels.SUPPORTED_HEAD_DIMS == (16, 32, 64, 128)
+    assert all(kernels.head_dim_supported(d) for d in (16, 32, 64, 128))
+    assert not any(kernels.head_dim_supported(d) for d in (8, 48, 256, 512))
+    for d in (256, 512, 8):
+        x = torch.zeros(1, 2, 4, d)
+        with pytest.raises(ValueError, match="head_dim"):
+            kernels.dilution_attention_forward(x, x, x)
+        with pytest.raises(ValueError, match="head_dim"):
+            kernels.dilution_attention(x, x, x)
+        kc, com = torch.zeros(1, 2, 8, d), torch.zeros(1, 2, 8)
+        with pytest.raises(ValueError, match="head_dim"):
+            kernels.dilution_decode_step(torch.zeros(1, 2, 1, d), kc, kc, com, 4)
+        with pytest.raises(ValueError, match="head_dim"):
+            kernels.dilution_prefill_chunk(x, kc, kc, com, 0)

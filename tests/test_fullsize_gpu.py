@@ -7,8 +7,10 @@ every slice.
   - output rows of slices 0 and 15 against ``attention_blocked_f64`` on the
     bf16-rounded inputs (2e-2 max-abs, 1e-2 mean-rel: the bf16 bounds);
   - dq, dk, dv of slices 0 and 15 against the row-blocked fp64 backward
-    ``grads_blocked_f64`` on the host (5e-2 max-abs), and of all 16 slices
-    against the same function evaluated in float64 on the device;
+    ``grads_blocked_f64`` on the host, and of all 16 slices against the same
+    function evaluated in float64 on the device: 5e-2 max-abs (the north-star
+    bound), 1e-2 of the largest gradient, and a mean error within 1e-2 of the
+    mean gradient (every bf16 gradient check in this file);
   - the first 4096 rows are bit-identical to the forward of the 4096-token
     prefix (causality, test_model.py:46-56);
   - rows of the attention matrix sum to one, so sum_j dv_j = sum_i dO_i.  The
@@ -68,10 +70,36 @@ def _grads_oracle(q, k, v, do, sl, device, block=1024):
     return orc.grads_blocked_f64(*args, block=block)
 
 
-def _check_grads(got, want, tol, where):
+# bf16-operand gradients: besides the north-star 5e-2 max-abs bound, the
+# largest error within 1e-2 of the largest gradient (the bound the ablation
+# tests hold the same one-pass kernel to) and the mean error within 1e-2 of
+# the mean gradient.  At C3 the mean |dq| is 0.029 and the largest 0.59, so a
+# systematic error of a few percent of a typical gradient fails the mean
+# bound.  Measured on MI355X: rel-to-max <= 7.6e-3 and mean-rel <= 3.3e-3 over
+# C3, C2 and T = 131072.
+BF16_REL_MAX = 1e-2
+BF16_MEAN_REL = 1e-2
+
+
+def _check_grads(got, want, tol, where, rel=None, mean_rel_tol=None):
+    """max-abs error of dq, dk, dv below `tol`; with `rel`, also below `rel`
+    times the largest |gradient|; with `mean_rel_tol`, the mean |error| below
+    that fraction of the mean |gradient|.  The measured errors are printed."""
     for name, g, w in zip(("dq", "dk", "dv"), got, want):
-        err = (g.double().cpu() - w.cpu()).abs().max().item()
+        e = (g.double() - w.to(g.device)).abs()
+        err, wmax = e.max().item(), w.abs().max().item()
+        merr, wmean = e.mean().item(), w.abs().mean().item()
+        print(f"{where} {name}: max-abs {err:.3e} rel-to-max {err / wmax:.3e} "
+              f"mean-rel {merr / wmean:.3e}")
         assert err < tol, f"{where} {name} max abs err {err}"
+        if rel is not None:
+            assert err < rel * wmax, f"{where} {name} err {err} above {rel} of the largest gradient {wmax}"
+        if mean_rel_tol is not None:
+            assert merr < mean_rel_tol * wmean, f"{where} {name} mean err {merr} vs mean gradient {wmean}"
+
+
+def _check_bf16_grads(got, want, where):
+    _check_grads(got, want, 5e-2, where, rel=BF16_REL_MAX, mean_rel_tol=BF16_MEAN_REL)
 
 
 def test_c3_training_bf16_full_size():
@@ -101,10 +129,10 @@ def test_c3_training_bf16_full_size():
     grads = [x.grad for x in xs]
     for h in range(16):
         want, inter = _grads_oracle(q, k, v, do, (0, h), "cuda")
-        _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (device oracle)")
+        _check_bf16_grads([g[0, h] for g in grads], want, f"slice {h} (device oracle)")
     for h in (0, 15):
         want, _ = _grads_oracle(q, k, v, do, (0, h), "cpu")
-        _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (host oracle)")
+        _check_bf16_grads([g[0, h] for g in grads], want, f"slice {h} (host oracle)")
 
 
 def test_c3_key_pass_full_size(monkeypatch):
@@ -140,7 +168,7 @@ def test_c3_key_pass_full_size(monkeypatch):
     grads = [x.grad for x in xs]
     for h in (0, 15):
         want, _ = _grads_oracle(q, k, v, do, (0, h), "cuda")
-        _check_grads([g[0, h] for g in grads], want, 5e-2, f"slice {h} (device oracle, key pass)")
+        _check_bf16_grads([g[0, h] for g in grads], want, f"slice {h} (device oracle, key pass)")
 
 
 def test_c3_training_fp32_full_size():
@@ -206,13 +234,13 @@ def test_c2_training_bf16_every_slice():
             want, inter = _grads_oracle(q, k, v, do, (b, h), "cuda", block=512)
             assert max_abs(out[b, h], inter["out"]) < 2e-2, (b, h)
             assert mean_rel(out[b, h], inter["out"]) < 1e-2, (b, h)
-            _check_grads([g[b, h] for g in grads], want, 5e-2, f"slice {(b, h)}")
+            _check_bf16_grads([g[b, h] for g in grads], want, f"slice {(b, h)}")
             worst = max(worst, max((g[b, h].double().cpu() - w.cpu()).abs().max().item()
                                    for g, w in zip(grads, want)))
     for sl in ((0, 0), (3, 7), (5, 2), (7, 15)):
         want, inter = _grads_oracle(q, k, v, do, sl, "cpu", block=512)
         assert max_abs(out[sl], inter["out"]) < 2e-2, sl
-        _check_grads([g[sl] for g in grads], want, 5e-2, f"slice {sl} (host oracle)")
+        _check_bf16_grads([g[sl] for g in grads], want, f"slice {sl} (host oracle)")
     print(f"C2 worst gradient error {worst:.3e}")
 
 
@@ -310,8 +338,8 @@ def test_sequence_of_131072_gradients_against_blocked_oracle():
     assert max_abs(out[0, 0], inter["out"]) < 2e-2
     assert mean_rel(out[0, 0], inter["out"]) < 1e-2
     mid = slice(seq // 2 - 2048, seq // 2 + 2048)
-    _check_grads([g[mid] for g in grads], [w[mid] for w in want], 5e-2, "middle rows / keys")
-    _check_grads(grads, want, 5e-2, "all rows / keys")
+    _check_bf16_grads([g[mid] for g in grads], [w[mid] for w in want], "middle rows / keys")
+    _check_bf16_grads(grads, want, "all rows / keys")
 
 
 def test_sequence_of_131072_far_end_closed_forms():

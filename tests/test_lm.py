@@ -35,6 +35,38 @@ def _small(dtype=torch.float32, chunk=16, kinds=None, **variant):
     return DilutionLM(cfg).to(device="cuda", dtype=dtype).eval()
 
 
+def test_rows_linear_rejects_mismatched_shapes():
+    """The few-row projections check every operand's shape before a launch:
+    the kernel indexes them with the rows, N and K of x and w1, so a
+    mismatched weight, norm weight or residual raises ValueError on the host
+    (CPU tensors: the checks run before the library is touched)."""
+    from dilution.lm import rows_linear, rows_linear_qkv
+
+    bf = torch.bfloat16
+    x = torch.zeros(4, 256, dtype=bf)
+    w = torch.zeros(512, 256, dtype=bf)
+    g = torch.ones(256, dtype=bf)
+    bad = [
+        dict(w1=torch.zeros(512, 128, dtype=bf), mode=0),                          # K mismatch
+        dict(w1=w, mode=3, w2=torch.zeros(256, 256, dtype=bf), g=g),              # w2 shape
+        dict(w1=w, mode=2, g=torch.ones(128, dtype=bf)),                           # norm weight
+        dict(w1=w, mode=1, resid=torch.zeros(4, 256, dtype=bf)),                   # resid shape
+        dict(w1=w, mode=2),                                                        # no norm weight
+        dict(w1=w, mode=3, g=g),                                                   # no w2
+        dict(w1=w, mode=1),                                                        # no resid
+        dict(w1=torch.zeros(512, 256, dtype=torch.float32), mode=0),               # dtype
+    ]
+    for kw in bad:
+        w1, mode = kw.pop("w1"), kw.pop("mode")
+        with pytest.raises(ValueError):
+            rows_linear(x, w1, mode, **kw)
+    kc = torch.zeros(4, 2, 32, 128, dtype=bf)
+    with pytest.raises(ValueError):                                                # norm weight
+        rows_linear_qkv(x, torch.zeros(768, 256, dtype=bf), torch.ones(255, dtype=bf), 1e-5, kc, kc.clone(), 0)
+    with pytest.raises(ValueError):                                                # c_attn shape
+        rows_linear_qkv(x, torch.zeros(512, 256, dtype=bf), g, 1e-5, kc, kc.clone(), 0)
+
+
 def test_config_validation():
     from dilution.lm import LMConfig
 
@@ -252,6 +284,11 @@ def test_generate_graph_matches_eager(dtype):
     mixed = _small(kinds=["softmax", "dilution"])   # not eligible: the eager steps run
     assert not mixed.graph_decode_eligible()
     assert torch.equal(mixed.generate(idx, 6, graph=True), mixed.generate(idx, 6))
+    # no new token returns the prompt, one new token the prefill's pick, on both paths
+    for new in (0, 1):
+        got, want = model.generate(idx, new, graph=True), model.generate(idx, new)
+        assert got.shape == want.shape == (2, 5 + new)
+        assert torch.equal(got, want)
 
 
 @pytest.mark.gpu
@@ -393,3 +430,57 @@ def test_c5_training_step_full_size():
     assert abs(loss.item() - math.log(cfg.vocab_size)) < 1.0, loss.item()
     for name, p in model.named_parameters():
         assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name
+
+
+@pytest.mark.gpu
+@needs_gpu
+def test_c5_inference_leg_full_size():
+    """BASELINE config 5's inference leg at size: the 12-layer d1024 bf16 LM
+    prefills a 16384-token prompt at B8 (2048-token chunks), then takes 512
+    greedy tokens eagerly (model.decode_step + the device argmax, as
+    generate() runs it) and through GraphDecoder's replayed steps from a copy
+    of the same caches.  The two token streams are equal, every logit is
+    finite, and after the last step every layer's demand vector sums to the
+    context length (each row's bids sum to one; model.py:198-257, the
+    generate loop of model.py:473-509)."""
+    from dilution.lm import DilutionLM, GraphDecoder, LMConfig, rows_argmax
+
+    cfg = LMConfig()
+    torch.manual_seed(0)
+    model = DilutionLM(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
+    assert model.fused_decode_eligible(8) and model.graph_decode_eligible()
+    g = torch.Generator(device="cuda").manual_seed(17)
+    prompt, new = 16384, 512
+    idx = torch.randint(0, cfg.vocab_size, (8, prompt), device="cuda", generator=g)
+    with torch.no_grad():
+        logits, caches_e = model.prefill(idx, capacity=prompt + new)
+    assert torch.isfinite(logits.float()).all()
+    caches_g = [{key: (val.clone() if torch.is_tensor(val) else val) for key, val in c.items()}
+                for c in caches_e]
+    first = rows_argmax(logits[:, -1, :])
+    finite = torch.ones((), dtype=torch.bool, device="cuda")
+    eager = [first]
+    nxt = first
+    with torch.no_grad():
+        for _ in range(new - 1):
+            step_logits = model.decode_step(nxt, caches_e)
+            finite &= torch.isfinite(step_logits.float()).all()
+            nxt = rows_argmax(step_logits[:, -1, :])
+            eager.append(nxt)
+    dec = GraphDecoder(model, caches_g, first)
+    replayed = [first]
+    for _ in range(new - 1):
+        replayed.append(dec.step().clone())
+        finite &= torch.isfinite(dec.logits.float()).all()
+    torch.cuda.synchronize()
+    assert bool(finite)
+    eager, replayed = torch.cat(eager, dim=1), torch.cat(replayed, dim=1)
+    assert eager.shape == (8, new)
+    assert torch.equal(eager, replayed)
+    length = prompt + new - 1
+    for i, (ce, cg) in enumerate(zip(caches_e, caches_g)):
+        assert ce["len"] == cg["len"] == length, i
+        for c in (ce, cg):
+            sums = c["committed"][..., :length].double().sum(-1)
+            assert (sums - length).abs().max().item() < 1e-5 * length, (i, sums)
+            assert torch.equal(c["committed"][..., length:], torch.zeros_like(c["committed"][..., length:]))
