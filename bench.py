@@ -734,63 +734,120 @@ def bench_train2k(args, dev):
     return res
 
 
-def cpu_baseline(shape):
-    """The fp32 CPU oracle, fwd+bwd through torch autograd, on one (batch,
-    head) slice of the workload (the slices are independent and identical in
-    cost), timed on this host's cores."""
+def _cpu_threads() -> int:
+    """All of this host's cores (or OMP_NUM_THREADS where it caps them)."""
     import torch
-
-    from oracle import dilution_oracle as orc
 
     threads = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
         threads = min(threads, int(env))
     torch.set_num_threads(threads)
-    _, _, seq, d = shape
-    q, k, v, do = orc.make_inputs((1, 1, seq, d), seed=2, qk_scale=0.5, with_dout=True,
-                                  dtype=torch.bfloat16)
-    xs = [t.float().requires_grad_(True) for t in (q, k, v)]
-    t0 = time.perf_counter()
-    out = orc.attention_fp32(*xs)
-    out.backward(do.float())
-    dt = time.perf_counter() - t0
-    flops = 7.0 * seq * seq * d
-    log(f"cpu baseline: one slice T={seq} fwd+bwd in {dt:.2f} s on {threads} threads")
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-            "cpu_model": cpu_model(), "kind": "port", "seconds": round(dt, 2),
-            "sample": f"fp32 torch-eager oracle fwd+bwd on 1 of {shape[0] * shape[1]} (batch, head) "
-                      f"slices, T={seq} d={d}"}
+    return threads
 
 
-def cpu_decode_baseline(context, d, slices=16):
-    """The CPU oracle's decode step (torch eager, float32) on `slices` of the
-    decode workload's (batch, head) slices at its context, caches converted
-    to float32 before the timed region; reported in the GPU figure's
-    algorithmic bytes, (4d + 8) per key per slice."""
+def _cpu_median(fn, runs: int = 3, warmup=None):
+    """Median seconds of `runs` calls of fn after one warm-up call (of
+    `warmup` when given, else of fn)."""
+    import statistics
+
+    (warmup or fn)()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def cpu_baseline(shape):
+    """The fp32 CPU oracle (torch eager, the reference's formula) on this
+    host's cores, each row the median of 3 runs after one warm-up, in the
+    GPU rows' algorithmic FLOPs: the headline workload's fwd+bwd on one of
+    its (batch, head) slices (the slices are independent and identical in
+    cost), beside C1's whole forward (B1 H4 T512 fp32), one C2 slice fwd+bwd
+    (T 2048) and one C3 slice forward (T 16384)."""
     import torch
 
     from oracle import dilution_oracle as orc
 
-    threads = torch.get_num_threads()
-    g = torch.Generator().manual_seed(7)
-    kc = torch.randn(1, slices, context, d, generator=g).to(torch.bfloat16).float()
-    vc = torch.randn(1, slices, context, d, generator=g).to(torch.bfloat16).float()
-    q1 = torch.randn(1, slices, 1, d, generator=g).to(torch.bfloat16).float()
-    com = torch.rand(1, slices, context, generator=g) * 4.0
-    com[..., context - 1] = 0.0
-    orc.decode_step(q1, kc, vc, com, context, dtype=torch.float32)      # warm-up
-    reps = 3
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        orc.decode_step(q1, kc, vc, com, context, dtype=torch.float32)
-    dt = (time.perf_counter() - t0) / reps
-    gbs = slices * context * (4 * d + 8) / dt / 1e9
-    log(f"cpu decode baseline: {slices} slices at L={context} in {dt * 1e3:.1f} ms on {threads} threads")
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "cpu_model": cpu_model(),
-            "kind": "port", "seconds": round(dt, 4),
+    threads = _cpu_threads()
+    model = cpu_model()
+
+    def slice_inputs(seq, d, dtype=torch.bfloat16):
+        q, k, v, do = orc.make_inputs((1, 1, seq, d), seed=2, qk_scale=0.5, with_dout=True, dtype=dtype)
+        return [t.float() for t in (q, k, v)], do.float()
+
+    def fwd_bwd(xs, do):
+        leaves = [x.detach().requires_grad_(True) for x in xs]
+        orc.attention_fp32(*leaves).backward(do)
+
+    def row(name, seconds, flops, runs, sample):
+        return {"name": name, "value": round(flops / seconds / 1e12, 6), "unit": "TFLOP/s",
+                "seconds_median": round(seconds, 4), "seconds_runs": [round(t, 4) for t in runs],
+                "cores": threads, "cpu_model": model, "sample": sample}
+
+    rows = []
+    # C1: the whole B1 H4 T512 d64 fp32 forward
+    q1, k1, v1 = orc.make_inputs((1, 4, 512, 64), seed=1)
+    sec, runs = _cpu_median(lambda: orc.attention_fp32(q1, k1, v1))
+    rows.append(row("C1 forward", sec, 2.0 * 4 * 512 * 512 * 64, runs,
+                    "fp32 oracle forward, B1 H4 T512 d64 (the whole C1 workload)"))
+    # C2: one of 128 slices, fwd+bwd
+    xs2, do2 = slice_inputs(2048, 64)
+    sec, runs = _cpu_median(lambda: fwd_bwd(xs2, do2))
+    rows.append(row("C2 fwd+bwd", sec, 7.0 * 2048 * 2048 * 64, runs,
+                    "fp32 oracle fwd+bwd on 1 of the 128 (batch, head) slices of B8 H16 T2048 d64"))
+    # C3 forward, then the headline fwd+bwd on the same slice (the forward
+    # runs warm the large allocations)
+    _, _, seq, d = shape
+    xs, do = slice_inputs(seq, d)
+    sec, runs = _cpu_median(lambda: orc.attention_fp32(*xs))
+    rows.append(row("C3 forward", sec, 2.0 * seq * seq * d, runs,
+                    f"fp32 oracle forward on 1 of the {shape[0] * shape[1]} (batch, head) slices, T={seq} d={d}"))
+    sec, runs = _cpu_median(lambda: fwd_bwd(xs, do), warmup=lambda: fwd_bwd(xs2, do2))
+    head = row("C3 fwd+bwd", sec, 7.0 * seq * seq * d, runs,
+               f"fp32 oracle fwd+bwd on 1 of the {shape[0] * shape[1]} (batch, head) slices, T={seq} d={d}")
+    log(f"cpu baseline: one slice T={seq} fwd+bwd median {sec:.2f} s on {threads} threads ({model})")
+    return {"value": head["value"], "unit": "TFLOP/s", "cores": threads, "cpu_model": model, "kind": "port",
+            "seconds": head["seconds_median"], "seconds_runs": head["seconds_runs"],
+            "sample": head["sample"] + " (median of 3 runs after one warm-up)", "rows": rows}
+
+
+def cpu_decode_baseline(context, d, slices=16, sweep=(16384, 32768, 65536)):
+    """The CPU oracle's decode step (torch eager, float32) on `slices` of the
+    decode workload's (batch, head) slices, caches converted to float32 before
+    the timed region; each context the median of 3 runs after one warm-up,
+    reported in the GPU figure's algorithmic bytes, (4d + 8) per key per
+    slice: the headline context, and beside it the shorter contexts of the
+    GPU decode sweep."""
+    import torch
+
+    from oracle import dilution_oracle as orc
+
+    threads = _cpu_threads()
+    model = cpu_model()
+
+    def one(ctx):
+        g = torch.Generator().manual_seed(7)
+        kc = torch.randn(1, slices, ctx, d, generator=g).to(torch.bfloat16).float()
+        vc = torch.randn(1, slices, ctx, d, generator=g).to(torch.bfloat16).float()
+        q1 = torch.randn(1, slices, 1, d, generator=g).to(torch.bfloat16).float()
+        com = torch.rand(1, slices, ctx, generator=g) * 4.0
+        com[..., ctx - 1] = 0.0
+        sec, runs = _cpu_median(lambda: orc.decode_step(q1, kc, vc, com, ctx, dtype=torch.float32))
+        gbs = slices * ctx * (4 * d + 8) / sec / 1e9
+        return {"context": ctx, "value": round(gbs, 2), "unit": "GB/s", "seconds_median": round(sec, 5),
+                "seconds_runs": [round(t, 5) for t in runs]}
+
+    head = one(context)
+    log(f"cpu decode baseline: {slices} slices at L={context} median {head['seconds_median'] * 1e3:.1f} ms "
+        f"on {threads} threads")
+    return {"value": head["value"], "unit": "GB/s", "cores": threads, "cpu_model": model, "kind": "port",
+            "seconds": head["seconds_median"], "seconds_runs": head["seconds_runs"],
             "sample": f"fp32 torch-eager oracle decode step on {slices} (batch, head) slices at "
-                      f"L={context} d={d} (float32 copies of bf16 caches)"}
+                      f"L={context} d={d} (float32 copies of bf16 caches), median of 3 runs after one warm-up",
+            "sweep": [one(ctx) for ctx in sweep if ctx < context]}
 
 
 def main() -> int:

@@ -1,6 +1,7 @@
 // Entry points of the forward (plain forward and chunked prefill): the
 // production operator for every head_dim; the ablation variants are built in
-// dil_variants.hip (head_dim 64) and reached through forward_bid<BID>.
+// dil_variants.hip (head_dim 16, 32, 64 and 128) and reached through
+// forward_bid<BID>.
 #include "dil_forward_impl.hpp"
 
 namespace dil {

@@ -651,12 +651,14 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
   }
 }
 // ---------------------------------------------------------------------------
-// key-parallel output pass (bf16 operands, head_dim 64, a chunk that starts
-// at row 0: the training forward and a first prefill chunk)
+// key-parallel output pass (bf16 operands, head_dim 64: the training forward
+// and prefill chunks that start at a multiple of the group's keys)
 //
-// fwd_demand's walk, widened to 8 waves = 256 keys per workgroup and forming
-// the output in the same walk, so the scores, exp2 and demand scan run once
-// after the statistics instead of twice.  Per 32-row tile every wave (32
+// fwd_demand's walk, widened to KW waves = 32 KW keys per workgroup and
+// forming the output in the same walk, so the scores, exp2 and demand scan
+// run once after the statistics instead of twice.  A group's keys before the
+// chunk start from the carried demand and meet every row tile of the chunk;
+// the others start at their diagonal tile.  Per 32-row tile every wave (32
 // keys, lane <-> key, rows in the query-split layout):
 //   * p = 2^(a c - lse), masked on the diagonal tile;
 //   * the demand entering the tile is the wave's running fp64 column sum
@@ -666,26 +668,29 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
 //   * the share tile is transposed with an identity MFMA (rows in lanes) and
 //     staged in LDS as bf16; its row sums (the normaliser's partial, over the
 //     same bf16 values that multiply V) come from an all-ones operand.
-// After the next tile's stash the 8 waves form the tile's share V over the
-// group's 256 keys, one 16 x 16 output block each (v_mfma_f32_16x16x32_bf16,
-// V parked in LDS), stored as one bf16 [d][32 rows] partial per (key group,
-// tile) with the fp32 row sums beside it, compactly (keyq_tile_base).
+// After the next tile's stash 8 waves form the tile's share V over the
+// group's keys, one 16 x 16 output block each (v_mfma_f32_16x16x32_bf16, V
+// parked in LDS), stored as one bf16 [d][32 rows] partial per (key group,
+// tile) with the fp32 row sums beside it, compactly (ChunkGroups).
 // fwd_out_reduce sums the partials of every key group in a fixed order and
-// normalises.
+// normalises.  With 16 waves (512 keys) a CU holds one workgroup (148 KB of
+// LDS) and there are half the partials of 8 waves.
 
-template <int D>
-__global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16* __restrict__ op,
-                                                             float* __restrict__ rp, int64_t ntiles) {
+template <int D, int KW>
+__global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf16* __restrict__ op,
+                                                               float* __restrict__ rp, int64_t ntiles) {
   static_assert(D == 64, "the key-parallel output pass is built for head_dim 64");
+  static_assert(KW == 8 || KW == 16, "key groups of 256 or 512 keys");
   using CT = __bf16;
   using TL = Tiles<CT, D>;
+  using KG = KeyGroups<KW>;
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) float st_s[2][kTileQ];          // lse of the tile's rows
-  __shared__ __attribute__((aligned(16))) CT sh_s[2][kTileQ * kPdStride];  // shares, [row][key]
-  __shared__ float rs_s[2][kKqWaves][kTileQ];                              // row sums per wave
+  __shared__ __attribute__((aligned(16))) CT sh_s[2][kTileQ * KG::kStride];  // shares, [row][key]
+  __shared__ float rs_s[2][KW][kTileQ];                                    // row sums per wave
   // B operand of the share V product: V of the group's keys, per d quarter
   // and key step (32 keys), lane-minor
-  __shared__ __attribute__((aligned(16))) bf16x8 vpark[D / 16][kKqWaves][64];
+  __shared__ __attribute__((aligned(16))) bf16x8 vpark[D / 16][KW][64];
   __shared__ __attribute__((aligned(16))) bf16x8 id_park[2][64];          // transpose identity
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
@@ -694,12 +699,16 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const float hf = static_cast<float>(h);
   const int kg = item.idx;
-  const int kb0 = kg * kKqWaves;                 // first key tile (and first row tile) of the group
+  const int kb0 = kg * KW;                       // first key tile of the group
   const int kb = kb0 + wave;                     // key tile of this wave
-  const int64_t T = P.Tk;                        // rows = keys: the chunk starts at row 0
+  const int64_t T = P.Tk;                        // keys [0, q0 + C)
+  const int64_t C = P.C;                         // chunk rows [q0, q0 + C)
+  const int q0t = static_cast<int>(P.q0 / kTileQ);   // global row tile of chunk row tile 0
+  const ChunkGroups<KW> cg{(C + kTileQ - 1) / kTileQ, P.q0 / KG::kKeys};
+  const int nq = static_cast<int>(cg.nq);
+  const int rt0 = static_cast<int>(cg.first(kg));    // the group's first chunk row tile
   const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
   const bool key_ok = key < T;
-  const int nq = static_cast<int>((T + kTileQ - 1) / kTileQ);
   const bool active = static_cast<int64_t>(kb) * kTileK < T;
 
   const CT* qs = static_cast<const CT*>(P.q) + slice * P.q_sn;
@@ -724,7 +733,10 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
       for (int s = 0; s < 2; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
     }
   }
-  double run = 0.0;                              // demand entering the current tile (this lane's key)
+  // demand entering the current tile (this lane's key): the carried demand of
+  // the rows before the chunk for its earlier keys
+  double run = (P.demand_in != nullptr && key < P.q0 && key_ok)
+                   ? static_cast<double>(P.demand_in[slice * P.din_sn + key]) : 0.0;
   float* ccol = P.carry + slice * P.nb * T + min(key, T - 1);
 
   // staging: threads 0-255 one 16-byte chunk of the Q row tile; threads 0-31
@@ -735,15 +747,15 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
   float lz = 0.f;
   const float* rmax = P.rmax + slice * P.C;
   const float* rden = P.rden + slice * P.C;
-  auto fetch = [&](int qt) {
-    const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
-    const int64_t rows = min(max(T - row0, int64_t{0}), int64_t{kTileQ});
+  auto fetch = [&](int rt) {
+    const int64_t row0 = static_cast<int64_t>(rt) * kTileQ;
+    const int64_t rows = min(max(C - row0, int64_t{0}), int64_t{kTileQ});
     if (stager)
       rr = buffer_load16<bf16x8>(make_rsrc(qs + row0 * D, rows * D * static_cast<int64_t>(sizeof(CT))),
                                  static_cast<uint32_t>(c256 * 16), 0);
     if (threadIdx.x < kTileQ) {
       const int64_t r = row0 + threadIdx.x;
-      lz = r < T ? rmax[r] + __log2f(rden[r]) : INFINITY;
+      lz = r < C ? rmax[r] + __log2f(rden[r]) : INFINITY;
     }
   };
   auto stash = [&](int buf) {
@@ -759,7 +771,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
   // transposed tile: fragment s of half h holds keys acc_row(8 s + t, h), two
   // runs of 4 consecutive keys (16 s + 4 h, 16 s + 8 + 4 h)
   auto stage_sh = [&](int buf, const bf16x8 (&xf)[2]) {
-    CT* dst = sh_s[buf] + l32 * kPdStride + wave * kTileK + 4 * h;
+    CT* dst = sh_s[buf] + l32 * KG::kStride + wave * kTileK + 4 * h;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const bf16x4 lo = {xf[s][0], xf[s][1], xf[s][2], xf[s][3]};
@@ -768,7 +780,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
       *reinterpret_cast<bf16x4*>(dst + 16 * s + 8) = hi;
     }
   };
-  auto step = [&](int buf, int qt, auto diag_tag) {
+  auto step = [&](int buf, int rt, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     RowFrag<CT, D> qf;
     lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
@@ -785,7 +797,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
         if (dk > i) p[i] = 0.f;
     }
     const float cin = static_cast<float>(run);
-    if (h == 0 && key_ok) ccol[static_cast<int64_t>(qt) * T] = cin;   // the demand entering the tile
+    if (h == 0 && key_ok) ccol[static_cast<int64_t>(rt) * T] = cin;   // the demand entering the tile
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = p[i];
     run += static_cast<double>(scan_incl_qs(x, cin + kEps, hf));      // demand + p + eps
@@ -816,62 +828,69 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
     if (h == 0) rs_s[buf][wave][l32] = 0.f;
   };
 
-  // share V of the group's 256 keys for tile qt: wave w forms rows
-  // 16 (w & 1) + [0, 16) x head dims 16 (w >> 1) + [0, 16)
-  const int rh = wave & 1, dq4 = wave >> 1;
+  // share V of the group's KW * 32 keys for tile qt, formed by the last 8
+  // waves: product wave pw forms rows 16 (pw & 1) + [0, 16) x head dims
+  // 16 (pw >> 1) + [0, 16) over all the group's keys (with 16 waves, waves
+  // 0-7 form none: each SIMD then holds two product waves and two others)
+  const int pw = wave - (KW - 8);
+  const bool prod_wave = pw >= 0;                // wave-uniform
+  const int rh = pw & 1, dq4 = (pw >> 1) & 3;
   __bf16* op_s = op + slice * ntiles * (D * kTileQ);
   float* rp_s = rp + slice * ntiles * kTileQ;
-  const int64_t gbase = keyq_tile_base(kg, nq) - static_cast<int64_t>(kKqTilesPerGroup) * kg;
-  auto product = [&](int qt, int buf) {
-    if (qt < 0) return;
+  const int64_t gbase = cg.base(kg) - rt0;
+  auto product = [&](int rt, int buf) {
+    if (rt < 0) return;
     floatx4 acc = floatx4{};
-    const CT* arow = sh_s[buf] + (16 * rh + (lane & 15)) * kPdStride + 8 * (lane >> 4);
+    const CT* arow = sh_s[buf] + (16 * rh + (lane & 15)) * KG::kStride + 8 * (lane >> 4);
 #pragma unroll
-    for (int ks = 0; ks < kKqWaves; ++ks) {
+    for (int ks = 0; ks < KW; ++ks) {
       const bf16x8 av = *reinterpret_cast<const bf16x8*>(arow + kTileK * ks);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, vpark[dq4][ks][lane], acc, 0, 0, 0);
     }
     // output: lane <-> head dim 16 dq4 + (lane & 15), register j <-> row 16 rh + 4 (lane >> 4) + j;
     // the partial tile is stored [d][32 rows], streamed past the caches
-    const int64_t tile = gbase + qt;
+    const int64_t tile = gbase + rt;
     const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
     const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
     const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
     __builtin_nontemporal_store(__builtin_bit_cast(floatx2, v),
                                 reinterpret_cast<floatx2*>(op_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ +
                                                            16 * rh + 4 * (lane >> 4)));
-    if (threadIdx.x < kTileQ) {
+    if (pw == 0 && lane < kTileQ) {
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < kKqWaves; ++w) s += rs_s[buf][w][threadIdx.x];
-      __builtin_nontemporal_store(s, rp_s + tile * kTileQ + threadIdx.x);
+      for (int w = 0; w < KW; ++w) s += rs_s[buf][w][lane];
+      __builtin_nontemporal_store(s, rp_s + tile * kTileQ + lane);
     }
   };
 
-  fetch(kb0);
+  fetch(rt0);
   stash(0);
   __syncthreads();
   // the product of tile qt - 1 (staged before the previous barrier, in the
   // other buffer) runs anywhere before this step's barrier, which the stage
   // of tile qt + 1 into that buffer follows.  Waves w and w + 4 share a SIMD:
-  // waves 4-7 form it before their step, waves 0-3 after their stash, so the
-  // two waves of a SIMD leave each barrier out of phase (-7% on this kernel)
+  // product waves 4-7 form it before their step, 0-3 after their stash, so
+  // the product waves of a SIMD leave each barrier out of phase (-7% on this
+  // kernel at 8 waves)
+  const bool early = prod_wave && pw >= 4, late = prod_wave && pw < 4;   // wave-uniform
   auto iter = [&](int j, int buf) __attribute__((always_inline)) {
-    const int qt = kb0 + j;                      // query tiles in causal order
-    fetch(min(qt + 1, nq - 1));                  // the last step reloads its own tile, unused
-    if (threadIdx.x >= 256) product(j > 0 ? qt - 1 : -1, buf ^ 1);
-    if (active && qt >= kb) {
-      if (qt > kb) step(buf, qt, std::false_type{});
-      else step(buf, qt, std::true_type{});
+    const int rt = rt0 + j;                      // chunk row tiles in causal order
+    const int grt = q0t + rt;                    // its global row tile (diagonal: grt == kb)
+    fetch(min(rt + 1, nq - 1));                  // the last step reloads its own tile, unused
+    if (early) product(j > 0 ? rt - 1 : -1, buf ^ 1);
+    if (active && grt >= kb) {
+      if (grt > kb) step(buf, rt, std::false_type{});
+      else step(buf, rt, std::true_type{});
     } else {
       stage_zero(buf);
     }
     stash(buf ^ 1);
-    if (threadIdx.x < 256) product(j > 0 ? qt - 1 : -1, buf ^ 1);
+    if (late) product(j > 0 ? rt - 1 : -1, buf ^ 1);
     sync_lds();
   };
-  double_buffered<true>(0, nq - kb0, iter);      // unrolled by two: buffer offsets fold into the LDS instructions
-  product(nq - 1, (nq - kb0 - 1) & 1);          // the last tile, staged before the final barrier
+  double_buffered<true>(0, nq - rt0, iter);      // unrolled by two: buffer offsets fold into the LDS instructions
+  if (prod_wave) product(nq - 1, (nq - rt0 - 1) & 1);   // the last tile, staged before the final barrier
   if (h == 0 && key_ok) P.total[slice * P.tot_sn + key] = static_cast<float>(run);
 }
 
@@ -880,21 +899,24 @@ __global__ __launch_bounds__(kKqThreads, 2) void fwd_keyout(FwdParams P, __bf16*
 // ssum.  Grid: (query tiles, slices from slice0), the tiles with the most key
 // groups first.  Thread t sums elements [8 t, 8 t + 8) of the [d][32 rows]
 // partial tiles.
-template <int D>
+template <int D, int KW>
 __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restrict__ op,
                                                            const float* __restrict__ rp, int64_t ntiles,
-                                                           int64_t T, float* __restrict__ out, int64_t o_sn,
-                                                           float* __restrict__ ssum, int64_t slice0) {
+                                                           int64_t T, int64_t Tk, float* __restrict__ out,
+                                                           int64_t o_sn, float* __restrict__ ssum, int64_t slice0) {
+  // T: the chunk's rows; Tk: keys (the chunk starts at row Tk - T)
   static_assert(D * kTileQ == 8 * kThreads, "one 16-byte chunk of the partial tile per thread");
   __shared__ float sum_s[D][kTileQ + 1];
   __shared__ float s_s[kTileQ];
   const int64_t slice = slice0 + blockIdx.y;
-  const int nq = static_cast<int>((T + kTileQ - 1) / kTileQ);
+  using KG = KeyGroups<KW>;
+  const ChunkGroups<KW> cg{(T + kTileQ - 1) / kTileQ, (Tk - T) / KG::kKeys};
+  const int nq = static_cast<int>(cg.nq);
   const int tq = nq - 1 - static_cast<int>(blockIdx.x);
-  const int ng = min(static_cast<int>(keyq_groups(T)) - 1, tq / kKqTilesPerGroup) + 1;
+  const int ng = static_cast<int>(min(KG::groups(Tk) - 1, cg.a + tq / KW)) + 1;
   const int t = threadIdx.x;
   const __bf16* base = op + slice * ntiles * (D * kTileQ) + 8 * t;
-  auto tile_of = [&](int g) { return keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g; };
+  auto tile_of = [&](int g) { return cg.base(g) + tq - cg.first(g); };
   // groups in order, four loads in flight
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int g = 0;
@@ -953,22 +975,26 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
 // ---------------------------------------------------------------------------
 // host side
 
-// The key-parallel output pass can replace fwd_demand + fwd_out where it
-// serves (bf16, head_dim 64, production operator, a chunk starting at row 0,
-// its partials -- ~1 byte per causal score element -- within the budget).
-// Measured at C3 it is not faster: fwd_keyout 1.18 ms + fwd_out_reduce 0.26 ms
-// against fwd_demand 0.45 ms + fwd_out 0.95 ms (the reduction's read of the
-// 1.1 GB of partials outweighs the exp2 sweep it saves), so it runs only when
-// the environment sets DILUTION_FORWARD_KEY_PASS=1 (read once by each call
-// and by each size query: ForwardArgs::key_pass).
+// The key-parallel output pass replaces fwd_demand + fwd_out where it serves:
+// bf16 operands, head_dim 64, the production operator, a chunk that starts at
+// a multiple of 512 keys (the training forward, chunked prefill at such
+// starts), its partials (~0.5 byte per causal score element) within the
+// budget.  512-key groups (16 waves); DILUTION_FORWARD_KEY_PASS=0 turns it
+// off (read once by each call and by each size query: ForwardArgs::key_pass).
 constexpr int64_t kKeyoutBudgetBytes = int64_t{24} << 30;
+constexpr int kKeyoutWaves = 16;
 
-inline int64_t keyout_partial_bytes(int64_t n, int64_t T, int D) {
-  return n * keyq_tiles(T) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
+inline int64_t keyout_tiles(int64_t C, int64_t Tk) {
+  using KG = KeyGroups<kKeyoutWaves>;
+  const ChunkGroups<kKeyoutWaves> cg{(C + kTileQ - 1) / kTileQ, (Tk - C) / KG::kKeys};
+  return cg.base(KG::groups(Tk));
+}
+inline int64_t keyout_partial_bytes(int64_t n, int64_t C, int64_t Tk, int D) {
+  return n * keyout_tiles(C, Tk) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
 }
 inline bool keyout_eligible(int64_t n, int64_t C, int64_t Tk, int64_t q0, int D, int prec, bool requested) {
-  return requested && prec == 2 && D == 64 && q0 == 0 && C == Tk &&
-         keyout_partial_bytes(n, Tk, D) <= kKeyoutBudgetBytes;
+  return requested && prec == 2 && D == 64 && q0 + C == Tk && q0 % KeyGroups<kKeyoutWaves>::kKeys == 0 &&
+         keyout_partial_bytes(n, C, Tk, D) <= kKeyoutBudgetBytes;
 }
 
 struct FwdWorkspace {
@@ -988,11 +1014,11 @@ FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int 
   w.op = w.kc + (convert ? align_up(ct * n * Tk * D) : 0);
   w.rp = w.op;
   w.total = w.op;
-  // the key pass's partials, when a chunk of this shape can take it (the
-  // size query does not know the chunk's start: sized whenever C == Tk)
-  if (keyout_eligible(n, C, Tk, 0, D, prec, key_pass)) {
-    w.rp = w.op + align_up(static_cast<size_t>(n * keyq_tiles(Tk) * D * kTileQ * 2));
-    w.total = w.rp + align_up(static_cast<size_t>(n * keyq_tiles(Tk) * kTileQ * 4));
+  // the key pass's partials, when a chunk of this shape can take it (every
+  // call is a chunk of rows [Tk - C, Tk) against keys [0, Tk))
+  if (keyout_eligible(n, C, Tk, Tk - C, D, prec, key_pass)) {
+    w.rp = w.op + align_up(static_cast<size_t>(n * keyout_tiles(C, Tk) * D * kTileQ * 2));
+    w.total = w.rp + align_up(static_cast<size_t>(n * keyout_tiles(C, Tk) * kTileQ * 4));
   }
   return w;
 }
@@ -1070,15 +1096,17 @@ int launch_forward(const ForwardArgs& a) {
       // partials; the reduction finishes out and ssum
       __bf16* op = reinterpret_cast<__bf16*>(ws + w.op);
       float* rp = reinterpret_cast<float*>(ws + w.rp);
-      const int64_t ntiles = keyq_tiles(a.Tk);
-      P.kgroups = static_cast<int>(keyq_groups(a.Tk));
+      constexpr int KW = kKeyoutWaves;
+      using KG = KeyGroups<KW>;
+      const unsigned nq = static_cast<unsigned>((a.C + kTileQ - 1) / kTileQ);
+      const int64_t ntiles = keyout_tiles(a.C, a.Tk);
+      P.kgroups = static_cast<int>(KG::groups(a.Tk));
       const dim3 gko(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
-      DIL_TIMED("fwd_keyout", st, (fwd_keyout<D><<<gko, kKqThreads, 0, st>>>(P, op, rp, ntiles)));
-      const unsigned nq = static_cast<unsigned>((a.Tk + kTileQ - 1) / kTileQ);
+      DIL_TIMED("fwd_keyout", st, (fwd_keyout<D, KW><<<gko, KG::kThreads, 0, st>>>(P, op, rp, ntiles)));
       slice_batches(a.n, [&](int64_t s0, unsigned ns) {
         DIL_TIMED("fwd_out_reduce", st,
-                  (fwd_out_reduce<D><<<dim3(nq, ns), kThreads, 0, st>>>(op, rp, ntiles, a.Tk, a.out, a.o_sn,
-                                                                       a.ssum, s0)));
+                  (fwd_out_reduce<D, KW><<<dim3(nq, ns), kThreads, 0, st>>>(op, rp, ntiles, a.C, a.Tk, a.out,
+                                                                           a.o_sn, a.ssum, s0)));
       });
       return static_cast<int>(hipGetLastError());
     }

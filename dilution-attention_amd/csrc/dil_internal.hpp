@@ -114,13 +114,14 @@ struct ForwardArgs {
   void* stream;
 };
 
-// DILUTION_FORWARD_KEY_PASS=1 requests the key-parallel output pass for the
-// calls that can take it.  Each entry point reads it once and hands the
-// answer to both its workspace check and its launch, so a change of the
-// variable between the two cannot make them disagree.
+// The key-parallel output pass serves the calls that can take it unless the
+// environment sets DILUTION_FORWARD_KEY_PASS=0 (the three-pass forward for
+// every call).  Each entry point reads it once and hands the answer to both
+// its workspace check and its launch, so a change of the variable between the
+// two cannot make them disagree.
 inline bool forward_key_pass_requested() {
   const char* e = getenv("DILUTION_FORWARD_KEY_PASS");
-  return e != nullptr && e[0] == '1' && e[1] == '\0';
+  return !(e != nullptr && e[0] == '0' && e[1] == '\0');
 }
 
 int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int prec,

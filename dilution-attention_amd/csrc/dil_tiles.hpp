@@ -162,14 +162,46 @@ constexpr int kKqTilesPerGroup = kKqKeys / kTileQ;  // query tiles spanned by a 
 // 16-way); a fully conflict-free layout measured no faster
 constexpr int kPdStride = kKqKeys + 8;
 
+// The same compact indexing for key groups of KW waves (KW * 32 keys): group
+// g meets query tiles [KW g, nq), and tile (g, qt) sits at tile_base(g, nq) +
+// qt - KW g.
+template <int KW>
+struct KeyGroups {
+  static constexpr int kWaves = KW;
+  static constexpr int kThreads = 64 * KW;
+  static constexpr int kKeys = KW * kTileK;
+  static constexpr int kTilesPerGroup = kKeys / kTileQ;
+  static constexpr int kStride = kKeys + 8;            // bf16 per staged [row][key] row
+  __host__ __device__ static int64_t tile_base(int64_t g, int64_t nq) {
+    return g * nq - static_cast<int64_t>(kTilesPerGroup) * g * (g - 1) / 2;
+  }
+  __host__ __device__ static int64_t groups(int64_t T) { return (T + kKeys - 1) / kKeys; }
+  __host__ __device__ static int64_t tiles(int64_t T) {
+    const int64_t nq = (T + kTileQ - 1) / kTileQ;
+    return tile_base(groups(T), nq);
+  }
+};
+
+// Key groups of KW waves over a chunk of rows [q0, q0 + C) against keys
+// [0, q0 + C), q0 a multiple of the group's keys: the a = q0 / (32 KW) groups
+// wholly before the chunk meet every one of its nq row tiles, group g >= a
+// first meets chunk row tile KW (g - a).  Partial tile (g, rt) sits at
+// base(g) + rt - first(g); a chunk at row 0 has the indexing of KeyGroups.
+template <int KW>
+struct ChunkGroups {
+  int64_t nq;   // row tiles of the chunk
+  int64_t a;    // key groups wholly before the chunk
+  __host__ __device__ int64_t first(int64_t g) const { return g > a ? KW * (g - a) : 0; }
+  __host__ __device__ int64_t base(int64_t g) const {
+    return g <= a ? g * nq : a * nq + KeyGroups<KW>::tile_base(g - a, nq);
+  }
+};
+
 __host__ __device__ inline int64_t keyq_tile_base(int64_t g, int64_t nq) {
-  return g * nq - static_cast<int64_t>(kKqTilesPerGroup) * g * (g - 1) / 2;
+  return KeyGroups<kKqWaves>::tile_base(g, nq);
 }
-__host__ __device__ inline int64_t keyq_groups(int64_t T) { return (T + kKqKeys - 1) / kKqKeys; }
-__host__ __device__ inline int64_t keyq_tiles(int64_t T) {
-  const int64_t nq = (T + kTileQ - 1) / kTileQ;
-  return keyq_tile_base(keyq_groups(T), nq);
-}
+__host__ __device__ inline int64_t keyq_groups(int64_t T) { return KeyGroups<kKqWaves>::groups(T); }
+__host__ __device__ inline int64_t keyq_tiles(int64_t T) { return KeyGroups<kKqWaves>::tiles(T); }
 
 // 16 consecutive floats of LDS into registers (four 16-byte reads).
 __device__ __forceinline__ void lds_read16(const float* src, float (&v)[16]) {

@@ -61,33 +61,37 @@ def test_workspace_queries(lib):
 
 
 def test_key_pass_switch_sizes_the_workspace(lib, monkeypatch):
-    """DILUTION_FORWARD_KEY_PASS=1 adds the key pass's partials to the forward's
-    workspace for the calls that can take it (bf16 operands, head_dim 64, full
-    causal), and dil_forward reads the switch once for its size check and its
-    launch: a workspace sized without the switch is an error (-3) with it,
-    before any launch.  The stand-in addresses are never dereferenced."""
-    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
+    """The key-parallel output pass adds its partials to the forward's
+    workspace for the calls that can take it (bf16 operands, head_dim 64, a
+    chunk starting at a multiple of 512 rows: the full causal forward and
+    aligned prefill chunks); DILUTION_FORWARD_KEY_PASS=0 turns it off.
+    dil_forward reads the switch once for its size check and its launch: a
+    workspace sized with the pass off is an error (-3) with it on, before any
+    launch.  The stand-in addresses are never dereferenced."""
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
     off = lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 1)
-    assert lib.dil_prefill_workspace_bytes(2, 300, 0, 64, 1, 2) == lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 0)
-    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
+    off_pre = lib.dil_prefill_workspace_bytes(2, 300, 0, 64, 1, 2)
+    assert off_pre == lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 0)
+    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
     on = lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 1)
     assert on > off
-    # not eligible: fp32 operands, head_dim 32, a later prefill chunk
+    assert lib.dil_prefill_workspace_bytes(2, 300, 0, 64, 1, 2) > off_pre
+    # not eligible: fp32 operands, head_dim 32, a prefill chunk at an unaligned start
     for args in ((2, 300, 64, 1, 0, 1), (2, 300, 32, 1, 2, 1)):
-        monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
+        monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
         base = lib.dil_forward_workspace_bytes(*args)
-        monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
+        monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
         assert lib.dil_forward_workspace_bytes(*args) == base, args
-    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
-    later = lib.dil_prefill_workspace_bytes(2, 300, 300, 64, 1, 2)
-    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
-    assert lib.dil_prefill_workspace_bytes(2, 300, 300, 64, 1, 2) == later
+    for start, eligible in ((300, False), (512, True), (1536, True), (1000, False)):
+        monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
+        base = lib.dil_prefill_workspace_bytes(2, 300, start, 64, 1, 2)
+        monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
+        assert (lib.dil_prefill_workspace_bytes(2, 300, start, 64, 1, 2) > base) == eligible, start
     fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(12)]
-    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
     assert lib.dil_forward(*fake[:3], 2, 300, 64, 1, 2, *fake[3:9], fake[9], fake[10], off, None) == -3
-    # the value must be exactly "1"
-    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "10")
-    assert lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 1) == off
+    # only the exact value "0" turns it off
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "00")
+    assert lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 1) == on
 
 
 def test_argument_errors_before_any_launch(lib):

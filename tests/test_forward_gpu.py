@@ -266,9 +266,9 @@ def test_precision_argument_errors():
 
 @pytest.mark.parametrize("seq", [1, 33, 257, 1000, 2048])
 def test_forward_key_pass_matches_three_pass(seq, monkeypatch):
-    """The key-parallel output pass (fwd_keyout + fwd_out_reduce, selected by
-    DILUTION_FORWARD_KEY_PASS=1) against the default three-pass forward and
-    the oracle: bf16 outputs at the bf16 bounds, the demand checkpoints
+    """The key-parallel output pass (fwd_keyout + fwd_out_reduce, the default
+    for these calls) against the three-pass forward (DILUTION_FORWARD_KEY_PASS=0)
+    and the oracle: bf16 outputs at the bf16 bounds, the demand checkpoints
     (causal part), totals and row sums of shares within fp32 summation-order
     differences; gradients through it within the bf16 gradient bound."""
     from dilution import kernels
@@ -276,9 +276,10 @@ def test_forward_key_pass_matches_three_pass(seq, monkeypatch):
     q, k, v, do = orc.make_inputs((2, 4, seq, 64), seed=300 + seq, qk_scale=0.5, with_dout=True,
                                   dtype=torch.bfloat16)
     qg, kg, vg = (x.cuda() for x in (q, k, v))
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
     out0, aux0 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True,
                                                     _save_pk=True)
-    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
+    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS")
     out1, aux1 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True,
                                                     _save_pk=True)
     want = orc.attention_fp32(q, k, v)
@@ -300,3 +301,52 @@ def test_forward_key_pass_matches_three_pass(seq, monkeypatch):
     (dq, dk, dv), _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
     for name, g, w in zip(("dq", "dk", "dv"), (x.grad for x in xs), (dq, dk, dv)):
         assert max_abs(g, torch.from_numpy(w)) < 5e-2, name
+
+
+@pytest.mark.parametrize("chunk", [512, 1536])
+def test_prefill_chunks_through_the_key_pass(chunk, monkeypatch):
+    """Prefill chunks that start at a multiple of 512 rows run the
+    key-parallel output pass with the carried demand as its starting point
+    (keys before the chunk meet every row tile of it).  Chunk after chunk,
+    against the same chunks through the three-pass forward
+    (DILUTION_FORWARD_KEY_PASS=0) and the fp64 oracle of the whole sequence:
+    outputs within bf16 rounding (1e-2 of each other, 2e-2 of the oracle), the
+    carried demand and the causal checkpoints within fp32 summation-order
+    differences (1e-5 relative), the row sums of shares within a few bf16
+    steps; the last chunk is ragged (3100 rows)."""
+    from dilution import kernels
+
+    batch, heads, seq, d = 2, 3, 3100, 64
+    q, k, v = orc.make_inputs((batch, heads, seq, d), seed=chunk + 5, qk_scale=0.5, dtype=torch.bfloat16)
+    full = orc.attention_f64(q, k, v)
+    cap = seq + 40
+    kc = torch.zeros(batch, heads, cap, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:, :, :seq] = k.cuda()
+    vc[:, :, :seq] = v.cuda()
+    com = {m: torch.zeros(batch, heads, cap, device="cuda") for m in ("key", "three")}
+    for start in range(0, seq, chunk):
+        stop = min(start + chunk, seq)
+        res = {}
+        for mode in ("three", "key"):
+            if mode == "three":
+                monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
+            else:
+                monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
+            res[mode] = kernels.dilution_prefill_chunk(q[:, :, start:stop].cuda(), kc, vc, com[mode], start,
+                                                       dot_precision="bf16", return_aux=True)
+        (o1, a1), (o0, a0) = res["key"], res["three"]
+        assert max_abs(o1, full[:, :, start:stop]) < 2e-2, start
+        assert mean_rel(o1, full[:, :, start:stop]) < 1e-2, start
+        assert max_abs(o1, o0) < 1e-2, start
+        assert max_abs(a1["ssum"], a0["ssum"]) < 2e-2, start
+        t0, t1 = com["three"][:, :, :stop].double(), com["key"][:, :, :stop].double()
+        assert ((t1 - t0).abs() / t0.abs().clamp(min=1.0)).max().item() < 1e-5, start
+        c0 = a0["carry"].reshape(batch, heads, -1, stop).double()
+        c1 = a1["carry"].reshape(batch, heads, -1, stop).double()
+        for rb in range(c0.shape[2]):
+            end = min(start + 32 * (rb + 1), stop)
+            diff = ((c1[:, :, rb, :end] - c0[:, :, rb, :end]).abs() / c0[:, :, rb, :end].abs().clamp(min=1.0))
+            assert diff.max().item() < 1e-5, (start, rb)
+    assert max_abs(com["key"][:, :, :seq], orc.demand_totals(q, k)) < 1e-5 * 8
+    assert com["key"][:, :, seq:].abs().max().item() == 0

@@ -16,11 +16,12 @@ every slice.
   - rows of the attention matrix sum to one, so sum_j dv_j = sum_i dO_i.  The
     kernel rounds the share tile, dO / (S + eps) and dv to bf16 (relative
     error <= 2^-9 each), which bounds the gap by 2^-8 (sum |dv| + sum |dO|).
-* The same shape through the key-parallel output pass
-  (DILUTION_FORWARD_KEY_PASS=1): outputs of slices 0 and 15 against the
-  blocked oracle, every output against the default forward (1e-2), demand
-  totals and checkpoints within fp32 summation-order differences (1e-5
-  relative), and dq, dk, dv of slices 0 and 15 against the device oracle.
+* The same shape through the key-parallel output pass (the default) and the
+  three-pass forward (DILUTION_FORWARD_KEY_PASS=0): outputs of slices 0 and
+  15 against the blocked oracle, every output of one against the other
+  (1e-2), demand totals and checkpoints within fp32 summation-order
+  differences (1e-5 relative), and dq, dk, dv of slices 0 and 15 against the
+  device oracle.
 * The same shape in fp32 operands: outputs and dq, dk, dv of slices 0 and 15
   against ``grads_blocked_f64`` on the host and of every slice on the device
   (1e-4 max-abs); sum_j dk_j = 0 (adding a constant to every key leaves each
@@ -141,8 +142,9 @@ def test_c3_key_pass_full_size(monkeypatch):
     q, k, v, do = orc.make_inputs((1, 16, 16384, 64), seed=4, qk_scale=0.5, with_dout=True,
                                   dtype=torch.bfloat16)
     qg, kg, vg = (t.cuda() for t in (q, k, v))
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
     out0, aux0 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True)
-    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "1")
+    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS")
     out1, aux1 = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True)
     torch.cuda.synchronize()
     for h in (0, 15):
@@ -162,13 +164,16 @@ def test_c3_key_pass_full_size(monkeypatch):
     causal = keys[None, :] < ends[:, None]
     diff = ((c1 - c0).abs() / c0.abs().clamp(min=1.0))[..., causal]
     assert diff.max().item() < 1e-5
+    # gradients through the three-pass forward (the default path's are
+    # checked on every slice by test_c3_training_bf16_full_size)
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
     xs = [t.cuda().requires_grad_(True) for t in (q, k, v)]
     out = kernels.dilution_attention(*xs, dot_precision="bf16")
     out.backward(do.cuda())
     grads = [x.grad for x in xs]
     for h in (0, 15):
         want, _ = _grads_oracle(q, k, v, do, (0, h), "cuda")
-        _check_bf16_grads([g[0, h] for g in grads], want, f"slice {h} (device oracle, key pass)")
+        _check_bf16_grads([g[0, h] for g in grads], want, f"slice {h} (device oracle, three-pass forward)")
 
 
 def test_c3_training_fp32_full_size():
