@@ -812,14 +812,12 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
     const bf16x8 xf[2] = {acc_frag<CT>(xv, 0), acc_frag<CT>(xv, 1)};
     stage_sh(buf, xf);
     // row sums of the staged (bf16) shares: each lane half adds its 16 keys of
-    // the transposed tile (the bf16-rounded values) on the VALU, then the
-    // halves (with the loop unrolled: fwd_keyout -1.5% against all-ones MFMAs)
-    float rv[16];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) rv[8 * s + t] = static_cast<float>(xf[s][t]);
-    const HalfPair rp = halves(sum16(rv));
+    // the transposed tile on the VALU, then the halves (with the loop
+    // unrolled: fwd_keyout -1.5% against all-ones MFMAs).  The transposed
+    // registers already hold the bf16-rounded values exactly (the identity
+    // product of bf16 operands is exact in fp32), so they are added as they
+    // are: the same sums as of the staged values, without converting back.
+    const HalfPair rp = halves(sum16(xv));
     if (h == 0) rs_s[buf][wave][l32] = rp.lo + rp.hi;
   };
   auto stage_zero = [&](int buf) {

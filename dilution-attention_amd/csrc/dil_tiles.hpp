@@ -171,7 +171,10 @@ struct KeyGroups {
   static constexpr int kThreads = 64 * KW;
   static constexpr int kKeys = KW * kTileK;
   static constexpr int kTilesPerGroup = kKeys / kTileQ;
-  static constexpr int kStride = kKeys + 8;            // bf16 per staged [row][key] row
+  // bf16 per staged [row][key] row: a row stride of 8 banks (mod 128) puts
+  // the 16 rows x 2 chunks of a 32-lane 16-byte product read, and the 16 rows
+  // of an 8-byte stage write, on distinct banks
+  static constexpr int kStride = kKeys + 16;
   __host__ __device__ static int64_t tile_base(int64_t g, int64_t nq) {
     return g * nq - static_cast<int64_t>(kTilesPerGroup) * g * (g - 1) / 2;
   }
