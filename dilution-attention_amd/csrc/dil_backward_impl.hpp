@@ -1224,9 +1224,9 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, KqPart* _
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kpark[dq4][ks][lane], acc, 0, 0, 0);
     }
     // output: lane <-> head dim 16 dq4 + (lane & 15), register j <-> row 16 rh + 4 (lane >> 4) + j;
-    // the partial tile is stored [d][32 rows]
+    // the partial tile is stored in 16 x 16 blocks (part_block_off)
     const int64_t tile = gbase + qt;
-    KqPart* dst = dqp_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ + 16 * rh + 4 * (lane >> 4);
+    KqPart* dst = dqp_s + tile * (D * kTileQ) + part_block_off(dq4, rh, lane);
     // streamed past the caches: the partials are read once, by bwd_dq_reduce
     if constexpr (std::is_same_v<KqPart, float>) {
       __builtin_nontemporal_store(acc, reinterpret_cast<floatx4*>(dst));
@@ -1300,7 +1300,7 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, KqPart* _
 // sum of the ghat partials, both in key-group order; and the (ghat * q)^T
 // tiles of the dk correction.  Grid: (query tiles, slices from slice0), the
 // tiles with the most key groups first.  Thread t sums elements [8 t, 8 t + 8)
-// of the [d][32 rows] partial tiles.
+// of the partial tiles (one head dim, 8 rows: part_dim / part_row).
 template <int D, bool GHAT = true>
 __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const KqPart* __restrict__ dqp,
                                                           const float* __restrict__ ghp, int64_t ntiles,
@@ -1353,9 +1353,13 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const KqPart* __restri
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += v[e];
   }
-  const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
+  {
+    // the thread's 8 elements: one head dim, 8 consecutive rows of the tile
+    const int pd = part_dim(8 * t), pr = part_row(8 * t);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
+    for (int e = 0; e < 8; ++e) sum_s[pd][pr + e] = acc[e];
+  }
+  const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
   if (GHAT && t < kTileQ) {
     // eight loads in flight, added in group order
     const float* gp = ghp + slice * ntiles * kTileQ + t;
@@ -1372,7 +1376,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const KqPart* __restri
     g_s[t] = s;
   }
   __syncthreads();
-  // (ghat * q)^T: the same [d][32 rows] chunk of the tile-major Q^T copy (the
+  // (ghat * q)^T: thread t scales the [d][32 rows] chunk t of the tile-major Q^T copy (the
   // elementwise bids have no ghat and no dk correction)
   if constexpr (GHAT) {
     const int64_t off = slice * D * t_pad + tmajor_index(static_cast<int64_t>(tq) * kTileQ + r8, d, D);

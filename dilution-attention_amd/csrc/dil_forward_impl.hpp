@@ -667,10 +667,10 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_out(FwdParams P) {
 //     running sum advances by the tile's column total;
 //   * the share tile is transposed with an identity MFMA (rows in lanes) and
 //     staged in LDS as bf16; its row sums (the normaliser's partial, over the
-//     same bf16 values that multiply V) come from an all-ones operand.
+//     same bf16 values that multiply V) are added on the VALU.
 // After the next tile's stash 8 waves form the tile's share V over the
 // group's keys, one 16 x 16 output block each (v_mfma_f32_16x16x32_bf16, V
-// parked in LDS), stored as one bf16 [d][32 rows] partial per (key group,
+// parked in LDS), stored as one bf16 [64 x 32] partial (part_block_off) per (key group,
 // tile) with the fp32 row sums beside it, compactly (ChunkGroups).
 // fwd_out_reduce sums the partials of every key group in a fixed order and
 // normalises.  With 16 waves (512 keys) a CU holds one workgroup (148 KB of
@@ -846,14 +846,13 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, vpark[dq4][ks][lane], acc, 0, 0, 0);
     }
     // output: lane <-> head dim 16 dq4 + (lane & 15), register j <-> row 16 rh + 4 (lane >> 4) + j;
-    // the partial tile is stored [d][32 rows], streamed past the caches
+    // the partial tile is stored in 16 x 16 blocks (part_block_off), streamed past the caches
     const int64_t tile = gbase + rt;
     const floatx2 a = {acc[0], acc[1]}, b = {acc[2], acc[3]};
     const bf16x2 pa = __builtin_convertvector(a, bf16x2), pb = __builtin_convertvector(b, bf16x2);
     const bf16x4 v = {pa[0], pa[1], pb[0], pb[1]};
     __builtin_nontemporal_store(__builtin_bit_cast(floatx2, v),
-                                reinterpret_cast<floatx2*>(op_s + tile * (D * kTileQ) + (16 * dq4 + (lane & 15)) * kTileQ +
-                                                           16 * rh + 4 * (lane >> 4)));
+                                reinterpret_cast<floatx2*>(op_s + tile * (D * kTileQ) + part_block_off(dq4, rh, lane)));
     if (pw == 0 && lane < kTileQ) {
       float s = 0.f;
 #pragma unroll
@@ -895,8 +894,8 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
 // out = (sum over key groups of the share V partials) / (S + eps), S = the sum
 // of the row-sum partials, both in key-group order; S is also the forward's
 // ssum.  Grid: (query tiles, slices from slice0), the tiles with the most key
-// groups first.  Thread t sums elements [8 t, 8 t + 8) of the [d][32 rows]
-// partial tiles.
+// groups first.  Thread t sums elements [8 t, 8 t + 8) of the partial tiles
+// (one head dim, 8 rows: part_dim / part_row).
 template <int D, int KW>
 __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restrict__ op,
                                                            const float* __restrict__ rp, int64_t ntiles,
@@ -932,9 +931,12 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
   }
-  const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
+  {
+    // the thread's 8 elements: one head dim, 8 consecutive rows of the tile
+    const int pd = part_dim(8 * t), pr = part_row(8 * t);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) sum_s[d][r8 + e] = acc[e];
+    for (int e = 0; e < 8; ++e) sum_s[pd][pr + e] = acc[e];
+  }
   if (t < kTileQ) {
     // eight loads in flight, added in group order
     const float* gp = rp + slice * ntiles * kTileQ + t;

@@ -162,6 +162,18 @@ constexpr int kKqTilesPerGroup = kKqKeys / kTileQ;  // query tiles spanned by a 
 // 16-way); a fully conflict-free layout measured no faster
 constexpr int kPdStride = kKqKeys + 8;
 
+// Layout of one partial tile (head_dim 64 x 32 rows) of the key-group
+// passes: eight 16 x 16 blocks, block (d / 16, row / 16) at 256 (2 (d / 16) +
+// row / 16), each [16 head dims][16 rows].  The wave that forms a block with
+// one 16x16x32 MFMA chain stores it as 512 contiguous bytes (lane l: head dim
+// l & 15, rows 4 (l >> 4) + [0, 4)), whole cache lines; element e of the tile
+// belongs to head dim part_dim(e) and row part_row(e).
+__host__ __device__ constexpr int part_block_off(int dq4, int rh, int lane) {
+  return 256 * (2 * dq4 + rh) + 16 * (lane & 15) + 4 * (lane >> 4);
+}
+__host__ __device__ constexpr int part_dim(int e) { return 16 * (e >> 9) + ((e >> 4) & 15); }
+__host__ __device__ constexpr int part_row(int e) { return 16 * ((e >> 8) & 1) + (e & 15); }
+
 // The same compact indexing for key groups of KW waves (KW * 32 keys): group
 // g meets query tiles [KW g, nq), and tile (g, qt) sits at tile_base(g, nq) +
 // qt - KW g.
