@@ -229,11 +229,19 @@ constexpr int bwd_occupancy() {
 // in LDS and sums ghat on the VALU, which leaves room for three workgroups per
 // CU (<= 168 VGPRs, 48 KB of LDS each) with bf16 operands up to head_dim 64:
 // -16% at T = 2048, -10% at 4096 and 16384 against the register form (ones
-// column MFMA for ghat, two workgroups per CU), which runs for fp32 operands,
-// head_dim 128 and the operator variants.
+// column MFMA for ghat, two workgroups per CU), which runs for head_dim 128
+// and the operator variants.  With fp32 or split operands (head_dim <= 64)
+// the parked form is 8 waves (256 rows) per workgroup: <= 256 registers a
+// lane (two waves per SIMD, where the register form holds one) and ~124 KB
+// of LDS (the parked dO' of 8 waves and one set of K / V / K^T stages for
+// all of them), one workgroup per CU.
 template <typename CT, int D>
 constexpr bool query_parks() {
-  return sizeof(CT) == 2 && D <= 64;
+  return D <= 64;
+}
+template <typename CT, int D>
+constexpr int query_waves() {
+  return sizeof(CT) == 2 ? 4 : 8;
 }
 
 // ---------------------------------------------------------------------------
@@ -465,23 +473,25 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
 // ---------------------------------------------------------------------------
 // row-parallel dq pass
 
-template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL, bool PARK = false>
-__global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd_occupancy<CT, D>())) void bwd_query(
+template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL, bool PARK = false,
+          int W = 4>
+__global__ __launch_bounds__(64 * W, ((PARK && query_parks<CT, D>()) ? (W == 4 ? 3 : 1) : bwd_occupancy<CT, D>())) void bwd_query(
     BwdParams P) {
   using TL = Tiles<CT, D>;
   using Frag = typename Mma<CT>::frag;
   constexpr int kNS = BID == BID_SOFTMAX ? 2 : 3;                // per-row statistics staged
   constexpr bool kPark = PARK && query_parks<CT, D>();
+  static_assert(W == 4 || (W == 8 && kPark), "8-wave workgroups are the parked form");
   constexpr int kSteps = kTileK / Mma<CT>::kStep;
   constexpr int kFS = RowFrag<CT, D>::kSteps;
   __shared__ __attribute__((aligned(16))) CT k_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT v_s[2][kTileK * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT kt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) float rs_s[4][kNS * kTileQ];   // per wave: lse (r0), -dbs, r1
-  __shared__ float g_s[4][kTileQ];
+  __shared__ __attribute__((aligned(16))) float rs_s[W][kNS * kTileQ];   // per wave: lse (r0), -dbs, r1
+  __shared__ float g_s[W][kTileQ];
   // parked operands, lane-minor so that one fragment read is conflict-free:
   // each wave's dO' row fragments, and the identity of the transposes
-  __shared__ __attribute__((aligned(16))) Frag do_park[kPark ? 4 : 1][kPark ? kFS : 1][64];
+  __shared__ __attribute__((aligned(16))) Frag do_park[kPark ? W : 1][kPark ? kFS : 1][64];
   __shared__ __attribute__((aligned(16))) Frag id_park[kPark ? kSteps : 1][64];
 
   const WorkItem item = xcd_work_item(P.kgroups, P.n, true, P.lpt != 0);    // heavy (late) row groups first
@@ -495,9 +505,9 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const float hf = static_cast<float>(h);
-  const int qt = g * 4 + wave;
+  const int qt = g * W + wave;
   const int64_t r0 = static_cast<int64_t>(qt) * kTileQ;
-  const int64_t wg_last = min(static_cast<int64_t>(g * 4 + 4) * kTileQ, P.T);
+  const int64_t wg_last = min(static_cast<int64_t>(g * W + W) * kTileQ, P.T);
   const int nkt_wg = static_cast<int>((wg_last + kTileK - 1) / kTileK);
   const int nkt_w = r0 < P.T ? qt + 1 : 0;
 
@@ -700,15 +710,20 @@ __global__ __launch_bounds__(kThreads, ((PARK && query_parks<CT, D>()) ? 3 : bwd
 
   // buffer loads in the parked form; the register form skips the rows past
   // the end (both measured best for their form)
+  // the tile loaders are laid out for kThreads threads: with 8 waves, waves
+  // 0-3 stage the tiles that all 8 read (a wave-uniform condition)
   KTileLoader<CT, D, false, kPark ? kLoadBuffer : kLoadSkip> kl, vl;
   TTileLoader<CT, D, kPark ? kLoadBuffer : kLoadClamp> ktl;
+  const bool stager = W == 4 || threadIdx.x < kThreads;
   auto fetch = [&](int kt) {
+    if (!stager) return;
     const int64_t key0 = static_cast<int64_t>(kt) * kTileK;
     kl.load(ks, key0, P.T);
     vl.load(vs, key0, P.T);
     ktl.load(kts, key0);
   };
   auto stash = [&](int buf) {
+    if (!stager) return;
     kl.store(k_s[buf]);
     vl.store(v_s[buf]);
     ktl.store(kt_s[buf]);
@@ -1570,7 +1585,14 @@ int launch_backward(const BackwardArgs& a) {
   const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
   DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
   constexpr bool kParked = query_parks<CT, D>() && is_production<BID, SHARE>();
-  DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, kParked><<<gkey, kThreads, 0, st>>>(P)));
+  constexpr int kQW = kParked ? query_waves<CT, D>() : 4;     // row tiles (waves) per workgroup
+  {
+    const int kgroups_key = P.kgroups;
+    P.kgroups = (nkt + kQW - 1) / kQW;
+    const dim3 gq(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
+    DIL_TIMED("bwd_query", st, (bwd_query<CT, D, BID, SHARE, kParked, kQW><<<gq, 64 * kQW, 0, st>>>(P)));
+    P.kgroups = kgroups_key;
+  }
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     DIL_TIMED("prep", st,
               prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), ns), kThreads, 0, st>>>(
