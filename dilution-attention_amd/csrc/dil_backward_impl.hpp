@@ -1332,41 +1332,41 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const KqPart* __restri
   const int ng = min(static_cast<int>(keyq_groups(T)) - 1, tq / kKqTilesPerGroup) + 1;
   const int t = threadIdx.x;
   const KqPart* base = dqp + slice * ntiles * (D * kTileQ) + 8 * t;
-  // groups in order, four loads in flight (the partial sums are added in
-  // group order: deterministic)
+  // the partial sums are added in group order: deterministic
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   auto tile_of = [&](int g) { return keyq_tile_base(g, nq) + tq - kKqTilesPerGroup * g; };
-  auto load8 = [&](int g, float (&v)[8]) {
+  // a group's 8 values stay in their storage type until they are added (4
+  // registers each for bf16: eight groups in flight keep the kernel at 8
+  // waves per SIMD)
+  using Raw = std::conditional_t<std::is_same_v<KqPart, float>, floatx8, bf16x8>;
+  auto load_raw = [&](int g) -> Raw {
     const KqPart* p = base + tile_of(g) * (D * kTileQ);
-    if constexpr (std::is_same_v<KqPart, float>) {
-      const floatx4 a = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
-      const floatx4 b = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p) + 1);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = a[e];
-        v[4 + e] = b[e];
-      }
-    } else {
-      const bf16x8 x = load_once(p);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(x[e]);
-    }
+    if constexpr (std::is_same_v<KqPart, float>) return __builtin_nontemporal_load(reinterpret_cast<const Raw*>(p));
+    else return load_once(p);
   };
-  int g = 0;
-  for (; g + 4 <= ng; g += 4) {
-    float v[4][8];
+  // eight groups in flight; threads 0-31 load the same groups' ghat partials
+  // beside them (both added in group order)
+  const bool grow_t = GHAT && t < kTileQ;
+  const float* gp = ghp + slice * ntiles * kTileQ + (grow_t ? t : 0);
+  float s = 0.f;
+  for (int g = 0; g < ng; g += 8) {
+    Raw v[8];
+    float r[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load8(g + u, v[u]);
+    for (int u = 0; u < 8; ++u) {
+      if (g + u < ng) {
+        v[u] = load_raw(g + u);
+        if (grow_t) r[u] = load_once(gp + tile_of(g + u) * kTileQ);
+      }
+    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < 8; ++u) {
+      if (g + u < ng) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += v[u][e];
-  }
-  for (; g < ng; ++g) {
-    float v[8];
-    load8(g, v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += v[e];
+        for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
+        if (grow_t) s += r[u];
+      }
+    }
   }
   {
     // the thread's 8 elements: one head dim, 8 consecutive rows of the tile
@@ -1375,21 +1375,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce(const KqPart* __restri
     for (int e = 0; e < 8; ++e) sum_s[pd][pr + e] = acc[e];
   }
   const int d = t / (kTileQ / 8), r8 = (t % (kTileQ / 8)) * 8;
-  if (GHAT && t < kTileQ) {
-    // eight loads in flight, added in group order
-    const float* gp = ghp + slice * ntiles * kTileQ + t;
-    float s = 0.f;
-    int gi = 0;
-    for (; gi + 8 <= ng; gi += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = load_once(gp + tile_of(gi + u) * kTileQ);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s += v[u];
-    }
-    for (; gi < ng; ++gi) s += load_once(gp + tile_of(gi) * kTileQ);
-    g_s[t] = s;
-  }
+  if (grow_t) g_s[t] = s;
   __syncthreads();
   // (ghat * q)^T: thread t scales the [d][32 rows] chunk t of the tile-major Q^T copy (the
   // elementwise bids have no ghat and no dk correction)

@@ -44,6 +44,8 @@ struct FwdParams {
   int64_t q_sn;
   const void* k;          // CT rows (n, >= Tk, D), slice stride k_sn
   int64_t k_sn;
+  const void* v;          // CT rows of V (n, >= Tk, D), slice stride v_sn: the key
+  int64_t v_sn;           // pass parks V from them when set (else from vt)
   const void* vt;         // CT V^T, tile-major (Tk_pad rows per slice)
   const void* kt;         // CT K^T, tile-major, or null
   int64_t t_sn, tk_pad;
@@ -715,10 +717,25 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
   RowFrag<CT, D> kf;
   if (key_ok) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + slice * P.k_sn + key * D + h * (D / 2));
   else zero_row_frag<CT, D>(kf);
-  // park V: fragment (d quarter u, key step w, lane) holds
-  // V[32 (kb0 + w) + 8 (lane >> 4) + t][16 u + (lane & 15)], t = 0..7: 16
-  // contiguous bytes of the tile-major V^T copy (zero past its padded rows)
-  {
+  // the parked V fragments: fragment (d quarter u, key step w, lane) holds
+  // V[32 (kb0 + w) + 8 (lane >> 4) + t][16 u + (lane & 15)], t = 0..7, zero
+  // past the last key.  From the bf16 rows of V (no transposed copy to
+  // write): chunk i of the group's rows (key i / 8, head dims 8 (i % 8) +
+  // [0, 8)) is loaded whole, and its 8 values are written to their fragments
+  // one by one.  Else 16 contiguous bytes of the tile-major V^T copy per
+  // fragment.  Loaded here, written to LDS once the first row tile's fetch is
+  // in flight too, so the walk starts after one memory wait instead of two.
+  constexpr int kVChunks = KG::kKeys * D / 8 / KG::kThreads;     // 16-byte row chunks per thread
+  bf16x8 vfr[kVChunks];
+  static_assert(kVChunks == D / 16, "one register set serves both parking forms");
+  if (P.v != nullptr) {
+    const int64_t first = static_cast<int64_t>(kb0) * kTileK;            // the group's first key
+    const CT* vs = static_cast<const CT*>(P.v) + slice * P.v_sn + first * D;
+    const auto rs = make_rsrc(vs, (T - first) * D * static_cast<int64_t>(sizeof(CT)));
+#pragma unroll
+    for (int c = 0; c < kVChunks; ++c)
+      vfr[c] = buffer_load16<bf16x8>(rs, static_cast<uint32_t>((threadIdx.x + c * KG::kThreads) * 16), 0);
+  } else {
     const CT* vts = static_cast<const CT*>(P.vt) + slice * P.t_sn;
     const int64_t first = static_cast<int64_t>(kb0) * kTileK * D;
     const auto rs = make_rsrc(vts + first, (P.t_sn - first) * static_cast<int64_t>(sizeof(CT)));
@@ -726,11 +743,7 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
     for (int u = 0; u < D / 16; ++u) {
       const int d = 16 * u + (lane & 15);
       const uint32_t off = static_cast<uint32_t>(((wave * D + d) * kTileK + 8 * (lane >> 4)) * sizeof(CT));
-      vpark[u][wave][lane] = buffer_load16<bf16x8>(rs, off, 0);
-    }
-    if (wave == 0) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
+      vfr[u] = buffer_load16<bf16x8>(rs, off, 0);
     }
   }
   // demand entering the current tile (this lane's key): the carried demand of
@@ -862,6 +875,25 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
   };
 
   fetch(rt0);
+  if (P.v != nullptr) {
+#pragma unroll
+    for (int c = 0; c < kVChunks; ++c) {
+      const int i = threadIdx.x + c * KG::kThreads;
+      const int kk = i / (D / 8), d0 = (i % (D / 8)) * 8;           // key in the group, first head dim
+      const int w = kk / kTileK, j = (kk % kTileK) / 8, t = kk % 8;
+      // one 2-byte store per value (lanes write distinct halves of shared words)
+      __bf16* dst = reinterpret_cast<__bf16*>(&vpark[d0 / 16][w][16 * j + d0 % 16]) + t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[8 * e] = vfr[c][e];
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < D / 16; ++u) vpark[u][wave][lane] = vfr[u];
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) id_park[s][lane] = ident_qs<CT>(l32, h, s);
+  }
   stash(0);
   __syncthreads();
   // the product of tile qt - 1 (staged before the previous barrier, in the
@@ -914,22 +946,30 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
   const int t = threadIdx.x;
   const __bf16* base = op + slice * ntiles * (D * kTileQ) + 8 * t;
   auto tile_of = [&](int g) { return cg.base(g) + tq - cg.first(g); };
-  // groups in order, four loads in flight
+  // groups in order, eight partial tiles in flight; threads 0-31 load the
+  // same groups' row sums beside them (both added in group order)
+  const bool srow = t < kTileQ;
+  const float* gp = rp + slice * ntiles * kTileQ + (srow ? t : 0);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  int g = 0;
-  for (; g + 4 <= ng; g += 4) {
-    bf16x8 v[4];
+  float s = 0.f;
+  for (int g = 0; g < ng; g += 8) {
+    bf16x8 v[8];
+    float r[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = load_once(base + tile_of(g + u) * (D * kTileQ));
+    for (int u = 0; u < 8; ++u) {
+      if (g + u < ng) {
+        v[u] = load_once(base + tile_of(g + u) * (D * kTileQ));
+        if (srow) r[u] = load_once(gp + tile_of(g + u) * kTileQ);
+      }
+    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < 8; ++u) {
+      if (g + u < ng) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
-  }
-  for (; g < ng; ++g) {
-    const bf16x8 v = load_once(base + tile_of(g) * (D * kTileQ));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
+        for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[u][e]);
+        if (srow) s += r[u];
+      }
+    }
   }
   {
     // the thread's 8 elements: one head dim, 8 consecutive rows of the tile
@@ -937,19 +977,7 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
 #pragma unroll
     for (int e = 0; e < 8; ++e) sum_s[pd][pr + e] = acc[e];
   }
-  if (t < kTileQ) {
-    // eight loads in flight, added in group order
-    const float* gp = rp + slice * ntiles * kTileQ + t;
-    float s = 0.f;
-    int gi = 0;
-    for (; gi + 8 <= ng; gi += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = load_once(gp + tile_of(gi + u) * kTileQ);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s += v[u];
-    }
-    for (; gi < ng; ++gi) s += load_once(gp + tile_of(gi) * kTileQ);
+  if (srow) {
     s_s[t] = s;
     const int64_t row = static_cast<int64_t>(tq) * kTileQ + t;
     if (row < T) ssum[slice * T + row] = s;
@@ -1035,17 +1063,24 @@ int launch_forward(const ForwardArgs& a) {
   CT* kt = a.pk ? reinterpret_cast<CT*>(ws + w.kt) : nullptr;
   CT* qc = convert ? reinterpret_cast<CT*>(ws + w.qc) : nullptr;
   CT* kc = convert ? reinterpret_cast<CT*>(ws + w.kc) : nullptr;
+  // the key pass parks V from the caller's bf16 rows: no V^T to write (the
+  // workspace keeps its room, shared with the three-pass forward's layout)
+  constexpr bool kKeyPassBuilt =
+      std::is_same_v<CT, __bf16> && D == 64 && BID == BID_SOFTMAX && SHARE == SHARE_INCL;
+  const bool key_pass = kKeyPassBuilt && keyout_eligible(a.n, a.C, a.Tk, a.q0, D, kOperandPrec<CT>, a.key_pass);
+  const bool v_rows = key_pass && !convert;
 
   // operands in the compute type; V^T (and K^T) tiles
   const unsigned ktiles = static_cast<unsigned>(tk_pad / 64);
   const unsigned qtiles = static_cast<unsigned>(pad64(a.C) / 64);
   slice_batches(a.n, [&](int64_t s0, unsigned ns) {
     PrepJobs kv{};
-    kv.job[0] = PrepJob{a.v, a.kv_sn, nullptr, 0, vt, nullptr};
-    kv.job[1] = PrepJob{a.k, a.kv_sn, kc, a.Tk * D, kt, nullptr};
-    const unsigned nkv = (convert || kt != nullptr) ? 2 : 1;
-    DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(ktiles, ns, nkv), kThreads, 0, st>>>(
-                              kv, a.dtype, a.Tk, D * tk_pad, tk_pad, s0)));
+    unsigned nkv = 0;
+    if (!v_rows) kv.job[nkv++] = PrepJob{a.v, a.kv_sn, nullptr, 0, vt, nullptr};
+    if (convert || kt != nullptr) kv.job[nkv++] = PrepJob{a.k, a.kv_sn, kc, a.Tk * D, kt, nullptr};
+    if (nkv > 0)
+      DIL_TIMED("prep", st, (prep_kernel<CT, D><<<dim3(ktiles, ns, nkv), kThreads, 0, st>>>(
+                                kv, a.dtype, a.Tk, D * tk_pad, tk_pad, s0)));
     if (convert) {
       PrepJobs qj{};
       qj.job[0] = PrepJob{a.q, a.q_sn, qc, a.C * D, nullptr, nullptr};
@@ -1058,6 +1093,8 @@ int launch_forward(const ForwardArgs& a) {
   P.q_sn = convert ? a.C * D : a.q_sn;
   P.k = convert ? static_cast<const void*>(kc) : a.k;
   P.k_sn = convert ? a.Tk * D : a.kv_sn;
+  P.v = v_rows ? a.v : nullptr;
+  P.v_sn = a.kv_sn;
   P.vt = vt;
   P.kt = kt;
   P.t_sn = D * tk_pad;
@@ -1090,8 +1127,8 @@ int launch_forward(const ForwardArgs& a) {
   const dim3 grid(static_cast<unsigned>(xcd_grid(P.groups * a.n)));
   if (a.pk) DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, true, BID><<<grid, kThreads, 0, st>>>(P)));
   else DIL_TIMED("fwd_stats", st, (fwd_stats<CT, D, false, BID><<<grid, kThreads, 0, st>>>(P)));
-  if constexpr (std::is_same_v<CT, __bf16> && D == 64 && BID == BID_SOFTMAX && SHARE == SHARE_INCL) {
-    if (keyout_eligible(a.n, a.C, a.Tk, a.q0, D, kOperandPrec<CT>, a.key_pass)) {
+  if constexpr (kKeyPassBuilt) {
+    if (key_pass) {
       // one key pass forms the checkpoints, the totals and the share V
       // partials; the reduction finishes out and ssum
       __bf16* op = reinterpret_cast<__bf16*>(ws + w.op);
@@ -1101,6 +1138,11 @@ int launch_forward(const ForwardArgs& a) {
       const unsigned nq = static_cast<unsigned>((a.C + kTileQ - 1) / kTileQ);
       const int64_t ntiles = keyout_tiles(a.C, a.Tk);
       P.kgroups = static_cast<int>(KG::groups(a.Tk));
+      // longest walks first, group by group, whatever the size: every chunk's
+      // walks differ in length (its diagonal groups are shorter), and in slice
+      // order a CU could finish a whole walk after the rest (a prefill chunk of
+      // 256 slices at 2048 rows ended ~0.17 ms after its work would balance)
+      P.lpt = 1;
       const dim3 gko(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
       DIL_TIMED("fwd_keyout", st, (fwd_keyout<D, KW><<<gko, KG::kThreads, 0, st>>>(P, op, rp, ntiles)));
       slice_batches(a.n, [&](int64_t s0, unsigned ns) {

@@ -280,7 +280,6 @@ __device__ __forceinline__ V buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t vo
 __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
-
 // Loads of a split reduction's partials, which are read exactly once: the
 // non-temporal hint streams them past the caches instead of evicting reused
 // data (measured 11% faster on the partial reductions).
