@@ -154,6 +154,9 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (3 times): the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run the C4 chunked-prefill leg and print its JSON object (for a "
+                         "kernel trace of the prefill kernels alone)")
     return ap.parse_args()
 
 
@@ -870,6 +873,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         copy_calibration(dev)
+        return 0
+    if args.prefill_only:
+        print(json.dumps(bench_prefill(args, dev)), flush=True)
         return 0
     tr = bench_training(args, dev)
     batch, heads, seq, d = tr["shape"]
