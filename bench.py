@@ -26,6 +26,10 @@ The same line carries
     with its own SDPA comparator;
   * ``prefill``: chunked prefill of a 16K prompt in 2K chunks (BASELINE
     configs[3]: B=16 H=16 d=64 bf16), algorithmic TFLOP/s;
+  * ``reference_shapes``: fwd+bwd at the four shapes the reference publishes
+    its own times for, and the forward alone (no aux) at its published long
+    contexts (B1 H12 T=128K and 256K, H8 T=256K), beside those times (other
+    hardware: context, not a baseline);
   * ``decode``: the cached decode step at 128K context (
     B=16 H=16 d=64 bf16), HBM GB/s over B H L (4d + 8) algorithmic bytes per
     step, with its own roofline object, and a ``sweep`` at 16K / 32K / 64K;
@@ -138,6 +142,8 @@ def parse_args():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-decode-sweep", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-reference-shapes", action="store_true",
+                    help="skip the fwd+bwd and long forward at the reference's published shapes")
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-lm", action="store_true")
@@ -563,6 +569,72 @@ def bench_prefill(args, dev):
                        "prompt": seq, "chunk": chunk, "head_dim": d, "dtype": "bf16"}}
 
 
+# The reference's published figures for this operator (bf16, head_dim 64, an
+# NVIDIA RTX PRO 6000 Blackwell; docs/kernels.md:206-209, 220-221): context
+# on other hardware, not a same-node comparison.
+REFERENCE_FWD_BWD = [  # (batch, heads, seq), ms per fwd+bwd
+    ((8, 8, 4096), 5.46), ((2, 8, 8192), 5.05), ((2, 12, 16384), 30.18), ((32, 12, 1024), 3.67)]
+REFERENCE_LONG_FORWARD = [  # (heads, seq) at B1, seconds and GiB per forward
+    ((12, 131072), 1.5, 17.0), ((12, 262144), 1.8, 17.9), ((8, 262144), 1.1, 17.3)]
+
+
+def bench_reference_shapes(args, dev) -> list:
+    """The operator's fwd+bwd at the shapes the reference publishes its own
+    times for, timed like the headline step (3 warm-ups, 10 steps)."""
+    rows = []
+    for (batch, heads, seq), ref_ms in REFERENCE_FWD_BWD:
+        sub = argparse.Namespace(**vars(args))
+        sub.warmup, sub.steps = 3, 10
+        WORKLOADS["_ref"] = (batch, heads, seq, 64)
+        sub.workload = "_ref"
+        tr = bench_training(sub, dev)
+        del tr["inputs"], tr["step"], WORKLOADS["_ref"]
+        rows.append({"batch": batch, "heads": heads, "seq_len": seq, "ms_per_step": round(tr["ms"], 4),
+                     "value": round(tr["value"], 2), "unit": "TFLOP/s",
+                     "reference_ms": ref_ms, "reference_over_this": round(ref_ms / tr["ms"], 2)})
+        log(f"reference shape B{batch} H{heads} T{seq}: {tr['ms']:.3f} ms (reference {ref_ms} ms)")
+    return rows
+
+
+def bench_long_forward(args, dev) -> list:
+    """Forward only, without aux (no demand checkpoints kept: the inference
+    forward), bf16, B1 d64, at the long contexts the reference publishes
+    times and memory for; algorithmic 2 B H T^2 d FLOPs (causal QK^T and
+    share @ V).  Peak memory is the allocator's high-water mark above the
+    resident inputs during the call."""
+    import torch
+
+    from dilution import kernels
+
+    rows = []
+    for (heads, seq), ref_s, ref_gib in REFERENCE_LONG_FORWARD:
+        g = torch.Generator(device=dev).manual_seed(11)
+        q, k, v = (torch.randn(1, heads, seq, 64, device=dev, generator=g, dtype=torch.bfloat16)
+                   for _ in range(3))
+        base = torch.cuda.memory_allocated(dev)
+
+        def fwd():
+            return kernels.dilution_attention_forward(q, k, v, dot_precision="bf16")
+
+        fwd()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        ms = timed(fwd, 2)
+        peak = (torch.cuda.max_memory_allocated(dev) - base) / 2**30
+        per = kernel_pass(fwd, 1)
+        tflops = 2.0 * heads * seq * seq * 64 / (ms * 1e-3) / 1e12
+        rows.append({"batch": 1, "heads": heads, "seq_len": seq, "ms": round(ms, 2),
+                     "value": round(tflops, 1), "unit": "TFLOP/s", "peak_gib_above_inputs": round(peak, 1),
+                     "kernels_ms": {name: round(tot, 2) for name, (_, tot) in per.items()},
+                     "reference_s": ref_s, "reference_gib": ref_gib,
+                     "reference_over_this": round(ref_s * 1e3 / ms, 1)})
+        log(f"long forward H{heads} T{seq}: {ms:.1f} ms, {tflops:.0f} TFLOP/s, {peak:.1f} GiB "
+            f"(reference {ref_s} s, {ref_gib} GiB)")
+        del q, k, v
+        torch.cuda.empty_cache()
+    return rows
+
+
 def _lm_phases(args, dev, kind: str, decode_tokens: int) -> dict:
     """One training step (forward, backward, AdamW) at B4 T16384, timed over
     ``--lm-train-steps`` steps, then a 16384-token prefill at B8 and
@@ -933,6 +1005,14 @@ def main() -> int:
     if not args.no_prefill:
         torch.cuda.empty_cache()
         line["prefill"] = bench_prefill(args, dev)
+    if not args.no_reference_shapes:
+        torch.cuda.empty_cache()
+        line["reference_shapes"] = {
+            "fwd_bwd": bench_reference_shapes(args, dev),
+            "long_forward": bench_long_forward(args, dev),
+            "note": "the reference's published times for this operator, bf16 d64 on an NVIDIA RTX PRO 6000 "
+                    "Blackwell (docs/kernels.md:206-209, 220-221): context on other hardware"}
+        torch.cuda.empty_cache()
     if not args.no_lm:
         torch.cuda.empty_cache()
         line["lm"] = bench_lm(args, dev)

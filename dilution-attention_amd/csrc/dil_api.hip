@@ -34,7 +34,7 @@ int check_variant(const Variant& v, int head_dim) {
 
 extern "C" {
 
-int dil_abi_version(void) { return 3; }
+int dil_abi_version(void) { return 4; }
 
 const char* dil_status_string(int status) {
   switch (status) {
@@ -150,10 +150,10 @@ int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, 
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
   if (n < 1 || seq < 1) return dil::kErrShape;
+  // carry may be null when the call takes the key pass (dil::forward checks)
   if (!all_set(q, k, v, static_cast<const void*>(out), static_cast<const void*>(rmax),
                static_cast<const void*>(rden), static_cast<const void*>(ssum),
-               static_cast<const void*>(carry), static_cast<const void*>(committed_total),
-               static_cast<const void*>(workspace)))
+               static_cast<const void*>(committed_total), static_cast<const void*>(workspace)))
     return dil::kErrShape;
   const bool key_pass = dil::forward_key_pass_requested();
   if (workspace_bytes <
@@ -200,6 +200,16 @@ int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t 
                              stream);
 }
 
+int dil_forward_key_pass(int64_t chunk, int64_t start, int head_dim, int dtype, int precision) {
+  if (!valid_head_dim(head_dim) || !valid_dtype(dtype) || !valid_precision(precision) || chunk < 1 ||
+      start < 0)
+    return 0;
+  return dil::forward_takes_key_pass(chunk, start + chunk, start, head_dim, precision, dil::Variant{},
+                                     dil::forward_key_pass_requested())
+             ? 1
+             : 0;
+}
+
 int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
                                     int dtype, int precision) {
   return dil::forward_workspace_bytes(n, chunk, start + chunk, head_dim, dtype, precision, 0,
@@ -215,10 +225,11 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
   if (n < 1 || chunk < 1 || start < 0 || start + chunk > capacity) return dil::kErrShape;
+  // carry may be null when the chunk takes the key pass (dil::forward checks)
   if (!all_set(q_chunk, k_cache, v_cache, static_cast<const void*>(committed),
                static_cast<const void*>(out), static_cast<const void*>(rmax),
                static_cast<const void*>(rden), static_cast<const void*>(ssum),
-               static_cast<const void*>(carry), static_cast<const void*>(workspace)))
+               static_cast<const void*>(workspace)))
     return dil::kErrShape;
   const bool key_pass = dil::forward_key_pass_requested();
   if (workspace_bytes <

@@ -24,8 +24,16 @@ int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, 
   return static_cast<int64_t>(fwd_layout(n, C, Tk, head_dim, dtype, prec, want_pk, key_pass).total);
 }
 
+bool forward_takes_key_pass(int64_t C, int64_t Tk, int64_t q0, int head_dim, int prec, const Variant& var,
+                            bool key_pass) {
+  return var.bid == BID_SOFTMAX && var.share == SHARE_INCL && keyout_eligible(C, Tk, q0, head_dim, prec, key_pass);
+}
+
 int forward(const ForwardArgs& a) {
   if (const int err = check_variant(a.var, a.head_dim)) return err;
+  // no checkpoint array: only the key pass can do without it
+  if (a.carry == nullptr && !forward_takes_key_pass(a.C, a.Tk, a.q0, a.head_dim, a.prec, a.var, a.key_pass))
+    return kErrShape;
   if (a.var.bid != BID_SOFTMAX || a.var.share != SHARE_INCL) {
     switch (a.var.bid) {
       case 0: return forward_bid<0>(a);

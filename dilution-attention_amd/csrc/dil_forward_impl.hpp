@@ -695,7 +695,9 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
   __shared__ __attribute__((aligned(16))) bf16x8 vpark[D / 16][KW][64];
   __shared__ __attribute__((aligned(16))) bf16x8 id_park[2][64];          // transpose identity
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
+  // early keys (long walks) first; a walk reads one row tile per step, so
+  // balance across the XCDs matters more than L2 sharing (spread)
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0, true);
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -750,7 +752,10 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
   // the rows before the chunk for its earlier keys
   double run = (P.demand_in != nullptr && key < P.q0 && key_ok)
                    ? static_cast<double>(P.demand_in[slice * P.din_sn + key]) : 0.0;
-  float* ccol = P.carry + slice * P.nb * T + min(key, T - 1);
+  // the checkpoints are written only for a caller that keeps them (the
+  // backward's input); an inference forward or prefill chunk passes none
+  const bool ckpt = P.carry != nullptr;          // wave-uniform
+  float* ccol = ckpt ? P.carry + slice * P.nb * T + min(key, T - 1) : nullptr;
 
   // staging: threads 0-255 one 16-byte chunk of the Q row tile; threads 0-31
   // the lse of its rows (+inf past the end: p = 0)
@@ -810,7 +815,7 @@ __global__ __launch_bounds__(64 * KW, 16 / KW) void fwd_keyout(FwdParams P, __bf
         if (dk > i) p[i] = 0.f;
     }
     const float cin = static_cast<float>(run);
-    if (h == 0 && key_ok) ccol[static_cast<int64_t>(rt) * T] = cin;   // the demand entering the tile
+    if (ckpt && h == 0 && key_ok) ccol[static_cast<int64_t>(rt) * T] = cin;   // the demand entering the tile
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = p[i];
     run += static_cast<double>(scan_incl_qs(x, cin + kEps, hf));      // demand + p + eps
@@ -1006,9 +1011,13 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
 // The key-parallel output pass replaces fwd_demand + fwd_out where it serves:
 // bf16 operands, head_dim 64, the production operator, a chunk that starts at
 // a multiple of 512 keys (the training forward, chunked prefill at such
-// starts), its partials (~0.5 byte per causal score element) within the
-// budget.  512-key groups (16 waves); DILUTION_FORWARD_KEY_PASS=0 turns it
-// off (read once by each call and by each size query: ForwardArgs::key_pass).
+// starts), one slice's partials (~0.5 byte per causal score element) within
+// the budget.  The workspace holds the partials of as many slices as the
+// budget allows, and the pass and its reduction run over the slices in
+// batches of that many (one batch up to 2^23 tokens of T^2 work per slice
+// pair: every training and prefill shape of the benchmark).  512-key groups
+// (16 waves); DILUTION_FORWARD_KEY_PASS=0 turns it off (read once by each call
+// and by each size query: ForwardArgs::key_pass).
 constexpr int64_t kKeyoutBudgetBytes = int64_t{24} << 30;
 constexpr int kKeyoutWaves = 16;
 
@@ -1020,9 +1029,19 @@ inline int64_t keyout_tiles(int64_t C, int64_t Tk) {
 inline int64_t keyout_partial_bytes(int64_t n, int64_t C, int64_t Tk, int D) {
   return n * keyout_tiles(C, Tk) * (static_cast<int64_t>(D) * kTileQ * 2 + kTileQ * 4);
 }
-inline bool keyout_eligible(int64_t n, int64_t C, int64_t Tk, int64_t q0, int D, int prec, bool requested) {
+inline bool keyout_eligible(int64_t C, int64_t Tk, int64_t q0, int D, int prec, bool requested) {
   return requested && prec == 2 && D == 64 && q0 + C == Tk && q0 % KeyGroups<kKeyoutWaves>::kKeys == 0 &&
-         keyout_partial_bytes(n, C, Tk, D) <= kKeyoutBudgetBytes;
+         keyout_partial_bytes(1, C, Tk, D) <= kKeyoutBudgetBytes;
+}
+// slices per key-pass batch: all of them when their partials fit the budget,
+// else as many batches as the budget needs, of equal size (a last batch of a
+// slice or two would leave most CUs idle behind its longest walks)
+inline int64_t keyout_batch(int64_t n, int64_t C, int64_t Tk, int D) {
+  const int64_t per = keyout_partial_bytes(1, C, Tk, D);
+  int64_t fit = per > 0 ? kKeyoutBudgetBytes / per : n;
+  fit = fit < 1 ? 1 : (fit < n ? fit : n);
+  const int64_t batches = (n + fit - 1) / fit;
+  return (n + batches - 1) / batches;
 }
 
 struct FwdWorkspace {
@@ -1044,9 +1063,10 @@ FwdWorkspace fwd_layout(int64_t n, int64_t C, int64_t Tk, int D, int dtype, int 
   w.total = w.op;
   // the key pass's partials, when a chunk of this shape can take it (every
   // call is a chunk of rows [Tk - C, Tk) against keys [0, Tk))
-  if (keyout_eligible(n, C, Tk, Tk - C, D, prec, key_pass)) {
-    w.rp = w.op + align_up(static_cast<size_t>(n * keyout_tiles(C, Tk) * D * kTileQ * 2));
-    w.total = w.rp + align_up(static_cast<size_t>(n * keyout_tiles(C, Tk) * kTileQ * 4));
+  if (keyout_eligible(C, Tk, Tk - C, D, prec, key_pass)) {
+    const int64_t nb = keyout_batch(n, C, Tk, D);
+    w.rp = w.op + align_up(static_cast<size_t>(nb * keyout_tiles(C, Tk) * D * kTileQ * 2));
+    w.total = w.rp + align_up(static_cast<size_t>(nb * keyout_tiles(C, Tk) * kTileQ * 4));
   }
   return w;
 }
@@ -1067,7 +1087,7 @@ int launch_forward(const ForwardArgs& a) {
   // workspace keeps its room, shared with the three-pass forward's layout)
   constexpr bool kKeyPassBuilt =
       std::is_same_v<CT, __bf16> && D == 64 && BID == BID_SOFTMAX && SHARE == SHARE_INCL;
-  const bool key_pass = kKeyPassBuilt && keyout_eligible(a.n, a.C, a.Tk, a.q0, D, kOperandPrec<CT>, a.key_pass);
+  const bool key_pass = kKeyPassBuilt && keyout_eligible(a.C, a.Tk, a.q0, D, kOperandPrec<CT>, a.key_pass);
   const bool v_rows = key_pass && !convert;
 
   // operands in the compute type; V^T (and K^T) tiles
@@ -1143,13 +1163,33 @@ int launch_forward(const ForwardArgs& a) {
       // order a CU could finish a whole walk after the rest (a prefill chunk of
       // 256 slices at 2048 rows ended ~0.17 ms after its work would balance)
       P.lpt = 1;
-      const dim3 gko(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
-      DIL_TIMED("fwd_keyout", st, (fwd_keyout<D, KW><<<gko, KG::kThreads, 0, st>>>(P, op, rp, ntiles)));
-      slice_batches(a.n, [&](int64_t s0, unsigned ns) {
-        DIL_TIMED("fwd_out_reduce", st,
-                  (fwd_out_reduce<D, KW><<<dim3(nq, ns), kThreads, 0, st>>>(op, rp, ntiles, a.C, a.Tk, a.out,
-                                                                           a.o_sn, a.ssum, s0)));
-      });
+      // slices in batches whose partials fit the workspace (one batch at
+      // every benchmark shape); each batch's pass and reduction see only its
+      // slices, through pointers advanced to its first slice
+      const int64_t batch = keyout_batch(a.n, a.C, a.Tk, D);
+      for (int64_t b0 = 0; b0 < a.n; b0 += batch) {
+        const int64_t nbat = min(batch, a.n - b0);
+        FwdParams B = P;
+        B.n = nbat;
+        B.q = static_cast<const CT*>(P.q) + b0 * P.q_sn;
+        B.k = static_cast<const CT*>(P.k) + b0 * P.k_sn;
+        if (P.v != nullptr) B.v = static_cast<const CT*>(P.v) + b0 * P.v_sn;
+        B.vt = static_cast<const CT*>(P.vt) + b0 * P.t_sn;
+        B.rmax = P.rmax + b0 * P.C;
+        B.rden = P.rden + b0 * P.C;
+        if (P.carry != nullptr) B.carry = P.carry + b0 * P.nb * P.Tk;
+        if (P.demand_in != nullptr) B.demand_in = P.demand_in + b0 * P.din_sn;
+        B.total = P.total + b0 * P.tot_sn;
+        const dim3 gko(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(B.kgroups) * nbat)));
+        DIL_TIMED("fwd_keyout", st, (fwd_keyout<D, KW><<<gko, KG::kThreads, 0, st>>>(B, op, rp, ntiles)));
+        float* out_b = a.out + b0 * a.o_sn;
+        float* ssum_b = a.ssum + b0 * a.C;
+        slice_batches(nbat, [&](int64_t s0, unsigned ns) {
+          DIL_TIMED("fwd_out_reduce", st,
+                    (fwd_out_reduce<D, KW><<<dim3(nq, ns), kThreads, 0, st>>>(op, rp, ntiles, a.C, a.Tk, out_b,
+                                                                             a.o_sn, ssum_b, s0)));
+        });
+      }
       return static_cast<int>(hipGetLastError());
     }
   }

@@ -126,6 +126,11 @@ inline bool forward_key_pass_requested() {
 
 int64_t forward_workspace_bytes(int64_t n, int64_t C, int64_t Tk, int head_dim, int dtype, int prec,
                                 int want_pk, bool key_pass);
+// Whether a forward over rows [q0, q0 + C) against keys [0, Tk) takes the
+// key-parallel output pass, whose demand checkpoints are an output only (the
+// caller may then pass no carry array); the three-pass forward reads them.
+bool forward_takes_key_pass(int64_t C, int64_t Tk, int64_t q0, int head_dim, int prec, const Variant& var,
+                            bool key_pass);
 int forward(const ForwardArgs& a);
 
 struct BackwardArgs {

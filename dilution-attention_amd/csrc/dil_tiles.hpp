@@ -517,9 +517,14 @@ struct WorkItem {
 // with 16 slices of 16 groups per XCD.  Otherwise, or with !longest_first
 // (a kernel with little arithmetic per byte, for which more slices in flight
 // per XCD cost more in L2 misses than the packing gains), the items are
-// split into contiguous ranges, slice by slice.
+// split into contiguous ranges, slice by slice.  With `spread` (a kernel whose
+// items read little that they share) slices that do not divide evenly go out
+// longest first over the whole chip instead: block b takes the rank b / slices
+// of slice b % slices, so every XCD gets its share of the long and the short
+// items (in contiguous ranges, two slices of 512 groups left the XCD holding
+// the longest walks with 7x the work of the one holding the shortest).
 __device__ __forceinline__ WorkItem xcd_work_item(int groups, int64_t slices, bool reverse,
-                                                 bool longest_first = true) {
+                                                 bool longest_first = true, bool spread = false) {
   const int64_t b = blockIdx.x;
   WorkItem w;
   int r;
@@ -528,6 +533,10 @@ __device__ __forceinline__ WorkItem xcd_work_item(int groups, int64_t slices, bo
     w.valid = j < spx * groups;
     r = static_cast<int>(j / spx);
     w.slice = (b % kXcds) * spx + j % spx;
+  } else if (longest_first && spread) {
+    w.valid = b < static_cast<int64_t>(groups) * slices;
+    r = static_cast<int>(b / slices);
+    w.slice = b % slices;
   } else {
     const int64_t total = static_cast<int64_t>(groups) * slices;
     const int64_t per = (total + kXcds - 1) / kXcds;

@@ -23,6 +23,7 @@ _vp = ctypes.c_void_p
 SIGNATURES = {
     "dil_abi_version": (_c_int, []),
     "dil_status_string": (ctypes.c_char_p, [_c_int]),
+    "dil_forward_key_pass": (_c_int, [_c_int64, _c_int64, _c_int, _c_int, _c_int]),
     "dil_forward_workspace_bytes": (_c_int64, [_c_int64, _c_int64, _c_int, _c_int, _c_int, _c_int]),
     "dil_forward": (_c_int, [_vp, _vp, _vp, _c_int64, _c_int64, _c_int, _c_int, _c_int,
                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _vp]),
@@ -62,7 +63,7 @@ SIGNATURES = {
                                  ctypes.POINTER(_c_int64)]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _load_error: str | None = None

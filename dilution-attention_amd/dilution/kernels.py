@@ -197,10 +197,12 @@ def dilution_attention_forward(
     committed_total``.  ``carry`` holds the demand entering every 32-row block
     (``bwd_block_m`` = 32) for the block's causal keys ``j < 32 (b + 1)``; the
     entries past them are left unwritten, as in the reference
-    (kernels.py:353-354; its tests read ``carry[:, b, :end]`` only).  Without return_aux the (batch, head) slices are
-    processed in groups sized so the (rows, T/32, T) fp32 checkpoint scratch
-    stays under scratch_budget_gib; slices are independent, so results are
-    identical.
+    (kernels.py:353-354; its tests read ``carry[:, b, :end]`` only).  Without
+    return_aux no checkpoint is kept: the key-parallel pass (bf16 operands,
+    head_dim 64) writes none, and the three-pass forward processes the
+    (batch, head) slices in groups sized so its (rows, T/32, T) fp32
+    checkpoint scratch stays under scratch_budget_gib; slices are independent,
+    so results are identical either way.
     """
     prec = _precision_code(dot_precision)
     if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
@@ -224,10 +226,16 @@ def dilution_attention_forward(
     pk = torch.empty(n, seq, head_dim, **f32) if _save_pk else None
 
     rows = n
-    if not return_aux:
+    carry = None
+    if return_aux:
+        carry = torch.empty(n, nb, seq, **f32)
+    elif tuple(_variant) != _PRODUCTION or not lib.dil_forward_key_pass(seq, 0, head_dim, _DTYPES[dt], prec):
+        # the three-pass forward reads the checkpoints it writes: the slices go
+        # in groups whose (rows, T/32, T) scratch fits the budget.  The key pass
+        # writes none without aux and takes every slice in one call.
         per_row = nb * seq * 4
         rows = max(1, min(n, int(scratch_budget_gib * 2**30) // max(per_row, 1)))
-    carry = torch.empty(rows, nb, seq, **f32)
+        carry = torch.empty(rows, nb, seq, **f32)
     ws_bytes = lib.dil_forward_workspace_bytes(rows, seq, head_dim, _DTYPES[dt], prec, int(_save_pk))
     ws = _workspace(ws_bytes, dev)
     for a in range(0, n, rows):
@@ -235,7 +243,7 @@ def dilution_attention_forward(
         head = (qf[a:b].data_ptr(), kf[a:b].data_ptr(), vf[a:b].data_ptr(), b - a, seq, head_dim,
                 _DTYPES[dt], prec)
         tail = (out[a:b].data_ptr(), rmax[a:b].data_ptr(), rden[a:b].data_ptr(),
-                ssum[a:b].data_ptr(), carry.data_ptr(), total[a:b].data_ptr(),
+                ssum[a:b].data_ptr(), _ptr(carry), total[a:b].data_ptr(),
                 None if pk is None else pk[a:b].data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
         with _on(dev):
             if tuple(_variant) == _PRODUCTION:
@@ -267,6 +275,10 @@ class _DilutionAttentionFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, dot_precision, block_m, block_n,
                 num_warps, bwd_num_warps, bwd_num_stages, b3_block_n, b3_num_warps, b4_num_warps):
+        if not any(ctx.needs_input_grad[:3]):
+            # no backward can follow: nothing to save, no checkpoints to write
+            return dilution_attention_forward(q, k, v, dot_precision=dot_precision, block_m=block_m,
+                                              block_n=block_n, num_warps=num_warps)
         out, aux = dilution_attention_forward(
             q, k, v, dot_precision=dot_precision, block_m=block_m, block_n=block_n,
             return_aux=True, num_warps=num_warps, _save_pk=any(ctx.needs_input_grad[:3]),
@@ -392,13 +404,16 @@ def dilution_prefill_chunk(
     rmax = torch.empty(n, chunk, **f32)
     rden = torch.empty(n, chunk, **f32)
     ssum = torch.empty(n, chunk, **f32)
-    carry = torch.empty(n, nb, start + chunk, **f32)
+    # the key pass writes the checkpoints only for a caller that keeps them
+    carry = None
+    if return_aux or not lib.dil_forward_key_pass(chunk, start, head_dim, _DTYPES[dt], prec):
+        carry = torch.empty(n, nb, start + chunk, **f32)
     ws = _workspace(lib.dil_prefill_workspace_bytes(n, chunk, start, head_dim, _DTYPES[dt], prec), dev)
     with _on(dev):
         status = lib.dil_prefill_chunk(
             qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), n, chunk, start, capacity, head_dim,
             _DTYPES[dt], prec, cf.data_ptr(), out.data_ptr(), rmax.data_ptr(), rden.data_ptr(),
-            ssum.data_ptr(), carry.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+            ssum.data_ptr(), _ptr(carry), ws.data_ptr(), ws.numel(), _stream(dev))
     _hip.check(status, "dil_prefill_chunk")
     result = out.reshape(batch, heads, chunk, head_dim)
     if return_aux:

@@ -21,14 +21,20 @@
  *                fp32 demand/share math in every mode.
  *   - head_dim in {16, 32, 64, 128}.
  *   - Every launch is asynchronous on `stream` (a hipStream_t); no entry point
- *     synchronises, allocates device memory or keeps state between calls.
- *     Scratch memory is caller-provided (`workspace`, at least the size the
- *     matching *_workspace_bytes query returns, 256-byte aligned).
+ *     synchronises or allocates device memory.  Scratch memory is
+ *     caller-provided (`workspace`, at least the size the matching
+ *     *_workspace_bytes query returns, 256-byte aligned).  The library's only
+ *     state is the optional kernel-timing records (dil_timing_*) and, for
+ *     dil_decode_step_noalloc alone, one static scratch array per GPU.
+ *   - The key-parallel forward's workspace holds at most 24 GiB of output
+ *     partials; a call whose slices need more runs over them in batches, so
+ *     the forward workspace stays bounded at any batch size.
  *   - Return value: 0 on success, a positive hipError_t from the launch, or a
  *     negative argument error (see dil_status_string).  A NULL pointer where
  *     an argument is required is an argument error (-4); only `pk` of
- *     dil_forward may be NULL.  Argument errors are returned before any
- *     launch.
+ *     dil_forward may be NULL, and `carry` of dil_forward and
+ *     dil_prefill_chunk on calls that take the key pass.  Argument errors are
+ *     returned before any launch.
  */
 #ifndef DILUTION_HIP_H
 #define DILUTION_HIP_H
@@ -46,6 +52,18 @@ int dil_abi_version(void);
 const char* dil_status_string(int status);
 
 /*
+ * Whether a dil_forward call (start = 0, chunk = seq) or a dil_prefill_chunk
+ * call of this shape takes the key-parallel output pass: 1 or 0.  Its demand
+ * checkpoints are an output only, so such a call may pass carry = NULL (an
+ * inference forward or a prefill chunk that keeps no aux); the three-pass
+ * forward reads the checkpoints it writes and needs the array.  No reference
+ * counterpart: the reference's forward always writes its carry
+ * (src/dilution/kernels.py:349-355).  Reads DILUTION_FORWARD_KEY_PASS as the
+ * entry points do.
+ */
+int dil_forward_key_pass(int64_t chunk, int64_t start, int head_dim, int dtype, int precision);
+
+/*
  * Forward over a whole sequence, with everything the backward needs.
  * Replaces dilution_attention_forward (src/dilution/kernels.py:328-455) and
  * the launches it makes (_dilution_k1 :137-198, _dilution_scan :251-264,
@@ -61,6 +79,9 @@ const char* dil_status_string(int status);
  *            written for the block's causal keys j < 32*(b+1) only: the
  *            future triangle is left unwritten and never read (as the
  *            reference leaves it, kernels.py:353-354, test_kernels.py:143-149).
+ *            May be NULL when dil_forward_key_pass(seq, 0, ...) is 1: then no
+ *            checkpoint is written (outputs, statistics and totals are the
+ *            same bits).
  * committed_total: (n, seq) float32 column totals of p (the decode demand).
  * pk:        (n, seq, head_dim) float32 (p @ k)/sqrt(head_dim), or NULL.
  */
@@ -87,7 +108,8 @@ int dil_forward(const void* q, const void* k, const void* v, int64_t n, int64_t 
  *            at and beyond start+chunk are not touched.
  * out:       (n, chunk, head_dim) float32.
  * rmax, rden, ssum: (n, chunk) float32; carry: (n, ceil(chunk/32), start+chunk),
- *            written for keys j < start + 32*(b+1) of block b only.
+ *            written for keys j < start + 32*(b+1) of block b only, or NULL
+ *            when dil_forward_key_pass(chunk, start, ...) is 1.
  */
 int64_t dil_prefill_workspace_bytes(int64_t n, int64_t chunk, int64_t start, int head_dim,
                                     int dtype, int precision);

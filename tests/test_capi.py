@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.dil_abi_version() == 3
+    assert lib.dil_abi_version() == 4
     assert lib.dil_status_string(0) == b"success"
     for code in (-1, -2, -3, -4, -5):
         assert lib.dil_status_string(code) != b"unknown status"
@@ -92,6 +92,51 @@ def test_key_pass_switch_sizes_the_workspace(lib, monkeypatch):
     # only the exact value "0" turns it off
     monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "00")
     assert lib.dil_forward_workspace_bytes(2, 300, 64, 1, 2, 1) == on
+
+
+def test_key_pass_query_and_optional_carry(lib, monkeypatch):
+    """dil_forward_key_pass says which calls take the key-parallel pass (bf16
+    operands, head_dim 64, a chunk starting at a multiple of 512 rows); only
+    those may pass carry = NULL.  A NULL carry on a three-pass call is an
+    argument error (-4) before any launch (the stand-in addresses are never
+    dereferenced).  The forward workspace holds the key pass's partials for
+    at most 24 GiB of slices: past that, the call runs in slice batches and
+    the workspace stops growing with the batch."""
+    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS", raising=False)
+    assert lib.dil_forward_key_pass(300, 0, 64, 1, 2) == 1
+    assert lib.dil_forward_key_pass(300, 0, 64, 0, 2) == 1      # fp32 inputs, bf16 operands
+    assert lib.dil_forward_key_pass(2048, 1536, 64, 1, 2) == 1
+    for args in ((300, 0, 64, 1, 0), (300, 0, 64, 1, 1), (300, 0, 32, 1, 2), (300, 0, 128, 1, 2),
+                 (2048, 1000, 64, 1, 2), (300, 0, 48, 1, 2), (0, 0, 64, 1, 2), (300, -512, 64, 1, 2)):
+        assert lib.dil_forward_key_pass(*args) == 0, args
+    monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
+    assert lib.dil_forward_key_pass(300, 0, 64, 1, 2) == 0
+    monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS")
+
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(12)]
+    q, k, v, out, rmax, rden, ssum, tot, ws = fake[:9]
+    big = 1 << 40
+    # fp32 operands: the three-pass forward needs the checkpoints
+    assert lib.dil_forward(q, k, v, 2, 300, 64, 1, 0, out, rmax, rden, ssum, None, tot, None, ws, big,
+                           None) == -4
+    # a prefill chunk at an unaligned start takes the three-pass forward too
+    assert lib.dil_prefill_chunk(q, k, v, 2, 300, 100, 1000, 64, 1, 2, tot, out, rmax, rden, ssum, None, ws,
+                                 big, None) == -4
+
+    # partial room: one 131072-row slice needs ~2.2 GB, so 24 GiB hold 11;
+    # past that the slices go in equal batches (12 -> 6 + 6, 100 -> 10 x 10)
+    def partial_room(n):
+        monkeypatch.setenv("DILUTION_FORWARD_KEY_PASS", "0")
+        off = lib.dil_forward_workspace_bytes(n, 131072, 64, 1, 2, 0)
+        monkeypatch.delenv("DILUTION_FORWARD_KEY_PASS")
+        return lib.dil_forward_workspace_bytes(n, 131072, 64, 1, 2, 0) - off
+
+    one = partial_room(1)
+    assert 2.1e9 < one < 2.3e9
+    assert partial_room(5) >= 5 * one - 1024
+    assert 11 * one - 1024 <= partial_room(11) <= 24 * 2**30
+    assert partial_room(12) == partial_room(6)
+    assert partial_room(100) == partial_room(10)
 
 
 def test_argument_errors_before_any_launch(lib):
@@ -178,12 +223,14 @@ def test_null_pointers_are_argument_errors(lib):
                                         None) == -4, hole
     assert lib.dil_decode_step_dlen(*fake[:5], 1, 8, fake[5], 9, 64, 1, 1, fake[6], big, None) == -4
     assert lib.dil_decode_step_dlen(*fake[:5], 1, 8, fake[5], 8, 64, 1, 1, fake[6], 0, None) == -3
-    # forward: pk may be NULL, nothing else may
+    # forward: pk may be NULL, and carry on a key-pass call (bf16 operands at
+    # head_dim 64), so its hole is tested on an "ieee" (three-pass) call
     fwd_ptrs = fake[:3]
     outs = fake[3:9]                              # out, rmax, rden, ssum, carry, committed_total
     for hole in range(6):
         o = [None if i == hole else outs[i] for i in range(6)]
-        assert lib.dil_forward(*fwd_ptrs, 1, 8, 64, 1, 2, *o, None, fake[9], big, None) == -4, hole
+        prec = 0 if hole == 4 else 2
+        assert lib.dil_forward(*fwd_ptrs, 1, 8, 64, 1, prec, *o, None, fake[9], big, None) == -4, hole
     assert lib.dil_forward(None, *fake[1:3], 1, 8, 64, 1, 2, *outs, None, fake[9], big, None) == -4
     assert lib.dil_forward(*fwd_ptrs, 1, 8, 64, 1, 2, *outs, None, fake[9], 0, None) == -3
     # backward: pk is required there

@@ -350,3 +350,52 @@ def test_prefill_chunks_through_the_key_pass(chunk, monkeypatch):
             assert diff.max().item() < 1e-5, (start, rb)
     assert max_abs(com["key"][:, :, :seq], orc.demand_totals(q, k)) < 1e-5 * 8
     assert com["key"][:, :, seq:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize("seq", [33, 1000, 2048])
+def test_forward_without_aux_keeps_no_checkpoints(seq):
+    """Without aux the key-parallel forward writes no demand checkpoints (the
+    carry array is an output only, for the backward): its outputs are the
+    same bits as the aux forward's.  The autograd forward with no input
+    needing a gradient takes that path, and the three-pass forward ("ieee")
+    still runs without aux (it keeps its own checkpoint scratch)."""
+    from dilution import _hip, kernels
+
+    assert _hip.lib().dil_forward_key_pass(seq, 0, 64, 1, 2) == 1
+    q, k, v = orc.make_inputs((2, 3, seq, 64), seed=40 + seq, qk_scale=0.5, dtype=torch.bfloat16)
+    qg, kg, vg = (x.cuda() for x in (q, k, v))
+    ref, aux = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16", return_aux=True)
+    plain = kernels.dilution_attention_forward(qg, kg, vg, dot_precision="bf16")
+    assert torch.equal(plain, ref)
+    assert torch.equal(kernels.dilution_attention(qg, kg, vg, dot_precision="bf16"), ref)
+    with torch.no_grad():
+        assert torch.equal(kernels.dilution_attention(qg, kg, vg, dot_precision="bf16"), ref)
+    want = orc.attention_fp32(q, k, v)
+    assert max_abs(plain, want) < 2e-2 and mean_rel(plain, want) < 1e-2
+    f32 = [x.float() for x in (qg, kg, vg)]
+    ieee = kernels.dilution_attention_forward(*f32, dot_precision="ieee")
+    assert max_abs(ieee, orc.attention_f64(q.float(), k.float(), v.float())) < 1e-4
+
+
+@pytest.mark.parametrize("chunk", [512, 700])
+def test_prefill_chunk_without_aux_is_identical(chunk):
+    """A prefill chunk without aux writes no checkpoints on the key pass
+    (starts at multiples of 512) and keeps them as scratch on the three-pass
+    forward (other starts): outputs and the carried demand are the same bits
+    as with aux, chunk after chunk."""
+    from dilution import kernels
+
+    batch, heads, seq, d = 1, 4, 2100, 64
+    q, k, v = orc.make_inputs((batch, heads, seq, d), seed=chunk, qk_scale=0.5, dtype=torch.bfloat16)
+    kc = torch.zeros(batch, heads, seq, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:], vc[:] = k.cuda(), v.cuda()
+    com = [torch.zeros(batch, heads, seq, device="cuda") for _ in range(2)]
+    for start in range(0, seq, chunk):
+        stop = min(start + chunk, seq)
+        qc = q[:, :, start:stop].cuda()
+        a, _ = kernels.dilution_prefill_chunk(qc, kc, vc, com[0], start, dot_precision="bf16", return_aux=True)
+        b = kernels.dilution_prefill_chunk(qc, kc, vc, com[1], start, dot_precision="bf16")
+        assert torch.equal(a, b), start
+        assert torch.equal(com[0], com[1]), start
+    assert max_abs(com[1], orc.demand_totals(q, k)) < 1e-5 * 8

@@ -347,6 +347,32 @@ def test_sequence_of_131072_gradients_against_blocked_oracle():
     _check_bf16_grads(grads, want, "all rows / keys")
 
 
+def test_key_pass_slice_batches_at_131072():
+    """B1 H12 T = 131072 bf16, forward without aux (the long-context
+    inference forward): one slice's key-pass partials take ~2.2 GB, so the
+    24 GiB workspace holds 11 slices and the pass runs in two equal slice
+    batches (6 + 6), writing no checkpoint array.  Slices are independent, so
+    each equals, bit for bit, the forward of that slice alone (one batch): the
+    first and last slices of each batch."""
+    from dilution import _hip, kernels
+
+    seq, heads, d = 131072, 12, 64
+    lib = _hip.lib()
+    assert lib.dil_forward_key_pass(seq, 0, d, 1, 2) == 1
+    one_slice = lib.dil_forward_workspace_bytes(1, seq, d, 1, 2, 0)
+    assert lib.dil_forward_workspace_bytes(heads, seq, d, 1, 2, 0) < heads * one_slice
+    g = torch.Generator(device="cuda").manual_seed(9)
+    q, k = ((torch.randn(1, heads, seq, d, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+            for _ in range(2))
+    v = torch.randn(1, heads, seq, d, device="cuda", generator=g).to(torch.bfloat16)
+    out = kernels.dilution_attention_forward(q, k, v, dot_precision="bf16")
+    assert torch.isfinite(out).all()
+    for h in (0, 5, 6, 11):
+        alone = kernels.dilution_attention_forward(*(x[:, h:h + 1].contiguous() for x in (q, k, v)),
+                                                   dot_precision="bf16")
+        assert torch.equal(alone, out[:, h:h + 1]), h
+
+
 def test_sequence_of_131072_far_end_closed_forms():
     """One slice at T = 131072 (bf16), where (T/32) x T checkpoints and T x d
     offsets are far past the benchmark's sizes.  The oracle does not fit, but
