@@ -88,6 +88,9 @@ WORKLOADS = {
     "lm16k": (4, 16, 16384, 64),
     # head_dim 128 at the headline's FLOPs (half the heads)
     "train16k_d128": (1, 8, 16384, 128),
+    # 12 heads (the reference's 209M model) at B1: slices that do not divide
+    # over the 8 XCDs
+    "train16k_h12": (1, 12, 16384, 64),
 }
 
 # Algorithmic products (each B H T^2 d FLOPs causal) that each kernel of the

@@ -970,7 +970,9 @@ __global__ __launch_bounds__(kKqThreads, 2) void bwd_keyq(BwdParams P, KqPart* _
   __shared__ __attribute__((aligned(16))) bf16x8 kpark[D / 16][kKqWaves][64];
   __shared__ __attribute__((aligned(16))) bf16x8 id_park[2][64];       // transpose identity
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
+  // early keys (long walks) first, over the whole chip when the slices do not
+  // divide over the XCDs (spread)
+  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0, true);
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;

@@ -112,7 +112,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_stats(FwdParams P) {
   using T = Tiles<CT, D>;
   __shared__ __attribute__((aligned(16))) CT ktile[2][kTileK * T::kKStride];
   __shared__ __attribute__((aligned(16))) CT kttile[PK ? 2 : 1][PK ? D * T::kTStride : 1];
-  const WorkItem item = xcd_work_item(P.groups, P.n, true, P.lpt != 0);   // heavy (late) row groups first
+  // heavy (late) row groups first, over the whole chip when the slices do not
+  // divide over the XCDs (spread)
+  const WorkItem item = xcd_work_item(P.groups, P.n, true, P.lpt != 0, true);
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int g = item.idx;
