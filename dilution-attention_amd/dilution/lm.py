@@ -22,9 +22,6 @@ weights).  It follows the reference's module layout and cache protocol
   ``forward(idx, targets)`` -> (logits, loss), ``prefill``, ``decode_step``
   and cached greedy / sampled ``generate`` (model.py:342-512, sampling with
   ``filter_logits``, model.py:289-304);
-* ``continuation_nll``: per-token NLL of continuations given their prompts
-  from one causal forward (sampling.py:297-323), the scoring caller of the
-  operator;
 * ``rows_linear``: the decode step's projections at M = batch (<= 8 rows) on
   the HIP library (``dil_rows_linear``), with the RMSNorms, the residual adds
   and the SwiGLU activation folded in: a bf16 model's cached decode step (eager
@@ -631,30 +628,3 @@ def filter_logits(logits: torch.Tensor, top_k: int | None = None, top_p: float |
         vals = vals.masked_fill(mass_before >= top_p, float("-inf"))
         out = torch.empty_like(out).scatter_(-1, order, vals)
     return out
-
-
-@torch.no_grad()
-def continuation_nll(model: DilutionLM, prompts: torch.Tensor, conts) -> list[float]:
-    """Mean per-token NLL (nats) of each continuation given its prompt
-    (sampling.py:297-323): prompts (B, L) share one length, conts are token
-    lists (ragged).  One causal forward over prompt + continuation; the LM
-    head runs on the positions that predict continuation tokens only.  Rows
-    are padded after their continuation, which causal attention never lets
-    reach a scored position; an empty continuation scores NaN."""
-    batch, length = prompts.shape
-    width = max(1, max(len(c) for c in conts))
-    idx = torch.zeros(batch, length + width, dtype=torch.long, device=prompts.device)
-    idx[:, :length] = prompts
-    tgt = torch.full((batch, width), -100, dtype=torch.long, device=prompts.device)
-    for r, c in enumerate(conts):
-        c = torch.as_tensor(list(c), dtype=torch.long, device=prompts.device)
-        idx[r, length:length + len(c)] = c
-        tgt[r, :len(c)] = c
-    h = model.hidden_states(idx)[:, length - 1:length - 1 + width]
-    logits = model.lm_head(h).float()
-    nll = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), tgt.reshape(-1), ignore_index=-100,
-                          reduction="none").view(batch, width)
-    valid = (tgt != -100).float()
-    counts = valid.sum(-1)
-    per_row = (nll * valid).sum(-1) / counts.clamp(min=1)
-    return [float(v) if n > 0 else float("nan") for v, n in zip(per_row.tolist(), counts.tolist())]

@@ -308,27 +308,6 @@ def test_generate_sampling():
         model.generate(idx, 2, vocab_limit=0)
 
 
-@pytest.mark.gpu
-@needs_gpu
-def test_continuation_nll_matches_full_forward():
-    from dilution.lm import continuation_nll
-
-    model = _small()
-    g = torch.Generator().manual_seed(6)
-    prompts = torch.randint(1, 97, (3, 20), generator=g).cuda()
-    conts = [[5, 9, 11, 2], [7], []]
-    got = continuation_nll(model, prompts, conts)
-    for r, c in enumerate(conts):
-        if not c:
-            assert got[r] != got[r]                                   # NaN
-            continue
-        seq = torch.cat([prompts[r], torch.tensor(c, device="cuda")])[None]
-        with torch.no_grad():
-            logits, _ = model(seq[:, :-1], seq[:, 1:])
-        want = torch.nn.functional.cross_entropy(logits[0, -len(c):].float(), seq[0, -len(c):])
-        assert abs(got[r] - want.item()) < 1e-4, r
-
-
 # --- the production operator against its specification --------------------
 
 def _spec_forward(q, k, v, dot_precision="ieee", return_aux=False, **_):
