@@ -86,8 +86,9 @@ WORKLOADS = {
     "train8k": (2, 16, 8192, 64),
     # the whole LM's attention call (B4 H16 at 16K)
     "lm16k": (4, 16, 16384, 64),
-    # head_dim 128 at the headline's FLOPs (half the heads)
+    # head_dim 128 and 256 at the headline's FLOPs (half, a quarter of the heads)
     "train16k_d128": (1, 8, 16384, 128),
+    "train16k_d256": (1, 4, 16384, 256),
     # 12 heads (the reference's 209M model) at B1: slices that do not divide
     # over the 8 XCDs
     "train16k_h12": (1, 12, 16384, 64),

@@ -9,7 +9,10 @@
 
 namespace {
 
-bool valid_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+bool valid_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
+// head_dim 256 runs with bf16 operands only: the fp32 and split-operand tiles
+// of the row-parallel output pass exceed the 160 KB of LDS at that width
+bool valid_head_dim(int d, int precision) { return valid_head_dim(d) && (d < 256 || precision == 2); }
 bool valid_dtype(int t) { return t == 0 || t == 1 || t == 2; }
 bool valid_precision(int p) { return p == 0 || p == 1 || p == 2; }
 
@@ -39,7 +42,9 @@ int dil_abi_version(void) { return 4; }
 const char* dil_status_string(int status) {
   switch (status) {
     case 0: return "success";
-    case dil::kErrHeadDim: return "head_dim must be one of 16, 32, 64, 128";
+    case dil::kErrHeadDim:
+      return "head_dim must be one of 16, 32, 64, 128, or 256 with bf16 operands (the bid / share "
+             "variants: 16-128)";
     case dil::kErrDtype: return "unsupported dtype code";
     case dil::kErrWorkspace: return "workspace smaller than the size query returned";
     case dil::kErrShape: return "invalid shape or length";
@@ -146,7 +151,7 @@ int dil_forward_variant(const void* q, const void* k, const void* v, int64_t n, 
                         float* out, float* rmax, float* rden, float* ssum, float* carry,
                         float* committed_total, float* pk, void* workspace, int64_t workspace_bytes,
                         void* stream) {
-  if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
+  if (!valid_head_dim(head_dim, precision)) return dil::kErrHeadDim;
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
   if (n < 1 || seq < 1) return dil::kErrShape;
@@ -221,7 +226,7 @@ int dil_prefill_chunk(const void* q_chunk, const void* k_cache, const void* v_ca
                       int precision, float* committed, float* out, float* rmax, float* rden,
                       float* ssum, float* carry, void* workspace, int64_t workspace_bytes,
                       void* stream) {
-  if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
+  if (!valid_head_dim(head_dim, precision)) return dil::kErrHeadDim;
   if (!valid_dtype(dtype)) return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;
   if (n < 1 || chunk < 1 || start < 0 || start + chunk > capacity) return dil::kErrShape;
@@ -277,7 +282,7 @@ int dil_backward_variant(const void* q, const void* k, const void* v, const void
                          int64_t seq, int head_dim, int dtype, int dout_dtype, int grad_dtype,
                          int precision, int bid, int share, float shift, void* dq, void* dk,
                          void* dv, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (!valid_head_dim(head_dim)) return dil::kErrHeadDim;
+  if (!valid_head_dim(head_dim, precision)) return dil::kErrHeadDim;
   if (!valid_dtype(dtype) || !valid_dtype(dout_dtype) || !valid_dtype(grad_dtype))
     return dil::kErrDtype;
   if (!valid_precision(precision)) return dil::kErrPrecision;

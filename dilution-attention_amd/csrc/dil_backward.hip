@@ -1,6 +1,7 @@
-// Entry points of the backward: the production operator for every head_dim;
-// the ablation variants are built in dil_variants.hip (head_dim 64) and
-// reached through backward_bid<BID>.
+// Entry points of the backward: the production operator for head_dim 16-128
+// in every precision and for 256 with bf16 operands; the ablation variants are
+// built in dil_variants.hip (head_dim 16-128) and reached through
+// backward_bid<BID>.
 #include "dil_backward_impl.hpp"
 
 namespace dil {
@@ -43,6 +44,7 @@ int backward(const BackwardArgs& a) {
     case 32: return dispatch_backward<32>(a);
     case 64: return dispatch_backward<64>(a);
     case 128: return dispatch_backward<128>(a);
+    case 256: return a.prec == 2 ? launch_backward<__bf16, 256>(a) : kErrHeadDim;
     default: return kErrHeadDim;
   }
 }

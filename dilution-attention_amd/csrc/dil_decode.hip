@@ -1,6 +1,6 @@
 // Entry points of the cached decode step: the production operator for every
-// head_dim and dtype; the ablation variants are built in dil_variants.hip
-// (every head_dim) and reached through decode_bid<BID>.
+// head_dim (16-256) and dtype; the ablation variants are built in
+// dil_variants.hip (head_dim 16-128) and reached through decode_bid<BID>.
 #include "dil_decode_impl.hpp"
 
 namespace dil {
@@ -43,6 +43,7 @@ int decode_step(const DecodeArgs& a) {
     case 32: return decode_dtype<32>(a);
     case 64: return decode_dtype<64>(a);
     case 128: return decode_dtype<128>(a);
+    case 256: return decode_dtype<256>(a);
     default: return kErrHeadDim;
   }
 }

@@ -91,7 +91,8 @@ struct DecLayout {
 };
 
 // Sum over the kLanesPerRow lanes that share one cached row, with DPP lane
-// moves (no LDS traffic).  The full sum is guaranteed only in the first lane
+// moves within a 16-lane row (no LDS traffic) and, for 32 lanes, one lane
+// shuffle across two rows.  The full sum is guaranteed only in the first lane
 // of each row group (lane % LPR == 0), the only lane that consumes it.
 template <int LPR>
 __device__ __forceinline__ float row_reduce(float x) {
@@ -107,6 +108,7 @@ __device__ __forceinline__ float row_reduce(float x) {
     x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowShl4, 0xF, 0xF, true));
   if constexpr (LPR >= 16)
     x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kRowShl8, 0xF, 0xF, true));
+  if constexpr (LPR >= 32) x += __shfl_down(x, 16, 64);   // across the two 16-lane DPP rows (head_dim 256)
   return x;
 }
 
@@ -349,10 +351,12 @@ __global__ __launch_bounds__(kDecThreads) void dec_apply(
   }
 }
 
-// One workgroup (256 threads > D) per slice: thread d < D sums column d of
-// the chunk partials, thread D the share totals, four chunks at a time.
+// One workgroup (more threads than D) per slice: thread d < D sums column d
+// of the chunk partials, thread D the share totals, four chunks at a time.
 template <int D>
-__global__ __launch_bounds__(256) void dec_finish(const float* __restrict__ part_out, int nchunk,
+constexpr int dec_finish_threads() { return D < 256 ? 256 : D + 64; }
+template <int D>
+__global__ __launch_bounds__(dec_finish_threads<D>()) void dec_finish(const float* __restrict__ part_out, int nchunk,
                                                   void* __restrict__ out, int64_t o_sn, int dt,
                                                   int64_t length, int64_t chunk,
                                                   const int64_t* __restrict__ dlen) {
@@ -419,7 +423,7 @@ int launch_decode(const DecodeArgs& a) {
                   a.var.shift, s0, a.n, a.dlen)));
   });
   DIL_TIMED("dec_finish", st,
-            dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), 256, 0, st>>>(part_out, nchunk, a.out,
+            dec_finish<D><<<dim3(static_cast<unsigned>(a.n)), dec_finish_threads<D>(), 0, st>>>(part_out, nchunk, a.out,
                                                                              a.o_sn, a.q_dtype, a.length,
                                                                              chunk, a.dlen));
   return static_cast<int>(hipGetLastError());

@@ -1,7 +1,7 @@
 // Entry points of the forward (plain forward and chunked prefill): the
-// production operator for every head_dim; the ablation variants are built in
-// dil_variants.hip (head_dim 16, 32, 64 and 128) and reached through
-// forward_bid<BID>.
+// production operator for head_dim 16-128 in every precision and for 256 with
+// bf16 operands; the ablation variants are built in dil_variants.hip (head_dim
+// 16, 32, 64 and 128) and reached through forward_bid<BID>.
 #include "dil_forward_impl.hpp"
 
 namespace dil {
@@ -51,6 +51,7 @@ int forward(const ForwardArgs& a) {
     case 32: return dispatch_forward<32>(a);
     case 64: return dispatch_forward<64>(a);
     case 128: return dispatch_forward<128>(a);
+    case 256: return a.prec == 2 ? launch_forward<__bf16, 256>(a) : kErrHeadDim;
     default: return kErrHeadDim;
   }
 }

@@ -63,7 +63,7 @@ extern "C" int dil_decode_step_noalloc(const void* q1, const void* k_cache, cons
                                        float* committed, void* out, int64_t n, int64_t capacity,
                                        int64_t length, int head_dim, int dtype, int q_dtype,
                                        void* stream) {
-  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128))
+  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256))
     return dil::kErrHeadDim;
   if (dtype < 0 || dtype > 2 || q_dtype < 0 || q_dtype > 2) return dil::kErrDtype;
   if (n < 1 || length < 1 || length > capacity) return dil::kErrShape;

@@ -48,19 +48,26 @@ _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 # through dilution.kernels_bid)
 _PRODUCTION = (0, 1, 1.0)
 _PRECISIONS = {"ieee": 0, "tf32": 1, "bf16": 2}
-_HEAD_DIMS = (16, 32, 64, 128)
+_HEAD_DIMS = (16, 32, 64, 128, 256)
 # The head widths the gfx950 kernels are built for.  The reference's model
-# routes every power of two >= 16 to its kernels (model.py:158-165); at 256 and
-# above this build's register-resident tiles (per wave, the dk and dv
-# accumulators alone are 256 fp32 registers per lane at head_dim 256) do not
-# fit, so a caller narrows its routing with head_dim_supported() and keeps its
-# eager path for wider heads.
+# routes every power of two >= 16 to its kernels (model.py:158-165).  Here
+# 16-128 run in every dot precision; 256 runs with bf16 operands (the forward,
+# prefill and backward; the decode step takes every cache dtype), since the
+# fp32 and split-operand tiles of the row-parallel output pass exceed the LDS
+# at that width; 512 and wider are not built.  A caller narrows its routing
+# with head_dim_supported(head_dim, dot_precision) and keeps its eager path
+# for the rest.
 SUPPORTED_HEAD_DIMS = _HEAD_DIMS
+_BF16_ONLY_HEAD_DIMS = (256,)
 
 
-def head_dim_supported(head_dim: int) -> bool:
-    """Whether the HIP kernels take this head width (16, 32, 64 or 128)."""
-    return int(head_dim) in _HEAD_DIMS
+def head_dim_supported(head_dim: int, dot_precision: str = "bf16") -> bool:
+    """Whether the HIP kernels take this head width at this dot precision
+    (16, 32, 64 or 128 in every precision; 256 with "bf16")."""
+    head_dim = int(head_dim)
+    if head_dim not in _HEAD_DIMS:
+        return False
+    return head_dim not in _BF16_ONLY_HEAD_DIMS or dot_precision == "bf16"
 
 
 def dilution_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -122,12 +129,17 @@ def _check_cache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return capacity
 
 
-def _check_head_dim(head_dim: int) -> None:
+def _check_head_dim(head_dim: int, dot_precision: str | None = None) -> None:
+    """ValueError unless the kernels take this width (at this dot precision;
+    None: the decode step, which has none)."""
     if head_dim & (head_dim - 1):
         raise ValueError("head_dim must be a power of two")
     if head_dim not in _HEAD_DIMS:
         raise ValueError(f"head_dim must be one of {_HEAD_DIMS} on the gfx950 kernels "
                          f"(head_dim_supported(); got {head_dim})")
+    if dot_precision is not None and head_dim in _BF16_ONLY_HEAD_DIMS and dot_precision != "bf16":
+        raise ValueError(f"head_dim {head_dim} runs with dot_precision='bf16' only on the gfx950 kernels "
+                         f"(head_dim_supported(); got {dot_precision!r})")
 
 
 def _common_dtype(*ts: torch.Tensor) -> torch.dtype:
@@ -209,7 +221,7 @@ def dilution_attention_forward(
         raise ValueError(f"q, k, v must share one (B, H, T, D) shape, got {tuple(q.shape)}, "
                          f"{tuple(k.shape)}, {tuple(v.shape)}")
     batch, heads, seq, head_dim = q.shape
-    _check_head_dim(head_dim)
+    _check_head_dim(head_dim, dot_precision)
     _check_device(q, k, v)
     lib = _hip.lib()
     n = batch * heads
@@ -384,7 +396,7 @@ def dilution_prefill_chunk(
     prec = _precision_code(dot_precision)
     capacity = _check_cache(q, k_cache, v_cache, committed)
     batch, heads, chunk, head_dim = q.shape
-    _check_head_dim(head_dim)
+    _check_head_dim(head_dim, dot_precision)
     if start < 0 or start + chunk > capacity:
         raise ValueError(f"rows [{start}, {start + chunk}) outside cache capacity {capacity}")
     _check_device(q, k_cache, v_cache, committed)

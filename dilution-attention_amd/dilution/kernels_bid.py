@@ -34,7 +34,8 @@ HAS_HIP = _k.HAS_HIP
 BID_TYPES = ("softmax", "relu", "relu2", "softplus", "minshift", "sigmoid", "expshift", "sigshift")
 
 VARIANT_HEAD_DIMS = (16, 32, 64, 128)
-"""head dims the ablation variants are built for (those of the production operator)."""
+"""head dims the ablation variants are built for (the production operator's in
+every precision; it also takes 256 with bf16 operands, the variants do not)."""
 
 
 def head_dim_supported(head_dim: int) -> bool:

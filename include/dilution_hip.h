@@ -19,7 +19,10 @@
  *                operand; the *_variant entry points run it as "ieee"),
  *                2 = "bf16" (bf16 MFMA operands).  fp32 accumulation and
  *                fp32 demand/share math in every mode.
- *   - head_dim in {16, 32, 64, 128}.
+ *   - head_dim in {16, 32, 64, 128}, and 256 with bf16 operands (precision 2)
+ *     for the forward, prefill and backward and with every cache dtype for the
+ *     decode steps; the *_variant entry points take 16-128.  Other widths are
+ *     an argument error (-1).
  *   - Every launch is asynchronous on `stream` (a hipStream_t); no entry point
  *     synchronises or allocates device memory.  Scratch memory is
  *     caller-provided (`workspace`, at least the size the matching

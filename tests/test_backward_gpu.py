@@ -80,9 +80,9 @@ def test_backward_bf16_matches_oracle(seq):
         _check_bf16(name, g, w)
 
 
-@pytest.mark.parametrize("head_dim", [16, 32, 128])
+@pytest.mark.parametrize("head_dim", [16, 32, 128, 256])
 def test_backward_bf16_head_dims(head_dim):
-    # head_dim 16 and 32 run the parked row pass, 128 the register form
+    # head_dim 16 and 32 run the parked row pass, 128 and 256 the register form
     q, k, v, do = orc.make_inputs((1, 2, 200, head_dim), seed=40 + head_dim, qk_scale=0.5,
                                   with_dout=True, dtype=torch.bfloat16)
     out, grads = _run(q, k, v, do, "bf16")
@@ -145,7 +145,7 @@ def test_backward_grad_dtypes_follow_inputs():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("head_dim", [32, 64, 128, 256])
 def test_backward_converted_operands_match_oracle(dtype, head_dim):
     """fp32 or fp16 inputs with dot_precision="bf16": the backward converts q,
     k, v (and dO) to bf16 operands in its preparation launch (the z = 3 job
@@ -159,4 +159,17 @@ def test_backward_converted_operands_match_oracle(dtype, head_dim):
     assert max_abs(out, orc.attention_f64(q, k, v)) < 5e-2
     for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         assert g.dtype == dtype, name
+        _check_bf16(name, g, w)
+
+
+def test_backward_head_dim_256_many_key_tiles():
+    """head_dim 256 over 1025 rows (33 key tiles, 33 row tiles: the suffix
+    checkpoints, the diagonal peel and a ragged last tile) against the
+    closed-form fp64 oracle at the bf16 bounds."""
+    q, k, v, do = orc.make_inputs((1, 2, 1025, 256), seed=256, qk_scale=0.5, with_dout=True,
+                                  dtype=torch.bfloat16)
+    out, grads = _run(q, k, v, do, "bf16")
+    want, _ = orc.grads_closed_form_f64(*(t.double().numpy() for t in (q, k, v, do)))
+    assert max_abs(out, orc.attention_f64(q, k, v)) < 2e-2
+    for name, g, w in zip(("dq", "dk", "dv"), grads, want):
         _check_bf16(name, g, w)

@@ -309,22 +309,31 @@ def test_tensors_on_two_devices_are_rejected():
         kernels._check_device(on(0), torch.zeros(1))
 
 
-def test_head_dims_beyond_128_are_rejected_before_any_launch():
+def test_head_dim_support_and_rejections_before_any_launch():
     """The reference's model routes every power-of-two head_dim >= 16 to its
-    kernels (model.py:158-165).  The gfx950 kernels take 16-128;
-    head_dim_supported() is the predicate a caller narrows its routing with,
-    and wider heads raise ValueError on the host from every entry point (the
-    reference model then keeps its eager path for them, model.py:182-257)."""
-    import torch
-    from dilution import kernels
+    kernels (model.py:158-165).  The gfx950 kernels take 16-128 in every dot
+    precision and 256 with bf16 operands (the decode step at 256 with any
+    cache dtype); head_dim_supported(d, dot_precision) is the predicate a
+    caller narrows its routing with.  Other widths, and 256 with "ieee" or
+    "tf32", raise ValueError on the host (the reference model then keeps its
+    eager path for them, model.py:182-257); the C ABI returns -1 before any
+    launch (the stand-in addresses are never dereferenced)."""
+    import ctypes
 
-    assert kernels.SUPPORTED_HEAD_DIMS == (16, 32, 64, 128)
-    assert all(kernels.head_dim_supported(d) for d in (16, 32, 64, 128))
-    assert not any(kernels.head_dim_supported(d) for d in (8, 48, 256, 512))
-    for d in (256, 512, 8):
+    import torch
+    from dilution import _hip, kernels, kernels_bid
+
+    assert kernels.SUPPORTED_HEAD_DIMS == (16, 32, 64, 128, 256)
+    for prec in ("bf16", "tf32", "ieee"):
+        assert all(kernels.head_dim_supported(d, prec) for d in (16, 32, 64, 128))
+        assert not any(kernels.head_dim_supported(d, prec) for d in (8, 48, 512))
+        assert kernels.head_dim_supported(256, prec) == (prec == "bf16")
+    assert kernels.head_dim_supported(256)
+    assert not kernels_bid.head_dim_supported(256)
+    for d in (512, 8):
         x = torch.zeros(1, 2, 4, d)
         with pytest.raises(ValueError, match="head_dim"):
-            kernels.dilution_attention_forward(x, x, x)
+            kernels.dilution_attention_forward(x, x, x, dot_precision="bf16")
         with pytest.raises(ValueError, match="head_dim"):
             kernels.dilution_attention(x, x, x)
         kc, com = torch.zeros(1, 2, 8, d), torch.zeros(1, 2, 8)
@@ -332,3 +341,27 @@ def test_head_dims_beyond_128_are_rejected_before_any_launch():
             kernels.dilution_decode_step(torch.zeros(1, 2, 1, d), kc, kc, com, 4)
         with pytest.raises(ValueError, match="head_dim"):
             kernels.dilution_prefill_chunk(x, kc, kc, com, 0)
+    x = torch.zeros(1, 2, 4, 256)
+    kc, com = torch.zeros(1, 2, 8, 256), torch.zeros(1, 2, 8)
+    for prec in ("ieee", "tf32"):
+        with pytest.raises(ValueError, match="head_dim 256"):
+            kernels.dilution_attention_forward(x, x, x, dot_precision=prec)
+        with pytest.raises(ValueError, match="head_dim 256"):
+            kernels.dilution_attention(x, x, x, dot_precision=prec)
+        with pytest.raises(ValueError, match="head_dim 256"):
+            kernels.dilution_prefill_chunk(x, kc, kc, com, 0, dot_precision=prec)
+    with pytest.raises(ValueError, match="head_dim"):
+        kernels_bid.dilution_attention_forward(x, x, x, bid="relu")
+
+    lib = _hip.lib()
+    f = [ctypes.c_void_p(4096 * (i + 1)) for i in range(14)]
+    big = 1 << 40
+    for prec, want in ((0, -1), (1, -1)):
+        assert lib.dil_forward(*f[:3], 1, 8, 256, 1, prec, *f[3:9], None, f[9], big, None) == want
+        assert lib.dil_prefill_chunk(*f[:3], 1, 8, 0, 16, 256, 1, prec, *f[3:9], f[9], big, None) == want
+        assert lib.dil_backward(*f[:10], 1, 8, 256, 1, 1, 1, prec, *f[10:13], f[13], big, None) == want
+    assert lib.dil_decode_step(*f[:5], 1, 8, 4, 512, 1, 1, f[5], big, None) == -1
+    # a bid / share variant at 256 (bf16 operands): its instantiations stop at 128
+    assert lib.dil_forward_variant(*f[:3], 1, 8, 256, 1, 2, 1, 1, 1.0, *f[3:9], None, f[9], big,
+                                   None) == -1
+    assert lib.dil_decode_step_noalloc(*f[:5], 1, 8, 4, 512, 1, 1, None) == -1

@@ -118,7 +118,7 @@ def test_decode_query_keeps_its_dtype(qdt, cdt, tol):
     assert comg[..., length:].abs().max().item() == 0
 
 
-@pytest.mark.parametrize("dtype,head_dim", [(torch.bfloat16, 64), (torch.float32, 128)])
+@pytest.mark.parametrize("dtype,head_dim", [(torch.bfloat16, 64), (torch.float32, 128), (torch.bfloat16, 256)])
 def test_device_length_decode_is_the_decode_step(dtype, head_dim):
     """decode_step_device_length (the length read from device memory, grid
     and workspace sized for max_length) against dilution_decode_step at the
@@ -197,3 +197,32 @@ def test_device_length_decode_clamps_the_live_length():
         kernels.decode_step_device_length(q1, kc, vc, c_zero, torch.tensor([5], device="cuda"), cap + 1)
     with pytest.raises(ValueError):
         kernels.decode_step_device_length(q1, kc, vc, c_zero, torch.tensor([5.0], device="cuda"), 10)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_decode_head_dim_256_rows(dtype):
+    """The decode step at head_dim 256 (every cache dtype) from a prefix
+    demand the oracle supplies, step after step against the fp64 oracle of the
+    whole sequence; the demand against the oracle's totals (1e-5); spare
+    capacity untouched."""
+    from dilution import kernels
+
+    batch, heads, prefix, steps, d = 2, 2, 40, 5, 256
+    total = prefix + steps
+    q, k, v = orc.make_inputs((batch, heads, total, d), seed=2560)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    full = orc.attention_f64(q, k, v)
+    capacity = total + 3
+    kc = torch.zeros(batch, heads, capacity, d, device="cuda", dtype=dtype)
+    vc = torch.zeros_like(kc)
+    committed = torch.zeros(batch, heads, capacity, device="cuda")
+    committed[:, :, :prefix] = orc.demand_totals(q[:, :, :prefix], k[:, :, :prefix]).float().cuda()
+    kc[:, :, :prefix], vc[:, :, :prefix] = k[:, :, :prefix].cuda(), v[:, :, :prefix].cuda()
+    tol = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-3}[dtype]
+    for t in range(prefix, total):
+        kc[:, :, t], vc[:, :, t] = k[:, :, t].cuda(), v[:, :, t].cuda()
+        out = kernels.dilution_decode_step(q[:, :, t:t + 1].cuda(), kc, vc, committed, t + 1)
+        assert out.dtype == dtype and out.shape == (batch, heads, 1, d)
+        assert max_abs(out[:, :, 0], full[:, :, t]) < tol, t
+    assert max_abs(committed[:, :, :total], orc.demand_totals(q, k)) < 1e-5 * 4
+    assert committed[:, :, total:].abs().max().item() == 0

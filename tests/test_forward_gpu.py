@@ -45,7 +45,7 @@ def test_forward_fp32_head_dims(head_dim, prec):
 
 
 @pytest.mark.parametrize("seq", [1, 64, 257, 2048])
-@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("head_dim", [32, 64, 128, 256])
 def test_forward_bf16_matches_oracle(seq, head_dim):
     from dilution import kernels
 
@@ -399,3 +399,36 @@ def test_prefill_chunk_without_aux_is_identical(chunk):
         assert torch.equal(a, b), start
         assert torch.equal(com[0], com[1]), start
     assert max_abs(com[1], orc.demand_totals(q, k)) < 1e-5 * 8
+
+
+@pytest.mark.parametrize("chunk", [100, 512])
+def test_head_dim_256_prefill_and_aux(chunk):
+    """head_dim 256 (bf16 operands, the three-pass forward): chunked prefill
+    chunk after chunk against the fp64 oracle of the whole sequence (bf16
+    bounds), the carried demand against the oracle's totals (1e-5 relative),
+    and the aux forward's pk, totals and causal checkpoints against the
+    oracle (pk within bf16 rounding of p and k)."""
+    from dilution import kernels
+
+    batch, heads, seq, d = 1, 2, 700, 256
+    q, k, v = orc.make_inputs((batch, heads, seq, d), seed=chunk + 256, qk_scale=0.5, dtype=torch.bfloat16)
+    full = orc.attention_f64(q, k, v)
+    kc, vc = (x.cuda().contiguous() for x in (k, v))
+    com = torch.zeros(batch, heads, seq, device="cuda")
+    for start in range(0, seq, chunk):
+        stop = min(start + chunk, seq)
+        out = kernels.dilution_prefill_chunk(q[:, :, start:stop].cuda(), kc, vc, com, start, dot_precision="bf16")
+        assert max_abs(out, full[:, :, start:stop]) < 2e-2, start
+        assert mean_rel(out, full[:, :, start:stop]) < 1e-2, start
+    tot = orc.demand_totals(q, k)
+    assert ((com.cpu().double() - tot.double()).abs() / tot.double().abs().clamp(min=1.0)).max().item() < 1e-5
+    out, aux = kernels.dilution_attention_forward(q.cuda(), k.cuda(), v.cuda(), dot_precision="bf16",
+                                                  return_aux=True, _save_pk=True)
+    assert max_abs(out, full) < 2e-2
+    assert max_abs(aux["committed_total"], tot) < 1e-5 * 8
+    assert max_abs(aux["pk"].reshape(batch, heads, seq, d), orc.pk(q, k)) < 2e-2
+    carry = aux["carry"].reshape(batch, heads, -1, seq)
+    want = orc.carry_checkpoints(q, k, 32)
+    for rb in range(carry.shape[2]):
+        end = min(32 * (rb + 1), seq)
+        assert max_abs(carry[:, :, rb, :end], want[:, :, rb, :end]) < 1e-5 * 8, rb

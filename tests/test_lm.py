@@ -293,6 +293,50 @@ def test_generate_graph_matches_eager(dtype):
 
 @pytest.mark.gpu
 @needs_gpu
+def test_head_dim_256_bf16_model():
+    """A bf16 model with head_dim 256 (d_model 512, 2 heads: the reference
+    routes it to its kernels, model.py:158-165) runs on the HIP operator: a
+    finite training step, cached decode against the full forward within bf16
+    rounding of the logits, every replay of the captured decode step bitwise
+    the eager step, and replayed greedy generation equal to eager."""
+    from dilution.lm import DilutionLM, GraphDecoder, LMConfig
+
+    cfg = LMConfig(vocab_size=97, n_layers=2, d_model=512, n_heads=2, prefill_chunk=16)
+    torch.manual_seed(0)
+    model = DilutionLM(cfg).to(device="cuda", dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(7)
+    idx = torch.randint(0, 97, (2, 48), generator=g).cuda()
+    _, loss = model.train()(idx[:, :-1], idx[:, 1:])
+    loss.backward()
+    assert torch.isfinite(loss)
+    for name, p in model.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name
+    model.eval()
+    prompt = 37
+    with torch.no_grad():
+        full = model.lm_head(model.ln_f(_hidden(model, idx))).float()
+        scale = full.abs().max().item()
+        logits, caches = model.prefill(idx[:, :prompt], capacity=idx.shape[1])
+        assert (logits[:, 0].float() - full[:, prompt - 1]).abs().max().item() < 5e-2 * scale
+        for t in range(prompt, idx.shape[1]):
+            logits = model.decode_step(idx[:, t:t + 1], caches)
+            assert (logits[:, 0].float() - full[:, t]).abs().max().item() < 5e-2 * scale, t
+        logits_e, caches_e = model.prefill(idx[:, :prompt], capacity=prompt + 6)
+        _, caches_g = model.prefill(idx[:, :prompt], capacity=prompt + 6)
+        tok = logits_e[:, -1, :].float().argmax(dim=-1, keepdim=True)
+        dec = GraphDecoder(model, caches_g, tok)
+        for step in range(6):
+            le = model.decode_step(tok, caches_e)
+            dec.step()
+            torch.cuda.synchronize()
+            assert torch.equal(dec.logits, le), step
+            tok = le[:, -1, :].float().argmax(dim=-1, keepdim=True)
+    start = torch.zeros(2, 5, dtype=torch.long, device="cuda")
+    assert torch.equal(model.generate(start, 7, graph=True), model.generate(start, 7))
+
+
+@pytest.mark.gpu
+@needs_gpu
 def test_generate_sampling():
     model = _small()
     idx = torch.zeros(2, 5, dtype=torch.long, device="cuda")
