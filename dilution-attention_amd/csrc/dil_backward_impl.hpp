@@ -247,24 +247,39 @@ constexpr int query_waves() {
 // ---------------------------------------------------------------------------
 // key-parallel reverse pass: dv, dk_main, suffix checkpoints
 
+// At head_dim 256 the dk and dv accumulators of a wave's 32 keys (256 fp32
+// registers a lane) do not fit beside the key and value fragments and the
+// chain: SPLIT workgroups then share a key group, each accumulating dk and dv
+// for D / SPLIT of the head dims while recomputing the whole chain (the score
+// products run over all D).  The first of them stores the suffix checkpoints.
+template <typename CT, int D> constexpr int key_split() { return D > 128 ? 2 : 1; }
+
 template <typename CT, int D, int BID = BID_SOFTMAX, int SHARE = SHARE_INCL>
 __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(BwdParams P) {
   using TL = Tiles<CT, D>;
+  constexpr int kSplit = key_split<CT, D>();
+  constexpr int kDH = D / kSplit;                     // head dims of dk / dv this workgroup forms
+  constexpr int kDT = kDTiles<kDH>;                   // ... in 32-dim tiles
   constexpr int kNS = BID == BID_SOFTMAX ? 2 : 3;                // per-row statistics staged
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
   __shared__ __attribute__((aligned(16))) CT do_s[2][kTileQ * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT qt_s[2][D * TL::kTStride];
-  __shared__ __attribute__((aligned(16))) CT dot_s[2][D * TL::kTStride];
+  // the transposed row tiles hold the workgroup's kDH head dims only
+  __shared__ __attribute__((aligned(16))) CT qt_s[2][kDH * TL::kTStride];
+  __shared__ __attribute__((aligned(16))) CT dot_s[2][kDH * TL::kTStride];
   // lse (r0), -dbs, r1, then padding: every thread of the stash writes a slot
   __shared__ __attribute__((aligned(16))) float st_s[2][kThreads];
   __shared__ float cs_s[2][kThreads];             // demand checkpoints of the 128 keys, then padding
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, P.lpt != 0);   // early keys (long walks) first
+  // early keys (long walks) first; with a head-dim split, both parts of a
+  // key group go out together
+  const WorkItem item = xcd_work_item(P.kgroups * kSplit, P.n, false, P.lpt != 0);
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const float hf = static_cast<float>(h);
-  const int kb0 = item.idx * 4;
+  const int part = item.idx % kSplit;            // which D / kSplit head dims of dk and dv
+  const int t0 = part * kDT;                     // first 32-dim tile of them
+  const int kb0 = (item.idx / kSplit) * 4;
   const int kb = kb0 + wave;                     // key tile of this wave
   const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
   const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
@@ -286,31 +301,33 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     zero_row_frag<CT, D>(kf);
     zero_row_frag<CT, D>(vf);
   }
-  floatx16 dka[kDTiles<D>], dva[kDTiles<D>];
+  floatx16 dka[kDT], dva[kDT];
 #pragma unroll
-  for (int t = 0; t < kDTiles<D>; ++t) {
+  for (int t = 0; t < kDT; ++t) {
     dka[t] = floatx16{};
     dva[t] = floatx16{};
   }
   float sufk = 0.f;
   float* sufk_col = P.sufk + slice * P.nb * P.T + key;
+  const bool store_suffix = part == 0;           // wave-uniform
 
   // a stage: the Q and dO' row tiles, their transposes, the row statistics and
   // the demand checkpoints of the workgroup's 128 keys entering the tile
   KTileLoader<CT, D, true> ql, dl;        // row tiles in query-split slot order
-  TTileLoader<CT, D> qtl, dtl;
+  TTileLoader<CT, kDH, kLoadBuffer, D> qtl, dtl;   // head dims [t0 * 32, t0 * 32 + kDH) of the transposes
   RowStatsLoader<kNS> sl;
   if constexpr (!bid_log2<BID>()) sl.pad0 = 0.f;
   const int64_t ck = static_cast<int64_t>(kb0) * kTileK + (threadIdx.x & (4 * kTileK - 1));
   const bool ck_ok = ck < P.T;
   const float* ccol = P.carry + slice * P.nb * P.T + min(ck, P.T - 1);
   float cr = 0.f;
+  const int64_t t_off = static_cast<int64_t>(t0) * 32 * kTileK;   // the first taken head dim within a tile
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
     dl.load(dos, row0, P.T);
-    qtl.load(qts, row0);
-    dtl.load(dots, row0);
+    qtl.load(qts + t_off, row0);
+    dtl.load(dots + t_off, row0);
     sl.load(lse, dbs, BID == BID_SOFTMAX ? dbs : P.rb1 + slice * P.T, row0, P.T);
     cr = ccol[static_cast<int64_t>(qt) * P.T];
   };
@@ -328,15 +345,24 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     constexpr bool DIAG = decltype(diag_tag)::value;
     const float* st = st_s[buf];
     const float cin = cs_s[buf][wave * kTileK + l32];   // demand entering the tile
-    RowFrag<CT, D> qf, dof;
-    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
-    lds_row_frag<CT, D>(dof, do_s[buf], l32, h);
     float lz[16], ndb[16];
     lds_read16(st + kTileQ + 16 * h, ndb);
     // both score-shaped products first; ds = dO' V^T - dbs starts from -dbs
-    // and runs under the p / demand chain
-    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
-    const floatx16 dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
+    // and runs under the p / demand chain.  Slot l32 of a row tile holds row
+    // qsig(l32); with a head-dim split (head_dim 256) the Q and dO' operands
+    // are read per instruction instead of whole
+    floatx16 sacc, dov;
+    if constexpr (kSplit > 1) {
+      const int off = l32 * TL::kKStride + h * (D / 2);
+      sacc = mma_rows_src<CT, D>(q_s[buf] + off, kf, floatx16{});
+      dov = mma_rows_src<CT, D>(do_s[buf] + off, vf, as_x16(ndb));
+    } else {
+      RowFrag<CT, D> qf, dof;
+      lds_row_frag<CT, D>(qf, q_s[buf], l32, h);
+      lds_row_frag<CT, D>(dof, do_s[buf], l32, h);
+      sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+      dov = mma_rows<CT, D>(dof, vf, as_x16(ndb));
+    }
     lds_read16(st + 16 * h, lz);
     float p[16], x[16], jac[16];
     if constexpr (BID == BID_SOFTMAX) {
@@ -380,8 +406,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     for (int s = 0; s < kSteps; ++s) {
       const auto bfr = acc_frag<CT>(sh, s);
 #pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dva[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
+      for (int t = 0; t < kDT; ++t)
+        dva[t] = Mma<CT>::mma(lds_tq_frag<CT, kDH>(dot_s[buf], 32 * t + l32, h, s), bfr, dva[t]);
     }
     if constexpr (is_production<BID, SHARE>()) {
 #pragma unroll
@@ -422,8 +448,8 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     for (int s = 0; s < kSteps; ++s) {
       const auto bfr = acc_frag<CT>(w, s);
 #pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dka[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
+      for (int t = 0; t < kDT; ++t)
+        dka[t] = Mma<CT>::mma(lds_tq_frag<CT, kDH>(qt_s[buf], 32 * t + l32, h, s), bfr, dka[t]);
     }
   };
 
@@ -446,7 +472,7 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
       else step(qt, buf, std::true_type{});
     }
     stash(buf ^ 1);
-    if (run && h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
+    if (run && store_suffix && h == 0 && key < P.T) sufk_col[static_cast<int64_t>(qt) * P.T] = sufk_in;
     sync_lds();
   };
   double_buffered<true>(0, nq - kb0, iter);
@@ -456,10 +482,10 @@ __global__ __launch_bounds__(kThreads, (bwd_occupancy<CT, D>())) void bwd_key(Bw
     float* dkrow = P.dkm + (slice * P.T + key) * D;
     const int64_t dvrow = (slice * P.T + key) * D;
 #pragma unroll
-    for (int t = 0; t < kDTiles<D>; ++t)
+    for (int t = 0; t < kDT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int d = 32 * t + acc_row(4 * j, h);
+        const int d = 32 * (t0 + t) + acc_row(4 * j, h);
         if (d < D) {
           *reinterpret_cast<floatx4*>(dkrow + d) =
               floatx4{dka[t][4 * j], dka[t][4 * j + 1], dka[t][4 * j + 2], dka[t][4 * j + 3]};
@@ -794,16 +820,20 @@ __global__ __launch_bounds__(64 * W, ((PARK && query_parks<CT, D>()) ? (W == 4 ?
 template <typename CT, int D, int BID = BID_SOFTMAX>
 __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) void bwd_dkcorr(BwdParams P) {
   using TL = Tiles<CT, D>;
+  constexpr int kSplit = key_split<CT, D>();          // head-dim split as in bwd_key
+  constexpr int kDH = D / kSplit;
+  constexpr int kDT = kDTiles<kDH>;
   constexpr int kNS = BID == BID_SOFTMAX ? 1 : 3;                // per-row statistics staged
   __shared__ __attribute__((aligned(16))) CT q_s[2][kTileQ * TL::kKStride];
-  __shared__ __attribute__((aligned(16))) CT qgt_s[2][D * TL::kTStride];
+  __shared__ __attribute__((aligned(16))) CT qgt_s[2][kDH * TL::kTStride];
   __shared__ __attribute__((aligned(16))) float st_s[2][kNS * kTileQ];   // lse (r0), (unused), r1
 
-  const WorkItem item = xcd_work_item(P.kgroups, P.n, false, false);   // slice by slice: measured faster here
+  const WorkItem item = xcd_work_item(P.kgroups * kSplit, P.n, false, false);   // slice by slice: measured faster here
   if (!item.valid) return;
   const int64_t slice = item.slice;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
-  const int kb0 = item.idx * 4;
+  const int t0 = (item.idx % kSplit) * kDT;       // first 32-dim tile of the workgroup's head dims
+  const int kb0 = (item.idx / kSplit) * 4;
   const int kb = kb0 + wave;
   const int64_t key = static_cast<int64_t>(kb) * kTileK + l32;
   const int nq = static_cast<int>((P.T + kTileQ - 1) / kTileQ);
@@ -816,18 +846,19 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
   RowFrag<CT, D> kf;
   if (key < P.T) load_row_frag<CT, D>(kf, static_cast<const CT*>(P.k) + (slice * P.T + key) * D + h * (D / 2));
   else zero_row_frag<CT, D>(kf);
-  floatx16 dkc[kDTiles<D>];
+  floatx16 dkc[kDT];
 #pragma unroll
-  for (int t = 0; t < kDTiles<D>; ++t) dkc[t] = floatx16{};
+  for (int t = 0; t < kDT; ++t) dkc[t] = floatx16{};
 
   KTileLoader<CT, D, true> ql;            // row tile in query-split slot order
-  TTileLoader<CT, D> qtl;
+  TTileLoader<CT, kDH, kLoadBuffer, D> qtl;   // the workgroup's head dims of (ghat q)^T
+  const int64_t t_off = static_cast<int64_t>(t0) * 32 * kTileK;
   RowStatsLoader<kNS, false> sl;
   if constexpr (!bid_log2<BID>()) sl.pad0 = 0.f;
   auto fetch = [&](int qt) {
     const int64_t row0 = static_cast<int64_t>(qt) * kTileQ;
     ql.load(qs, row0, P.T);
-    qtl.load(qgts, row0);
+    qtl.load(qgts + t_off, row0);
     sl.load(lse, lse, BID == BID_SOFTMAX ? lse : P.rb1 + slice * P.T, row0, P.T);
   };
   auto stash = [&](int buf) {
@@ -839,9 +870,14 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
 
   auto step = [&](int buf, auto diag_tag) {
     constexpr bool DIAG = decltype(diag_tag)::value;
-    RowFrag<CT, D> qf;
-    lds_row_frag<CT, D>(qf, q_s[buf], l32, h);      // slot l32 holds row qsig(l32)
-    const floatx16 sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    floatx16 sacc;                               // slot l32 holds row qsig(l32)
+    if constexpr (kSplit > 1) {
+      sacc = mma_rows_src<CT, D>(q_s[buf] + l32 * TL::kKStride + h * (D / 2), kf, floatx16{});
+    } else {
+      RowFrag<CT, D> qf;
+      lds_row_frag<CT, D>(qf, q_s[buf], l32, h);
+      sacc = mma_rows<CT, D>(qf, kf, floatx16{});
+    }
     float lz[16], p[16];
     lds_read16(st_s[buf] + 16 * h, lz);
     if constexpr (BID == BID_SOFTMAX) {
@@ -867,8 +903,8 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
     for (int s = 0; s < kSteps; ++s) {
       const auto bfr = acc_frag<CT>(p, s);
 #pragma unroll
-      for (int t = 0; t < kDTiles<D>; ++t)
-        dkc[t] = Mma<CT>::mma(lds_tq_frag<CT, D>(qgt_s[buf], 32 * t + l32, h, s), bfr, dkc[t]);
+      for (int t = 0; t < kDT; ++t)
+        dkc[t] = Mma<CT>::mma(lds_tq_frag<CT, kDH>(qgt_s[buf], 32 * t + l32, h, s), bfr, dkc[t]);
     }
   };
 
@@ -894,19 +930,19 @@ __global__ __launch_bounds__(kThreads, (sizeof(CT) == 2 && D <= 64) ? 3 : 2) voi
     // every dk_main load first (the dk stores could alias them for all the
     // compiler knows), four consecutive head dims per load and store
     const int64_t base = (slice * P.T + key) * D;
-    floatx4 dm[kDTiles<D>][4];
+    floatx4 dm[kDT][4];
 #pragma unroll
-    for (int t = 0; t < kDTiles<D>; ++t)
+    for (int t = 0; t < kDT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int d = 32 * t + acc_row(4 * j, h);
+        const int d = 32 * (t0 + t) + acc_row(4 * j, h);
         dm[t][j] = d < D ? *reinterpret_cast<const floatx4*>(P.dkm + base + d) : floatx4{};
       }
 #pragma unroll
-    for (int t = 0; t < kDTiles<D>; ++t)
+    for (int t = 0; t < kDT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int d = 32 * t + acc_row(4 * j, h);
+        const int d = 32 * (t0 + t) + acc_row(4 * j, h);
         if (d < D) {
           floatx4 v;
 #pragma unroll
@@ -1564,14 +1600,15 @@ int launch_backward(const BackwardArgs& a) {
                                                                              a.dq, a.grad_dtype, P.scale, qgt, s0)));
       });
       P.kgroups = (nkt + 3) / 4;
-      const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
+      const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * key_split<CT, D>() * a.n)));
       DIL_TIMED("bwd_dkcorr", st, (bwd_dkcorr<CT, D, BID><<<gkey, kThreads, 0, st>>>(P)));
       return static_cast<int>(hipGetLastError());
     }
   }
   P.kgroups = (nkt + 3) / 4;
-  const dim3 gkey(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * a.n)));
-  DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkey, kThreads, 0, st>>>(P)));
+  // bwd_key and bwd_dkcorr: key groups x head-dim parts x slices
+  const dim3 gkeys(static_cast<unsigned>(xcd_grid(static_cast<int64_t>(P.kgroups) * key_split<CT, D>() * a.n)));
+  DIL_TIMED("bwd_key", st, (bwd_key<CT, D, BID, SHARE><<<gkeys, kThreads, 0, st>>>(P)));
   constexpr bool kParked = query_parks<CT, D>() && is_production<BID, SHARE>();
   constexpr int kQW = kParked ? query_waves<CT, D>() : 4;     // row tiles (waves) per workgroup
   {
@@ -1586,7 +1623,7 @@ int launch_backward(const BackwardArgs& a) {
               prep_ghat_q<CT, D><<<dim3(static_cast<unsigned>(t_pad / 32), ns), kThreads, 0, st>>>(
                   qt, P.ghat, a.T, t_pad, qgt, s0));
   });
-  DIL_TIMED("bwd_dkcorr", st, (bwd_dkcorr<CT, D, BID><<<gkey, kThreads, 0, st>>>(P)));
+  DIL_TIMED("bwd_dkcorr", st, (bwd_dkcorr<CT, D, BID><<<gkeys, kThreads, 0, st>>>(P)));
   return static_cast<int>(hipGetLastError());
 }
 

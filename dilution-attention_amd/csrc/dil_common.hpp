@@ -270,6 +270,17 @@ __device__ __forceinline__ floatx16 mma_rows(const RowFrag<CT, D>& a, const RowF
   return acc;
 }
 
+// The same with A's row segment read from memory (an LDS row tile) one
+// instruction's fragment at a time, so that a wide A never sits in registers
+// whole (head_dim 256; 8-element fragment types).
+template <typename CT, int D>
+__device__ __forceinline__ floatx16 mma_rows_src(const CT* a_src, const RowFrag<CT, D>& b, floatx16 acc) {
+  static_assert(kWideFrag<CT>, "one 8-element fragment per instruction");
+#pragma unroll
+  for (int s = 0; s < RowFrag<CT, D>::kSteps; ++s) acc = Mma<CT>::mma(frag8_at<CT>(a_src + 8 * s), b.f[s], acc);
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // wave-level helpers
 

@@ -375,7 +375,9 @@ struct KTileLoader {
 // Copy one transposed tile (rows d in [0, D), columns [key0, key0 + 32), key0
 // a multiple of 32) of a tile-major slice into registers: 32 * D contiguous
 // elements.
-template <typename CT, int D, int MODE = kLoadBuffer>
+// DSTRIDE: the head dims of the tile-major copy, when the loader takes only
+// D of them (base then points at the first taken row of the first tile).
+template <typename CT, int D, int MODE = kLoadBuffer, int DSTRIDE = D>
 struct TTileLoader {
   using T = Tiles<CT, D>;
   using V = typename Vec16<CT>::type;
@@ -383,7 +385,7 @@ struct TTileLoader {
   static constexpr int kPerRow = kTileK / T::kChunk;
   V r[kPer];
   __device__ void load(const CT* base, int64_t key0) {
-    const CT* tile = base + key0 * D;               // (key0 / 32) * D * 32: the tile's first element
+    const CT* tile = base + key0 * DSTRIDE;         // (key0 / 32) * DSTRIDE * 32: the tile's first element
     if constexpr (MODE == kLoadBuffer) {
       const auto rs = make_rsrc(tile, kTileK * D * static_cast<int64_t>(sizeof(CT)));
 #pragma unroll
