@@ -3,7 +3,7 @@
 // Conventions used by every kernel in this library:
 //   * Tensors on the path are row-major (rows, D) per (batch*head) slice with
 //     64-bit slice strides passed explicitly.  D is a template parameter in
-//     {16, 32, 64, 128}.
+//     {16, 32, 64, 128}, and 256 for bf16 operands and the decode step.
 //   * Matrix products use the 32x32 MFMA family: bf16 operands
 //     (v_mfma_f32_32x32x16_bf16), fp32 operands (v_mfma_f32_32x32x2_f32), or
 //     split operands (fp32 values as bf16 hi + lo pairs, three bf16 MFMAs per
