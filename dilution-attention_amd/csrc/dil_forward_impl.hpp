@@ -1016,8 +1016,8 @@ __global__ __launch_bounds__(kThreads) void fwd_out_reduce(const __bf16* __restr
 // starts), one slice's partials (~0.5 byte per causal score element) within
 // the budget.  The workspace holds the partials of as many slices as the
 // budget allows, and the pass and its reduction run over the slices in
-// batches of that many (one batch up to 2^23 tokens of T^2 work per slice
-// pair: every training and prefill shape of the benchmark).  512-key groups
+// batches of that many (a single batch at every training and prefill shape of
+// the benchmark: one slice's partials are 35 MB at T = 16384).  512-key groups
 // (16 waves); DILUTION_FORWARD_KEY_PASS=0 turns it off (read once by each call
 // and by each size query: ForwardArgs::key_pass).
 constexpr int64_t kKeyoutBudgetBytes = int64_t{24} << 30;
