@@ -365,3 +365,31 @@ def test_head_dim_support_and_rejections_before_any_launch():
     assert lib.dil_forward_variant(*f[:3], 1, 8, 256, 1, 2, 1, 1, 1.0, *f[3:9], None, f[9], big,
                                    None) == -1
     assert lib.dil_decode_step_noalloc(*f[:5], 1, 8, 4, 512, 1, 1, None) == -1
+
+
+def test_integration_loader_re_exports_the_module(monkeypatch):
+    """The Option-A loader that INTEGRATION.md gives a maintainer (the body of
+    the reference's src/dilution/kernels.py) runs as written: with
+    DILUTION_AMD_ROOT pointing at this package it re-exports the operator's
+    functions, the routing predicate and the test gate, and loads nothing
+    from the reference."""
+    import sys
+
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    loader = next(b for b in blocks if "DILUTION_AMD_ROOT" in b)
+    monkeypatch.setenv("DILUTION_AMD_ROOT", os.path.join(ROOT, "dilution-attention_amd"))
+    ns = {"__name__": "reference_kernels_stand_in"}
+    try:
+        exec(compile(loader, "INTEGRATION.md", "exec"), ns)
+        from dilution import kernels
+
+        for name in ("dilution_attention_reference", "dilution_attention_forward", "dilution_attention",
+                     "dilution_decode_step", "dilution_prefill_chunk", "head_dim_supported",
+                     "_DilutionAttentionFn", "KEY_FORWARD_MIN_SEQ"):
+            assert getattr(ns[name], "__name__", name) == getattr(getattr(kernels, name), "__name__", name), name
+        assert ns["HAS_TRITON"] == kernels.HAS_HIP
+        assert ns["head_dim_supported"](256, "bf16") and not ns["head_dim_supported"](256, "tf32")
+    finally:
+        for mod in [m for m in sys.modules if m == "dilution_amd" or m.startswith("dilution_amd.")]:
+            del sys.modules[mod]
